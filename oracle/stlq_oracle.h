@@ -1,0 +1,99 @@
+/*
+ * CPU oracle for the STLQ basic-encode path — TEST INFRASTRUCTURE ONLY.
+ *
+ * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load this
+ * library, and only as the checker (or as the timed CPU baseline). The product path in
+ * stlq_amd/ never links or calls it.
+ *
+ * Every function restates a reference routine (file:line relative to the ighxiy/STLQ tree).
+ * Matrices follow the reference's column-major ColMajorMatrix convention
+ * (include/stlq/common/types.h:35-51): element (row, col) lives at data[col*rows + row].
+ *   X      d x n   (vector i = X + i*d)
+ *   C_all  d x H   (codeword f = C_all + f*d)
+ *   G      H x H   (G(row, col) = G[col*H + row])
+ *   xC     H x n   (xC + i*H holds <x_i, c_f> for all flat codes f)
+ *   codes  m x n   uint8 (codes + i*m)
+ *   a      m x n   float
+ */
+#pragma once
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* encoder_precomp.inc:1-53 (C_all concat, invnorm, G = C_all^T C_all). */
+int orc_build_precomp(int d, int m, const int* h_vec, const float* C_all,
+                      float* G, float* invnorm, int nthreads);
+
+/* cost_utils.cpp:88-110 (||x||^2, fixed sequential order). */
+void orc_xnorm2(const float* X, int d, int64_t n, float* out, int nthreads);
+
+/* blas.cpp:33-54 call site encoder_encode_base.inc:33-37 (xC = C_all^T X).
+ * mode 0: sequential mul+add (no FMA), r ascending.
+ * mode 1: fused k-ordered accumulation s = fma(c[r], x[r], s), r ascending — the order of the
+ *         device's fp32 MFMA GEMM. */
+void orc_gemm_xc(const float* C_all, int d, int H, const float* X, int64_t n,
+                 float* xC, int mode, int nthreads);
+
+/* beam_search.cpp:196-422 BeamSearchPrefixLS. best_err may be NULL. */
+int orc_beam_search(const float* nx2, const float* xC, const float* G, int H, int m,
+                    const int* h_vec, int H_beam, int64_t n, uint8_t* codes,
+                    float* best_err, int nthreads);
+
+/* least_squares.cpp:406-565 SolveLeastSquaresAll. Returns the failure count. */
+int64_t orc_solve_ls_all(const float* xC, const float* G, int H, int m, const int* h_vec,
+                         const uint8_t* codes, int64_t n, float* a, int nthreads);
+
+/* cost_utils.cpp:112-158 SampleCost / ComputeCosts. */
+void orc_compute_costs(const float* xC, const float* G, int H, int m, const int* h_vec,
+                       const uint8_t* codes, const float* a, const float* nx2, int64_t n,
+                       float* cost, int nthreads);
+
+/* icm.cpp:89-344 RunIcm + icm.cpp:872-899 DynamicIcmWithIlsImpl with ils_iters = 0:
+ * LS refit, costs, then icm_iters sweeps. codes/a/cost are updated in place
+ * (a and cost are outputs; codes is input/output). */
+int64_t orc_icm(const float* xC, const float* G, const float* invnorm, int H, int m,
+                const int* h_vec, const float* nx2, int64_t n, int icm_iters, int use_abs,
+                uint32_t seed, uint8_t* codes, float* a, float* cost, int nthreads);
+
+/* The layer order RunIcm uses on iteration `it` (std::shuffle with std::mt19937(seed),
+ * icm.cpp:137/242/890). order_out has m * icm_iters entries. */
+void orc_icm_orders(int m, int icm_iters, uint32_t seed, int* order_out);
+
+/* linkage_tools.cpp:170-221 MeanMseFromPrecomp (double accumulation, per-vector). */
+void orc_mse_from_precomp(const float* X, int d, const float* xC, const float* G, int H,
+                          int m, const int* h_vec, const uint8_t* codes, const float* a,
+                          int64_t n, double* per_vec, int nthreads);
+
+/* Independent fp64 evaluator (not a reference routine): LS-refit the given codes in fp64
+ * and return ||x - sum_l a_l c_l||^2 per vector by explicit reconstruction. */
+void orc_mse_fp64_refit(const float* X, int d, const float* C_all, int H, int m,
+                        const int* h_vec, const uint8_t* codes, int64_t n, double* per_vec,
+                        int nthreads);
+
+/* precomp_large_root.cpp:27-157 BuildPrecompLargeRoot. norm0[h0], G_small (Hs x Hs),
+ * G0S (h0 x Hs, column-major: G0S(root, flat) = G0S[flat*h0 + root]). */
+int orc_build_precomp_large_root(int d, int h0, int Hs, const float* C0,
+                                 const float* C_small, float* norm0, float* G_small,
+                                 float* G0S, int nthreads);
+
+/* beam_search.cpp:579-726 BeamSearchPrefixLSLargeRoot, root scores from fused k-ordered
+ * dot products (the device GEMM's order) instead of GemmRaw; expansion via
+ * beam_search.cpp:728-992.
+ * h_vec has m entries (h_vec[0] = h0); xC_small is Hs x n.
+ * forced_root: NULL for the full large-root beam; otherwise a per-vector root id and the
+ * root layer contributes exactly one finite candidate (the forced root).
+ * root_mode: when forced_root is NULL and root_mode == 1, the nearest root by the
+ * root-layer LS error is forced (one finite slot). */
+int orc_beam_search_large_root(const float* X, int d, const float* nx2, const float* C0,
+                               const float* norm0, const float* xC_small,
+                               const float* G_small, const float* G0S, int h0, int Hs,
+                               int m, const int* h_vec, int H_beam, int64_t n,
+                               const uint32_t* forced_root, int root_mode,
+                               uint32_t* cluster_id, uint8_t* B_small, float* best_err,
+                               int nthreads);
+
+#ifdef __cplusplus
+}
+#endif

@@ -1,0 +1,1049 @@
+// C ABI of libstlq_mi355: context, device precomp, tiled encode orchestration, streaming.
+// The reference routine each entry point replaces is named in include/stlq_mi355.h.
+#include "stlq_mi355.h"
+#include "stlq_mi355_tools.h"
+#include "internal.hpp"
+
+#include <algorithm>
+#include <chrono>
+#include <cstdlib>
+#include <cstring>
+#include <numeric>
+#include <random>
+#include <string>
+#include <vector>
+
+using namespace stlq_mi355;
+
+namespace {
+
+thread_local std::string g_err;
+
+int Fail(int code, const std::string& msg) {
+    g_err = msg;
+    return code;
+}
+
+#define HIP_TRY(expr)                                                                         \
+    do {                                                                                      \
+        hipError_t e_ = (expr);                                                               \
+        if (e_ != hipSuccess)                                                                 \
+            return Fail(STLQ_MI355_ERR_HIP, std::string(#expr) + ": " + hipGetErrorString(e_)); \
+    } while (0)
+
+#define RC_TRY(expr)                   \
+    do {                               \
+        int rc_ = (expr);              \
+        if (rc_ != STLQ_MI355_OK) return rc_; \
+    } while (0)
+
+struct DevBuf {
+    void* p = nullptr;
+    size_t bytes = 0;
+    hipError_t Ensure(size_t want) {
+        if (want <= bytes && p) return hipSuccess;
+        if (p) {
+            hipError_t e = hipFree(p);
+            if (e != hipSuccess) return e;
+        }
+        p = nullptr;
+        bytes = 0;
+        if (want == 0) want = 256;
+        hipError_t e = hipMalloc(&p, want);
+        if (e == hipSuccess) bytes = want;
+        return e;
+    }
+    void Release() {
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        bytes = 0;
+    }
+    template <class T>
+    T* as() const {
+        return static_cast<T*>(p);
+    }
+};
+
+// One tile's event set; resolved lazily when timings are read.
+struct TileEvents {
+    hipEvent_t e[7] = {};  // start, xnorm, gemm, beam, ls, icm, end
+    hipEvent_t lay[kMaxM + 1] = {};  // before layer 0, after each beam layer
+    int layers = 0;
+    int64_t n = 0;
+    int gemm_launches = 0;
+    int beam_launches = 0;
+};
+
+int64_t EnvWorkspaceBytes() {
+    const char* s = std::getenv("STLQ_MI355_WORKSPACE_GB");
+    double gb = s ? std::atof(s) : 24.0;
+    if (!(gb > 0.0)) gb = 24.0;
+    return static_cast<int64_t>(gb * 1024.0 * 1024.0 * 1024.0);
+}
+
+}  // namespace
+
+struct stlq_mi355_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    hipStream_t copy_stream = nullptr;
+
+    // Full precomp (BuildPrecomp).
+    bool has_pre = false;
+    int d = 0, m = 0, H = 0;
+    int h_vec[kMaxM] = {}, off[kMaxM] = {};
+    DevBuf C_all, G_rm, G_cm, gdiag, invnorm;
+    bool g_shared = true;  // G_cm aliases G_rm (symmetric G built on the device)
+
+    // Large-root precomp (BuildPrecompLargeRoot).
+    bool has_lr = false;
+    int lr_d = 0, lr_m = 0, h0 = 0, Hs = 0;
+    int lr_h[kMaxM] = {}, soff[kMaxM] = {};
+    DevBuf C0, Cs, norm0, G_small, G0S, gdiag_small;
+
+    // Work buffers (grown on demand, reused across calls).
+    DevBuf X, nx2, xC, codes, a, cost, best, fails, active, changed, mse, gam0, roots, scores;
+    DevBuf st_err[2], st_code[2], st_coef[2], st_R[2], st_root[2], st_curH[2];
+
+    std::vector<TileEvents> tiles;
+    std::vector<hipEvent_t> event_pool;
+    size_t event_next = 0;
+
+    hipEvent_t NextEvent() {
+        if (event_next == event_pool.size()) {
+            hipEvent_t e = nullptr;
+            if (hipEventCreate(&e) != hipSuccess) return nullptr;
+            event_pool.push_back(e);
+        }
+        return event_pool[event_next++];
+    }
+    void ResetTimings() {
+        tiles.clear();
+        event_next = 0;
+    }
+};
+
+namespace {
+
+int CheckCtx(stlq_mi355_ctx* ctx) {
+    if (!ctx) return Fail(STLQ_MI355_ERR_INVALID, "null context");
+    HIP_TRY(hipSetDevice(ctx->device));
+    return STLQ_MI355_OK;
+}
+
+int CheckPre(stlq_mi355_ctx* ctx) {
+    RC_TRY(CheckCtx(ctx));
+    if (!ctx->has_pre) return Fail(STLQ_MI355_ERR_STATE, "codebooks not set (call stlq_mi355_set_codebooks)");
+    return STLQ_MI355_OK;
+}
+
+int CheckBeam(int Hb) {
+    if (Hb < 1 || Hb > kMaxBeam)
+        return Fail(STLQ_MI355_ERR_UNSUPPORTED, "H_beam must be in [1, 64], got " + std::to_string(Hb));
+    return STLQ_MI355_OK;
+}
+
+int ValidateLayers(int d, int m, const int* h_vec, int first_max) {
+    if (d <= 0) return Fail(STLQ_MI355_ERR_INVALID, "d must be positive");
+    if (m < 1 || m > kMaxM) return Fail(STLQ_MI355_ERR_UNSUPPORTED, "m must be in [1, 20]");
+    if (!h_vec) return Fail(STLQ_MI355_ERR_INVALID, "h_vec is null");
+    for (int l = 0; l < m; ++l) {
+        const int lim = (l == 0) ? first_max : kMaxK;
+        if (h_vec[l] < 1 || h_vec[l] > lim)
+            return Fail(STLQ_MI355_ERR_UNSUPPORTED,
+                        "codebook size of layer " + std::to_string(l) + " out of range: " + std::to_string(h_vec[l]));
+    }
+    return STLQ_MI355_OK;
+}
+
+// Per-vector device bytes of one encode tile.
+int64_t PerVectorBytes(int d, int m, int H, int Hb) {
+    const int64_t state = static_cast<int64_t>(Hb) *
+                          (4 + CodeStride(m) + 4 * m + 4 * TriSize(m) + 4);
+    return 4LL * d + 4 + 4LL * H + m + 4LL * m + 4 + 4 + 2 + 8 + 2 * (state + 4);
+}
+
+int64_t TileVectors(int64_t n, int d, int m, int H, int Hb) {
+    const int64_t per = PerVectorBytes(d, m, H, Hb);
+    int64_t t = EnvWorkspaceBytes() / std::max<int64_t>(per, 1);
+    t = std::max<int64_t>(t, 1024);
+    t = std::min<int64_t>(t, std::max<int64_t>(n, 1));
+    return t;
+}
+
+int EnsureState(stlq_mi355_ctx* c, int64_t n, int m, int Hb) {
+    const size_t slots = static_cast<size_t>(n) * Hb;
+    for (int b = 0; b < 2; ++b) {
+        HIP_TRY(c->st_err[b].Ensure(slots * 4));
+        HIP_TRY(c->st_code[b].Ensure(slots * CodeStride(m)));
+        HIP_TRY(c->st_coef[b].Ensure(slots * 4 * m));
+        HIP_TRY(c->st_R[b].Ensure(slots * 4 * TriSize(m)));
+        HIP_TRY(c->st_root[b].Ensure(slots * 4));
+        HIP_TRY(c->st_curH[b].Ensure(static_cast<size_t>(n) * 4));
+    }
+    return STLQ_MI355_OK;
+}
+
+BeamState StateOf(stlq_mi355_ctx* c, int b) {
+    BeamState s;
+    s.err = c->st_err[b].as<float>();
+    s.code = c->st_code[b].as<uint8_t>();
+    s.coef = c->st_coef[b].as<float>();
+    s.R = c->st_R[b].as<float>();
+    s.root = c->st_root[b].as<uint32_t>();
+    s.curH = c->st_curH[b].as<int>();
+    return s;
+}
+
+// Full-precomp beam over one tile: layer 0 then layers 1..m-1 (BeamSearchPrefixLS).
+int RunBeam(stlq_mi355_ctx* c, const float* dxC, int64_t ldx, const float* dnx2, int64_t n, int Hb,
+            uint8_t* dcodes, float* dbest, hipStream_t s, int* launches, TileEvents* te = nullptr) {
+    RC_TRY(EnsureState(c, n, c->m, Hb));
+    auto mark = [&](int k) -> hipError_t {
+        if (!te) return hipSuccess;
+        te->lay[k] = c->NextEvent();
+        te->layers = k;
+        return hipEventRecord(te->lay[k], s);
+    };
+    HIP_TRY(mark(0));
+    LayerArgs a;
+    a.gram.G = c->G_rm.as<float>();
+    a.gram.ld = c->H;
+    for (int l = 0; l < c->m; ++l) a.gram.off[l] = c->off[l];
+    a.xC = dxC;
+    a.ldx = ldx;
+    a.nx2 = dnx2;
+    a.gdiag = c->gdiag.as<float>();
+    a.n = n;
+    a.m = c->m;
+    a.Hb = Hb;
+    a.codes_out = dcodes;
+    a.best_err = dbest;
+    int cur = 0;
+    a.out = StateOf(c, cur);
+    a.K = c->h_vec[0];
+    a.offL = c->off[0];
+    a.is_last = (c->m == 1);
+    HIP_TRY(LaunchBeamLayer0(a, s));
+    HIP_TRY(mark(1));
+    int nl = 1;
+    for (int L = 1; L < c->m; ++L) {
+        a.in = StateOf(c, cur);
+        a.out = StateOf(c, cur ^ 1);
+        a.K = c->h_vec[L];
+        a.offL = c->off[L];
+        a.is_last = (L == c->m - 1);
+        HIP_TRY(LaunchBeamLayer(L, false, a, s));
+        HIP_TRY(mark(L + 1));
+        cur ^= 1;
+        ++nl;
+    }
+    if (launches) *launches += nl;
+    return STLQ_MI355_OK;
+}
+
+LsArgs MakeLs(stlq_mi355_ctx* c, const float* dxC, int64_t ldx, const uint8_t* dcodes, float* da, const float* dnx2,
+              float* dcost, int64_t n) {
+    LsArgs p;
+    p.xC = dxC;
+    p.ldx = ldx;
+    p.G_rm = c->G_rm.as<float>();
+    p.H = c->H;
+    p.m = c->m;
+    for (int l = 0; l < c->m; ++l) p.off[l] = c->off[l];
+    p.codes = dcodes;
+    p.a = da;
+    p.nx2 = dnx2;
+    p.cost = dcost;
+    p.fails = c->fails.as<int>();
+    p.n = n;
+    return p;
+}
+
+std::vector<int> IcmOrders(int m, int iters, uint32_t seed) {
+    // icm.cpp:119-122, :137/:242, :890: order = iota(m) shuffled in place once per iteration
+    // with one std::mt19937(seed) stream.
+    std::mt19937 rng(static_cast<std::mt19937::result_type>(seed));
+    std::vector<int> order(m), all;
+    std::iota(order.begin(), order.end(), 0);
+    for (int it = 0; it < iters; ++it) {
+        std::shuffle(order.begin(), order.end(), rng);
+        all.insert(all.end(), order.begin(), order.end());
+    }
+    return all;
+}
+
+// RunIcm (icm.cpp:89-344) on one tile: LS refit + costs, then icm_iters sweeps.
+int RunIcm(stlq_mi355_ctx* c, const float* dxC, int64_t ldx, const float* dnx2, int64_t n, int iters,
+           int use_abs, uint32_t seed, uint8_t* dcodes, float* da, float* dcost, hipStream_t s) {
+    LsArgs ls = MakeLs(c, dxC, ldx, dcodes, da, dnx2, dcost, n);
+    HIP_TRY(LaunchLsAll(ls, s));
+    HIP_TRY(LaunchCosts(ls, s));
+    if (iters <= 0) return STLQ_MI355_OK;
+    HIP_TRY(c->active.Ensure(static_cast<size_t>(n)));
+    HIP_TRY(c->changed.Ensure(static_cast<size_t>(n)));
+    HIP_TRY(LaunchFill8(c->active.as<uint8_t>(), 1, n, s));
+    const std::vector<int> orders = IcmOrders(c->m, iters, seed);
+    IcmArgs q;
+    q.ls = ls;
+    q.codes_rw = dcodes;
+    q.G_cm = c->G_cm.as<float>();
+    q.invnorm = c->invnorm.as<float>();
+    q.active = c->active.as<uint8_t>();
+    q.changed = c->changed.as<uint8_t>();
+    q.fails = c->fails.as<int>();
+    q.use_abs = use_abs ? 1 : 0;
+    for (int it = 0; it < iters; ++it) {
+        HIP_TRY(LaunchFill8(q.changed, 0, n, s));
+        for (int oi = 0; oi < c->m; ++oi) {
+            const int j = orders[static_cast<size_t>(it) * c->m + oi];
+            if (j == 0) continue;                 // icm.cpp:250: layer 0 frozen
+            if (c->h_vec[j] <= 1) continue;        // icm.cpp:255
+            q.j = j;
+            q.hj = c->h_vec[j];
+            HIP_TRY(LaunchIcmLayer(q, s));
+        }
+        HIP_TRY(LaunchIcmDeactivate(q.active, q.changed, n, s));
+    }
+    return STLQ_MI355_OK;
+}
+
+struct EncodeOut {
+    uint8_t* codes;  // device [n*m]
+    float* a;        // device [n*m] or null
+    float* cost;     // device [n] or null
+    float* best;     // device [n] or null
+};
+
+// One tile of EncodeBase on device-resident X.
+int EncodeTile(stlq_mi355_ctx* c, const float* dX, int64_t n, const stlq_mi355_encode_params& P,
+               const EncodeOut& o, hipStream_t s, bool record) {
+    const int Hb = std::max(1, P.H_beam);
+    HIP_TRY(c->nx2.Ensure(static_cast<size_t>(n) * 4));
+    HIP_TRY(c->xC.Ensure(static_cast<size_t>(n) * c->H * 4));
+    TileEvents te;
+    te.n = n;
+    auto rec = [&](int k) -> hipError_t {
+        if (!record) return hipSuccess;
+        te.e[k] = c->NextEvent();
+        return hipEventRecord(te.e[k], s);
+    };
+    HIP_TRY(rec(0));
+    HIP_TRY(LaunchXNorm2(dX, c->d, n, c->nx2.as<float>(), s));
+    HIP_TRY(rec(1));
+    HIP_TRY(LaunchGemmXc(dX, n, c->d, c->C_all.as<float>(), c->H, c->xC.as<float>(), c->H, s));
+    te.gemm_launches = 1;
+    HIP_TRY(rec(2));
+    RC_TRY(RunBeam(c, c->xC.as<float>(), c->H, c->nx2.as<float>(), n, Hb, o.codes, o.best, s, &te.beam_launches,
+                   record ? &te : nullptr));
+    HIP_TRY(rec(3));
+    const bool need_ls = P.want_coeffs || P.icm_iters > 0;
+    float* da = o.a;
+    float* dcost = o.cost;
+    if (need_ls) {
+        if (!da) {
+            HIP_TRY(c->a.Ensure(static_cast<size_t>(n) * c->m * 4));
+            da = c->a.as<float>();
+        }
+        if (!dcost) {
+            HIP_TRY(c->cost.Ensure(static_cast<size_t>(n) * 4));
+            dcost = c->cost.as<float>();
+        }
+        LsArgs ls = MakeLs(c, c->xC.as<float>(), c->H, o.codes, da, c->nx2.as<float>(), dcost, n);
+        HIP_TRY(LaunchLsAll(ls, s));
+        HIP_TRY(LaunchCosts(ls, s));
+    }
+    HIP_TRY(rec(4));
+    if (P.icm_iters > 0) {
+        RC_TRY(RunIcm(c, c->xC.as<float>(), c->H, c->nx2.as<float>(), n, P.icm_iters, P.use_abs, P.seed, o.codes,
+                      da, dcost, s));
+    }
+    HIP_TRY(rec(5));
+    HIP_TRY(rec(6));
+    if (record) c->tiles.push_back(te);
+    return STLQ_MI355_OK;
+}
+
+int CheckParams(const stlq_mi355_encode_params* p) {
+    if (!p) return Fail(STLQ_MI355_ERR_INVALID, "params is null");
+    if (p->ils_iters != 0) return Fail(STLQ_MI355_ERR_UNSUPPORTED, "ils_iters must be 0 (ILS is not part of this build)");
+    if (p->icm_iters < 0) return Fail(STLQ_MI355_ERR_INVALID, "icm_iters must be >= 0");
+    return CheckBeam(std::max(1, p->H_beam));
+}
+
+double Mean(const std::vector<float>& v) {
+    // MeanMseFromPrecomp accumulates in double and clamps each error at 0 (linkage_tools.cpp:170-221).
+    double s = 0.0;
+    for (float x : v) s += x < 0.0f ? 0.0 : static_cast<double>(x);
+    return v.empty() ? 0.0 : s / static_cast<double>(v.size());
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* stlq_mi355_last_error(void) { return g_err.c_str(); }
+
+const char* stlq_mi355_version(void) { return "stlq_mi355 1.0 gfx950"; }
+
+int stlq_mi355_ctx_create(int device, stlq_mi355_ctx** out) {
+    if (!out) return Fail(STLQ_MI355_ERR_INVALID, "out is null");
+    *out = nullptr;
+    int count = 0;
+    HIP_TRY(hipGetDeviceCount(&count));
+    if (device < 0 || device >= count) return Fail(STLQ_MI355_ERR_INVALID, "no HIP device " + std::to_string(device));
+    HIP_TRY(hipSetDevice(device));
+    auto* c = new stlq_mi355_ctx();
+    c->device = device;
+    if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess ||
+        hipStreamCreateWithFlags(&c->copy_stream, hipStreamNonBlocking) != hipSuccess) {
+        delete c;
+        return Fail(STLQ_MI355_ERR_HIP, "stream creation failed");
+    }
+    if (c->fails.Ensure(256) != hipSuccess) {
+        delete c;
+        return Fail(STLQ_MI355_ERR_HIP, "allocation failed");
+    }
+    *out = c;
+    return STLQ_MI355_OK;
+}
+
+int stlq_mi355_ctx_destroy(stlq_mi355_ctx* c) {
+    if (!c) return STLQ_MI355_OK;
+    (void)hipSetDevice(c->device);
+    (void)hipStreamSynchronize(c->stream);
+    (void)hipStreamSynchronize(c->copy_stream);
+    DevBuf* bufs[] = {&c->C_all, &c->G_rm, &c->G_cm, &c->gdiag, &c->invnorm, &c->C0, &c->Cs, &c->norm0,
+                      &c->G_small, &c->G0S, &c->gdiag_small, &c->X, &c->nx2, &c->xC, &c->codes, &c->a,
+                      &c->cost, &c->best, &c->fails, &c->active, &c->changed, &c->mse, &c->gam0, &c->roots,
+                      &c->scores};
+    if (c->g_shared) c->G_cm.p = nullptr;
+    for (DevBuf* b : bufs) b->Release();
+    for (int b = 0; b < 2; ++b) {
+        c->st_err[b].Release();
+        c->st_code[b].Release();
+        c->st_coef[b].Release();
+        c->st_R[b].Release();
+        c->st_root[b].Release();
+        c->st_curH[b].Release();
+    }
+    for (hipEvent_t e : c->event_pool) (void)hipEventDestroy(e);
+    (void)hipStreamDestroy(c->stream);
+    (void)hipStreamDestroy(c->copy_stream);
+    delete c;
+    return STLQ_MI355_OK;
+}
+
+static int SetPrecompCommon(stlq_mi355_ctx* c, int d, int m, const int* h_vec, const float* C_all) {
+    RC_TRY(CheckCtx(c));
+    RC_TRY(ValidateLayers(d, m, h_vec, kMaxK));
+    if (!C_all) return Fail(STLQ_MI355_ERR_INVALID, "C_all is null");
+    c->has_pre = false;
+    c->d = d;
+    c->m = m;
+    int o = 0;
+    for (int l = 0; l < m; ++l) {
+        c->h_vec[l] = h_vec[l];
+        c->off[l] = o;
+        o += h_vec[l];
+    }
+    c->H = o;
+    const size_t H = static_cast<size_t>(c->H);
+    HIP_TRY(c->C_all.Ensure(H * d * 4));
+    HIP_TRY(c->G_rm.Ensure(H * H * 4));
+    HIP_TRY(c->gdiag.Ensure(H * 4));
+    HIP_TRY(c->invnorm.Ensure(H * 4));
+    HIP_TRY(hipMemcpyAsync(c->C_all.p, C_all, H * d * 4, hipMemcpyHostToDevice, c->stream));
+    return STLQ_MI355_OK;
+}
+
+int stlq_mi355_set_codebooks(stlq_mi355_ctx* c, int d, int m, const int* h_vec, const float* C_all) {
+    RC_TRY(SetPrecompCommon(c, d, m, h_vec, C_all));
+    if (!c->g_shared) c->G_cm.Release();
+    c->g_shared = true;
+    c->G_cm.p = c->G_rm.p;
+    c->G_cm.bytes = 0;  // alias, never freed through G_cm
+    HIP_TRY(LaunchGram(c->C_all.as<float>(), d, c->H, c->G_rm.as<float>(), c->stream));
+    HIP_TRY(LaunchNorms(c->C_all.as<float>(), d, c->H, nullptr, c->invnorm.as<float>(), c->stream));
+    HIP_TRY(LaunchDiag(c->G_rm.as<float>(), c->H, c->gdiag.as<float>(), c->stream));
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    c->has_pre = true;
+    return STLQ_MI355_OK;
+}
+
+int stlq_mi355_set_precomp(stlq_mi355_ctx* c, int d, int m, const int* h_vec, const float* C_all,
+                           const float* G, const float* invnorm) {
+    if (!G || !invnorm) return Fail(STLQ_MI355_ERR_INVALID, "G and invnorm are required");
+    RC_TRY(SetPrecompCommon(c, d, m, h_vec, C_all));
+    const size_t H = static_cast<size_t>(c->H);
+    if (c->g_shared) c->G_cm.p = nullptr;
+    c->g_shared = false;
+    c->G_cm.bytes = 0;
+    HIP_TRY(c->G_cm.Ensure(H * H * 4));
+    HIP_TRY(hipMemcpyAsync(c->G_cm.p, G, H * H * 4, hipMemcpyHostToDevice, c->stream));
+    // Row-major copy of the reference element G(row, col) = G[col*H + row].
+    HIP_TRY(LaunchTranspose(c->G_cm.as<float>(), c->H, c->H, c->G_rm.as<float>(), c->stream));
+    HIP_TRY(hipMemcpyAsync(c->invnorm.p, invnorm, H * 4, hipMemcpyHostToDevice, c->stream));
+    HIP_TRY(LaunchDiag(c->G_rm.as<float>(), c->H, c->gdiag.as<float>(), c->stream));
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    c->has_pre = true;
+    return STLQ_MI355_OK;
+}
+
+int stlq_mi355_get_precomp(stlq_mi355_ctx* c, float* G, float* invnorm) {
+    RC_TRY(CheckPre(c));
+    const size_t H = static_cast<size_t>(c->H);
+    if (G) HIP_TRY(hipMemcpyAsync(G, c->G_cm.p, H * H * 4, hipMemcpyDeviceToHost, c->stream));
+    if (invnorm) HIP_TRY(hipMemcpyAsync(invnorm, c->invnorm.p, H * 4, hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    return STLQ_MI355_OK;
+}
+
+int stlq_mi355_xnorm2(stlq_mi355_ctx* c, const float* X, int64_t n, float* out) {
+    RC_TRY(CheckPre(c));
+    if (n < 0 || (n > 0 && (!X || !out))) return Fail(STLQ_MI355_ERR_INVALID, "bad arguments");
+    if (n == 0) return STLQ_MI355_OK;
+    HIP_TRY(c->X.Ensure(static_cast<size_t>(n) * c->d * 4));
+    HIP_TRY(c->nx2.Ensure(static_cast<size_t>(n) * 4));
+    HIP_TRY(hipMemcpyAsync(c->X.p, X, static_cast<size_t>(n) * c->d * 4, hipMemcpyHostToDevice, c->stream));
+    HIP_TRY(LaunchXNorm2(c->X.as<float>(), c->d, n, c->nx2.as<float>(), c->stream));
+    HIP_TRY(hipMemcpyAsync(out, c->nx2.p, static_cast<size_t>(n) * 4, hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    return STLQ_MI355_OK;
+}
+
+int stlq_mi355_gemm_xc(stlq_mi355_ctx* c, const float* X, int64_t n, float* xC) {
+    RC_TRY(CheckPre(c));
+    if (n < 0 || (n > 0 && (!X || !xC))) return Fail(STLQ_MI355_ERR_INVALID, "bad arguments");
+    if (n == 0) return STLQ_MI355_OK;
+    HIP_TRY(c->X.Ensure(static_cast<size_t>(n) * c->d * 4));
+    HIP_TRY(c->xC.Ensure(static_cast<size_t>(n) * c->H * 4));
+    HIP_TRY(hipMemcpyAsync(c->X.p, X, static_cast<size_t>(n) * c->d * 4, hipMemcpyHostToDevice, c->stream));
+    HIP_TRY(LaunchGemmXc(c->X.as<float>(), n, c->d, c->C_all.as<float>(), c->H, c->xC.as<float>(), c->H, c->stream));
+    HIP_TRY(hipMemcpyAsync(xC, c->xC.p, static_cast<size_t>(n) * c->H * 4, hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    return STLQ_MI355_OK;
+}
+
+int stlq_mi355_beam_search(stlq_mi355_ctx* c, const float* X, const float* nx2, const float* xC, int64_t n,
+                           int H_beam, uint8_t* codes, float* best_err) {
+    RC_TRY(CheckPre(c));
+    const int Hb = std::max(1, H_beam);
+    RC_TRY(CheckBeam(Hb));
+    if (n < 0 || (n > 0 && (!xC || !codes || (!X && !nx2)))) return Fail(STLQ_MI355_ERR_INVALID, "bad arguments");
+    if (n == 0) return STLQ_MI355_OK;
+    c->ResetTimings();
+    const int64_t tile = TileVectors(n, c->d, c->m, c->H, Hb);
+    HIP_TRY(c->xC.Ensure(static_cast<size_t>(tile) * c->H * 4));
+    HIP_TRY(c->nx2.Ensure(static_cast<size_t>(tile) * 4));
+    HIP_TRY(c->codes.Ensure(static_cast<size_t>(tile) * c->m));
+    HIP_TRY(c->best.Ensure(static_cast<size_t>(tile) * 4));
+    if (!nx2) HIP_TRY(c->X.Ensure(static_cast<size_t>(tile) * c->d * 4));
+    for (int64_t t0 = 0; t0 < n; t0 += tile) {
+        const int64_t nt = std::min(tile, n - t0);
+        HIP_TRY(hipMemcpyAsync(c->xC.p, xC + t0 * c->H, static_cast<size_t>(nt) * c->H * 4, hipMemcpyHostToDevice,
+                               c->stream));
+        if (nx2) {
+            HIP_TRY(hipMemcpyAsync(c->nx2.p, nx2 + t0, static_cast<size_t>(nt) * 4, hipMemcpyHostToDevice, c->stream));
+        } else {
+            HIP_TRY(hipMemcpyAsync(c->X.p, X + t0 * c->d, static_cast<size_t>(nt) * c->d * 4, hipMemcpyHostToDevice,
+                                   c->stream));
+            HIP_TRY(LaunchXNorm2(c->X.as<float>(), c->d, nt, c->nx2.as<float>(), c->stream));
+        }
+        TileEvents te;
+        te.n = nt;
+        te.e[0] = te.e[1] = te.e[2] = c->NextEvent();
+        HIP_TRY(hipEventRecord(te.e[0], c->stream));
+        RC_TRY(RunBeam(c, c->xC.as<float>(), c->H, c->nx2.as<float>(), nt, Hb, c->codes.as<uint8_t>(),
+                       c->best.as<float>(), c->stream, &te.beam_launches, &te));
+        te.e[3] = te.e[4] = te.e[5] = te.e[6] = c->NextEvent();
+        HIP_TRY(hipEventRecord(te.e[3], c->stream));
+        c->tiles.push_back(te);
+        HIP_TRY(hipMemcpyAsync(codes + t0 * c->m, c->codes.p, static_cast<size_t>(nt) * c->m, hipMemcpyDeviceToHost,
+                               c->stream));
+        if (best_err)
+            HIP_TRY(hipMemcpyAsync(best_err + t0, c->best.p, static_cast<size_t>(nt) * 4, hipMemcpyDeviceToHost,
+                                   c->stream));
+        HIP_TRY(hipStreamSynchronize(c->stream));
+    }
+    return STLQ_MI355_OK;
+}
+
+// Host-side check that caller-supplied codes index their layer's codebook (the kernels gather
+// G rows by code; an out-of-range code would read outside G).
+static int CheckCodes(const stlq_mi355_ctx* c, const uint8_t* codes, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) {
+        const uint8_t* ci = codes + i * c->m;
+        for (int l = 0; l < c->m; ++l) {
+            if (ci[l] >= c->h_vec[l])
+                return Fail(STLQ_MI355_ERR_INVALID, "code " + std::to_string(ci[l]) + " of vector " + std::to_string(i) +
+                                                        " exceeds layer " + std::to_string(l) + " size " +
+                                                        std::to_string(c->h_vec[l]));
+        }
+    }
+    return STLQ_MI355_OK;
+}
+
+static int LsCommon(stlq_mi355_ctx* c, const float* xC, const uint8_t* codes, const float* a_in, const float* nx2,
+                    int64_t n, float* a_out, float* cost_out, int64_t* fail_count) {
+    RC_TRY(CheckPre(c));
+    if (n < 0 || (n > 0 && (!xC || !codes))) return Fail(STLQ_MI355_ERR_INVALID, "bad arguments");
+    RC_TRY(CheckCodes(c, codes, n));
+    if (fail_count) *fail_count = 0;
+    if (n == 0) return STLQ_MI355_OK;
+    const size_t m = static_cast<size_t>(c->m);
+    HIP_TRY(c->xC.Ensure(static_cast<size_t>(n) * c->H * 4));
+    HIP_TRY(c->codes.Ensure(static_cast<size_t>(n) * m));
+    HIP_TRY(c->a.Ensure(static_cast<size_t>(n) * m * 4));
+    HIP_TRY(c->nx2.Ensure(static_cast<size_t>(n) * 4));
+    HIP_TRY(c->cost.Ensure(static_cast<size_t>(n) * 4));
+    HIP_TRY(hipMemcpyAsync(c->xC.p, xC, static_cast<size_t>(n) * c->H * 4, hipMemcpyHostToDevice, c->stream));
+    HIP_TRY(hipMemcpyAsync(c->codes.p, codes, static_cast<size_t>(n) * m, hipMemcpyHostToDevice, c->stream));
+    HIP_TRY(hipMemsetAsync(c->fails.p, 0, 4, c->stream));
+    LsArgs ls = MakeLs(c, c->xC.as<float>(), c->H, c->codes.as<uint8_t>(), c->a.as<float>(), c->nx2.as<float>(),
+                       c->cost.as<float>(), n);
+    if (a_out) {
+        HIP_TRY(LaunchLsAll(ls, c->stream));
+        HIP_TRY(hipMemcpyAsync(a_out, c->a.p, static_cast<size_t>(n) * m * 4, hipMemcpyDeviceToHost, c->stream));
+    }
+    if (cost_out) {
+        HIP_TRY(hipMemcpyAsync(c->a.p, a_in, static_cast<size_t>(n) * m * 4, hipMemcpyHostToDevice, c->stream));
+        HIP_TRY(hipMemcpyAsync(c->nx2.p, nx2, static_cast<size_t>(n) * 4, hipMemcpyHostToDevice, c->stream));
+        HIP_TRY(LaunchCosts(ls, c->stream));
+        HIP_TRY(hipMemcpyAsync(cost_out, c->cost.p, static_cast<size_t>(n) * 4, hipMemcpyDeviceToHost, c->stream));
+    }
+    int fails = 0;
+    HIP_TRY(hipMemcpyAsync(&fails, c->fails.p, 4, hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    if (fail_count) *fail_count = fails;
+    return STLQ_MI355_OK;
+}
+
+int stlq_mi355_solve_ls_all(stlq_mi355_ctx* c, const float* xC, const uint8_t* codes, int64_t n, float* a,
+                            int64_t* fail_count) {
+    if (n > 0 && !a) return Fail(STLQ_MI355_ERR_INVALID, "a is null");
+    return LsCommon(c, xC, codes, nullptr, nullptr, n, a, nullptr, fail_count);
+}
+
+int stlq_mi355_compute_costs(stlq_mi355_ctx* c, const float* xC, const uint8_t* codes, const float* a,
+                             const float* nx2, int64_t n, float* cost) {
+    if (n > 0 && (!a || !nx2 || !cost)) return Fail(STLQ_MI355_ERR_INVALID, "bad arguments");
+    return LsCommon(c, xC, codes, a, nx2, n, nullptr, cost, nullptr);
+}
+
+int stlq_mi355_icm(stlq_mi355_ctx* c, const float* X, const float* nx2, const float* xC, int64_t n, int icm_iters,
+                   int use_abs, uint32_t seed, uint8_t* codes, float* a, float* cost) {
+    RC_TRY(CheckPre(c));
+    if (n < 0 || (n > 0 && (!xC || !codes || !a || !cost || (!X && !nx2))))
+        return Fail(STLQ_MI355_ERR_INVALID, "bad arguments");
+    if (icm_iters < 0) return Fail(STLQ_MI355_ERR_INVALID, "icm_iters must be >= 0");
+    if (n == 0) return STLQ_MI355_OK;
+    RC_TRY(CheckCodes(c, codes, n));
+    c->ResetTimings();
+    const size_t m = static_cast<size_t>(c->m);
+    HIP_TRY(c->xC.Ensure(static_cast<size_t>(n) * c->H * 4));
+    HIP_TRY(c->codes.Ensure(static_cast<size_t>(n) * m));
+    HIP_TRY(c->a.Ensure(static_cast<size_t>(n) * m * 4));
+    HIP_TRY(c->nx2.Ensure(static_cast<size_t>(n) * 4));
+    HIP_TRY(c->cost.Ensure(static_cast<size_t>(n) * 4));
+    HIP_TRY(hipMemcpyAsync(c->xC.p, xC, static_cast<size_t>(n) * c->H * 4, hipMemcpyHostToDevice, c->stream));
+    HIP_TRY(hipMemcpyAsync(c->codes.p, codes, static_cast<size_t>(n) * m, hipMemcpyHostToDevice, c->stream));
+    if (nx2) {
+        HIP_TRY(hipMemcpyAsync(c->nx2.p, nx2, static_cast<size_t>(n) * 4, hipMemcpyHostToDevice, c->stream));
+    } else {
+        HIP_TRY(c->X.Ensure(static_cast<size_t>(n) * c->d * 4));
+        HIP_TRY(hipMemcpyAsync(c->X.p, X, static_cast<size_t>(n) * c->d * 4, hipMemcpyHostToDevice, c->stream));
+        HIP_TRY(LaunchXNorm2(c->X.as<float>(), c->d, n, c->nx2.as<float>(), c->stream));
+    }
+    HIP_TRY(hipMemsetAsync(c->fails.p, 0, 4, c->stream));
+    TileEvents te;
+    te.n = n;
+    te.e[0] = te.e[1] = te.e[2] = te.e[3] = te.e[4] = c->NextEvent();
+    HIP_TRY(hipEventRecord(te.e[0], c->stream));
+    RC_TRY(RunIcm(c, c->xC.as<float>(), c->H, c->nx2.as<float>(), n, icm_iters, use_abs, seed,
+                  c->codes.as<uint8_t>(), c->a.as<float>(), c->cost.as<float>(), c->stream));
+    te.e[5] = te.e[6] = c->NextEvent();
+    HIP_TRY(hipEventRecord(te.e[5], c->stream));
+    c->tiles.push_back(te);
+    HIP_TRY(hipMemcpyAsync(codes, c->codes.p, static_cast<size_t>(n) * m, hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(hipMemcpyAsync(a, c->a.p, static_cast<size_t>(n) * m * 4, hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(hipMemcpyAsync(cost, c->cost.p, static_cast<size_t>(n) * 4, hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    return STLQ_MI355_OK;
+}
+
+int stlq_mi355_encode(stlq_mi355_ctx* c, const float* X, int64_t n, const stlq_mi355_encode_params* params,
+                      uint8_t* codes, float* a, float* cost, double* beam_mse, double* final_mse) {
+    RC_TRY(CheckPre(c));
+    RC_TRY(CheckParams(params));
+    if (n < 0 || (n > 0 && (!X || !codes))) return Fail(STLQ_MI355_ERR_INVALID, "bad arguments");
+    if (n == 0) return STLQ_MI355_OK;
+    c->ResetTimings();
+    stlq_mi355_encode_params P = *params;
+    const bool want_mse = beam_mse || final_mse;
+    const bool need_ls = P.want_coeffs || P.icm_iters > 0 || want_mse;
+    const int Hb = std::max(1, P.H_beam);
+    const size_t m = static_cast<size_t>(c->m);
+    const int64_t tile = TileVectors(n, c->d, c->m, c->H, Hb);
+    HIP_TRY(c->X.Ensure(static_cast<size_t>(tile) * c->d * 4));
+    HIP_TRY(c->codes.Ensure(static_cast<size_t>(tile) * m));
+    HIP_TRY(c->a.Ensure(static_cast<size_t>(tile) * m * 4));
+    HIP_TRY(c->cost.Ensure(static_cast<size_t>(tile) * 4));
+    HIP_TRY(hipMemsetAsync(c->fails.p, 0, 4, c->stream));
+    std::vector<float> beam_cost, fin_cost;
+    double beam_sum = 0.0, fin_sum = 0.0;
+    for (int64_t t0 = 0; t0 < n; t0 += tile) {
+        const int64_t nt = std::min(tile, n - t0);
+        HIP_TRY(hipMemcpyAsync(c->X.p, X + t0 * c->d, static_cast<size_t>(nt) * c->d * 4, hipMemcpyHostToDevice,
+                               c->stream));
+        EncodeOut o{c->codes.as<uint8_t>(), c->a.as<float>(), c->cost.as<float>(), nullptr};
+        stlq_mi355_encode_params Pt = P;
+        Pt.want_coeffs = need_ls ? 1 : 0;
+        if (want_mse && P.icm_iters > 0) {
+            // Beam MSE before ICM: run the beam + LS alone first, then ICM on the same codes.
+            Pt.icm_iters = 0;
+            RC_TRY(EncodeTile(c, c->X.as<float>(), nt, Pt, o, c->stream, true));
+            beam_cost.resize(static_cast<size_t>(nt));
+            HIP_TRY(hipMemcpyAsync(beam_cost.data(), c->cost.p, static_cast<size_t>(nt) * 4, hipMemcpyDeviceToHost,
+                                   c->stream));
+            HIP_TRY(hipStreamSynchronize(c->stream));
+            beam_sum += Mean(beam_cost) * static_cast<double>(nt);
+            RC_TRY(RunIcm(c, c->xC.as<float>(), c->H, c->nx2.as<float>(), nt, P.icm_iters, P.use_abs, P.seed,
+                          o.codes, o.a, o.cost, c->stream));
+        } else {
+            RC_TRY(EncodeTile(c, c->X.as<float>(), nt, Pt, o, c->stream, true));
+        }
+        HIP_TRY(hipMemcpyAsync(codes + t0 * m, c->codes.p, static_cast<size_t>(nt) * m, hipMemcpyDeviceToHost,
+                               c->stream));
+        if (a && need_ls)
+            HIP_TRY(hipMemcpyAsync(a + t0 * m, c->a.p, static_cast<size_t>(nt) * m * 4, hipMemcpyDeviceToHost,
+                                   c->stream));
+        if (need_ls) {
+            fin_cost.resize(static_cast<size_t>(nt));
+            HIP_TRY(hipMemcpyAsync(fin_cost.data(), c->cost.p, static_cast<size_t>(nt) * 4, hipMemcpyDeviceToHost,
+                                   c->stream));
+        }
+        HIP_TRY(hipStreamSynchronize(c->stream));
+        if (need_ls) {
+            if (cost) std::memcpy(cost + t0, fin_cost.data(), static_cast<size_t>(nt) * 4);
+            fin_sum += Mean(fin_cost) * static_cast<double>(nt);
+            if (P.icm_iters == 0) beam_sum += Mean(fin_cost) * static_cast<double>(nt);
+        }
+    }
+    if (beam_mse) *beam_mse = beam_sum / static_cast<double>(n);
+    if (final_mse) *final_mse = fin_sum / static_cast<double>(n);
+    return STLQ_MI355_OK;
+}
+
+int stlq_mi355_encode_device(stlq_mi355_ctx* c, const float* dX, int64_t n, const stlq_mi355_encode_params* params,
+                             uint8_t* dcodes, float* da, float* dcost, void* stream) {
+    RC_TRY(CheckPre(c));
+    RC_TRY(CheckParams(params));
+    if (n < 0 || (n > 0 && (!dX || !dcodes))) return Fail(STLQ_MI355_ERR_INVALID, "bad arguments");
+    if (n == 0) return STLQ_MI355_OK;
+    c->ResetTimings();
+    hipStream_t s = stream ? static_cast<hipStream_t>(stream) : c->stream;
+    const int Hb = std::max(1, params->H_beam);
+    const int64_t tile = TileVectors(n, c->d, c->m, c->H, Hb);
+    const size_t m = static_cast<size_t>(c->m);
+    HIP_TRY(hipMemsetAsync(c->fails.p, 0, 4, s));
+    for (int64_t t0 = 0; t0 < n; t0 += tile) {
+        const int64_t nt = std::min(tile, n - t0);
+        EncodeOut o{dcodes + t0 * m, da ? da + t0 * m : nullptr, dcost ? dcost + t0 : nullptr, nullptr};
+        RC_TRY(EncodeTile(c, dX + t0 * c->d, nt, *params, o, s, true));
+    }
+    return STLQ_MI355_OK;
+}
+
+int stlq_mi355_last_timings(stlq_mi355_ctx* c, stlq_mi355_timings* out) {
+    RC_TRY(CheckCtx(c));
+    if (!out) return Fail(STLQ_MI355_ERR_INVALID, "out is null");
+    std::memset(out, 0, sizeof(*out));
+    for (const TileEvents& te : c->tiles) {
+        if (!te.e[0] || !te.e[6]) continue;
+        HIP_TRY(hipEventSynchronize(te.e[6]));
+        float ms[6] = {};
+        for (int k = 0; k < 6; ++k) {
+            if (te.e[k] && te.e[k + 1] && te.e[k] != te.e[k + 1]) HIP_TRY(hipEventElapsedTime(&ms[k], te.e[k], te.e[k + 1]));
+        }
+        float tot = 0.0f;
+        HIP_TRY(hipEventElapsedTime(&tot, te.e[0], te.e[6]));
+        out->xnorm_ms += ms[0];
+        out->gemm_ms += ms[1];
+        out->beam_ms += ms[2];
+        out->ls_ms += ms[3];
+        out->icm_ms += ms[4];
+        out->total_ms += tot;
+        out->n += te.n;
+        out->gemm_launches += te.gemm_launches;
+        out->beam_launches += te.beam_launches;
+        for (int l = 0; l < te.layers && l < kMaxM; ++l) {
+            float lm = 0.0f;
+            HIP_TRY(hipEventElapsedTime(&lm, te.lay[l], te.lay[l + 1]));
+            out->layer_ms[l] += lm;
+        }
+    }
+    return STLQ_MI355_OK;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Streaming encode: pinned host chunks -> two device buffers on the copy stream, encode on the
+// context stream, pinned outputs handed to the sink in order.
+int stlq_mi355_encode_stream(stlq_mi355_ctx* c, int64_t n_total, int64_t chunk, const stlq_mi355_encode_params* params,
+                             stlq_mi355_fill_fn fill, stlq_mi355_sink_fn sink, void* user,
+                             stlq_mi355_stream_stats* stats) {
+    RC_TRY(CheckPre(c));
+    RC_TRY(CheckParams(params));
+    if (n_total < 0 || chunk <= 0 || !fill || !sink) return Fail(STLQ_MI355_ERR_INVALID, "bad arguments");
+    if (stats) std::memset(stats, 0, sizeof(*stats));
+    if (n_total == 0) return STLQ_MI355_OK;
+    c->ResetTimings();
+    const auto t_begin = std::chrono::steady_clock::now();
+    const size_t m = static_cast<size_t>(c->m);
+    const size_t d = static_cast<size_t>(c->d);
+    chunk = std::min(chunk, n_total);
+    const bool want = params->want_coeffs || params->icm_iters > 0;
+    struct Slot {
+        float* hX = nullptr;
+        uint8_t* hcodes = nullptr;
+        float* ha = nullptr;
+        float* hcost = nullptr;
+        DevBuf dX, dcodes, da, dcost;
+        hipEvent_t copied = nullptr, done = nullptr, c0 = nullptr, c1 = nullptr, k0 = nullptr;
+        int64_t first = 0, count = 0;
+        bool busy = false;
+    } slot[2];
+    int rc = STLQ_MI355_OK;
+    auto cleanup = [&]() {
+        (void)hipStreamSynchronize(c->copy_stream);
+        (void)hipStreamSynchronize(c->stream);
+        for (Slot& s : slot) {
+            if (s.hX) (void)hipHostFree(s.hX);
+            if (s.hcodes) (void)hipHostFree(s.hcodes);
+            if (s.ha) (void)hipHostFree(s.ha);
+            if (s.hcost) (void)hipHostFree(s.hcost);
+            s.dX.Release();
+            s.dcodes.Release();
+            s.da.Release();
+            s.dcost.Release();
+            for (hipEvent_t e : {s.copied, s.done, s.c0, s.c1, s.k0})
+                if (e) (void)hipEventDestroy(e);
+        }
+    };
+    auto hip_ok = [&](hipError_t e, const char* what) {
+        if (e == hipSuccess) return true;
+        rc = Fail(STLQ_MI355_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+        return false;
+    };
+    for (Slot& s : slot) {
+        if (!hip_ok(hipHostMalloc(reinterpret_cast<void**>(&s.hX), chunk * d * 4, hipHostMallocDefault), "hipHostMalloc") ||
+            !hip_ok(hipHostMalloc(reinterpret_cast<void**>(&s.hcodes), chunk * m, hipHostMallocDefault), "hipHostMalloc") ||
+            !hip_ok(hipHostMalloc(reinterpret_cast<void**>(&s.ha), want ? chunk * m * 4 : 4, hipHostMallocDefault), "hipHostMalloc") ||
+            !hip_ok(hipHostMalloc(reinterpret_cast<void**>(&s.hcost), want ? chunk * 4 : 4, hipHostMallocDefault), "hipHostMalloc") ||
+            !hip_ok(s.dX.Ensure(chunk * d * 4), "hipMalloc") || !hip_ok(s.dcodes.Ensure(chunk * m), "hipMalloc") ||
+            !hip_ok(s.da.Ensure(want ? chunk * m * 4 : 4), "hipMalloc") ||
+            !hip_ok(s.dcost.Ensure(want ? chunk * 4 : 4), "hipMalloc") ||
+            !hip_ok(hipEventCreate(&s.copied), "hipEventCreate") || !hip_ok(hipEventCreate(&s.done), "hipEventCreate") ||
+            !hip_ok(hipEventCreate(&s.c0), "hipEventCreate") || !hip_ok(hipEventCreate(&s.c1), "hipEventCreate") ||
+            !hip_ok(hipEventCreate(&s.k0), "hipEventCreate")) {
+            cleanup();
+            return rc;
+        }
+    }
+    double fill_ms = 0.0, h2d_ms = 0.0, comp_ms = 0.0, h2d_bytes = 0.0;
+    int64_t nchunks = 0;
+    auto drain = [&](Slot& s) -> bool {
+        if (!s.busy) return true;
+        if (!hip_ok(hipEventSynchronize(s.done), "hipEventSynchronize")) return false;
+        float ms = 0.0f;
+        if (hip_ok(hipEventElapsedTime(&ms, s.c0, s.c1), "hipEventElapsedTime")) h2d_ms += ms;
+        if (hip_ok(hipEventElapsedTime(&ms, s.k0, s.done), "hipEventElapsedTime")) comp_ms += ms;
+        s.busy = false;
+        if (sink(user, s.first, s.count, s.hcodes, want ? s.ha : nullptr, want ? s.hcost : nullptr) != 0) {
+            rc = Fail(STLQ_MI355_ERR_CALLBACK, "sink callback failed");
+            return false;
+        }
+        return true;
+    };
+    int64_t ci = 0;
+    for (int64_t first = 0; first < n_total; first += chunk, ++ci) {
+        Slot& s = slot[ci & 1];
+        // Reuse of this slot's pinned and device buffers waits for its previous chunk.
+        if (!drain(s)) break;
+        s.first = first;
+        s.count = std::min(chunk, n_total - first);
+        const auto f0 = std::chrono::steady_clock::now();
+        if (fill(user, s.first, s.count, s.hX) != 0) {
+            rc = Fail(STLQ_MI355_ERR_CALLBACK, "fill callback failed");
+            break;
+        }
+        fill_ms += std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - f0).count();
+        const size_t xb = static_cast<size_t>(s.count) * d * 4;
+        if (!hip_ok(hipEventRecord(s.c0, c->copy_stream), "hipEventRecord") ||
+            !hip_ok(hipMemcpyAsync(s.dX.p, s.hX, xb, hipMemcpyHostToDevice, c->copy_stream), "hipMemcpyAsync") ||
+            !hip_ok(hipEventRecord(s.c1, c->copy_stream), "hipEventRecord") ||
+            !hip_ok(hipEventRecord(s.copied, c->copy_stream), "hipEventRecord") ||
+            !hip_ok(hipStreamWaitEvent(c->stream, s.copied, 0), "hipStreamWaitEvent") ||
+            !hip_ok(hipEventRecord(s.k0, c->stream), "hipEventRecord"))
+            break;
+        h2d_bytes += static_cast<double>(xb);
+        EncodeOut o{s.dcodes.as<uint8_t>(), want ? s.da.as<float>() : nullptr, want ? s.dcost.as<float>() : nullptr,
+                    nullptr};
+        rc = EncodeTile(c, s.dX.as<float>(), s.count, *params, o, c->stream, false);
+        if (rc != STLQ_MI355_OK) break;
+        if (!hip_ok(hipMemcpyAsync(s.hcodes, s.dcodes.p, static_cast<size_t>(s.count) * m, hipMemcpyDeviceToHost,
+                                   c->stream), "hipMemcpyAsync"))
+            break;
+        if (want && (!hip_ok(hipMemcpyAsync(s.ha, s.da.p, static_cast<size_t>(s.count) * m * 4, hipMemcpyDeviceToHost,
+                                            c->stream), "hipMemcpyAsync") ||
+                     !hip_ok(hipMemcpyAsync(s.hcost, s.dcost.p, static_cast<size_t>(s.count) * 4,
+                                            hipMemcpyDeviceToHost, c->stream), "hipMemcpyAsync")))
+            break;
+        if (!hip_ok(hipEventRecord(s.done, c->stream), "hipEventRecord")) break;
+        s.busy = true;
+        ++nchunks;
+        // Hand the previous chunk to the sink while this one copies and encodes.
+        Slot& prev = slot[(ci + 1) & 1];
+        if (!drain(prev)) break;
+    }
+    if (rc == STLQ_MI355_OK) {
+        for (int k = 0; k < 2 && rc == STLQ_MI355_OK; ++k) {
+            // drain in chunk order: the older busy slot first
+            Slot* older = nullptr;
+            for (Slot& s : slot)
+                if (s.busy && (!older || s.first < older->first)) older = &s;
+            if (older && !drain(*older)) break;
+        }
+    }
+    cleanup();
+    if (stats) {
+        stats->wall_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t_begin).count();
+        stats->h2d_ms = h2d_ms;
+        stats->compute_ms = comp_ms;
+        stats->fill_ms = fill_ms;
+        stats->h2d_bytes = h2d_bytes;
+        stats->chunks = nchunks;
+    }
+    return rc;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Large root.
+int stlq_mi355_set_large_root(stlq_mi355_ctx* c, int d, int m, const int* h_vec, const float* C0,
+                              const float* C_small) {
+    RC_TRY(CheckCtx(c));
+    RC_TRY(ValidateLayers(d, m, h_vec, 1 << 30));
+    if (!C0 || (m > 1 && !C_small)) return Fail(STLQ_MI355_ERR_INVALID, "null codebooks");
+    c->has_lr = false;
+    c->lr_d = d;
+    c->lr_m = m;
+    c->h0 = h_vec[0];
+    int o = 0;
+    for (int l = 0; l < m; ++l) c->lr_h[l] = h_vec[l];
+    c->soff[0] = 0;
+    for (int l = 1; l < m; ++l) {
+        c->soff[l] = o;
+        o += h_vec[l];
+    }
+    c->Hs = o;
+    const size_t h0 = static_cast<size_t>(c->h0), Hs = static_cast<size_t>(std::max(c->Hs, 1));
+    HIP_TRY(c->C0.Ensure(h0 * d * 4));
+    HIP_TRY(c->norm0.Ensure(h0 * 4));
+    HIP_TRY(c->Cs.Ensure(Hs * d * 4));
+    HIP_TRY(c->G_small.Ensure(Hs * Hs * 4));
+    HIP_TRY(c->G0S.Ensure(h0 * Hs * 4));
+    HIP_TRY(c->gdiag_small.Ensure(Hs * 4));
+    HIP_TRY(hipMemcpyAsync(c->C0.p, C0, h0 * d * 4, hipMemcpyHostToDevice, c->stream));
+    HIP_TRY(LaunchNorms(c->C0.as<float>(), d, c->h0, c->norm0.as<float>(), nullptr, c->stream));
+    if (c->Hs > 0) {
+        HIP_TRY(hipMemcpyAsync(c->Cs.p, C_small, static_cast<size_t>(c->Hs) * d * 4, hipMemcpyHostToDevice, c->stream));
+        HIP_TRY(LaunchGram(c->Cs.as<float>(), d, c->Hs, c->G_small.as<float>(), c->stream));
+        HIP_TRY(LaunchCross(c->C0.as<float>(), c->h0, c->Cs.as<float>(), c->Hs, d, c->G0S.as<float>(), c->stream));
+        HIP_TRY(LaunchDiag(c->G_small.as<float>(), c->Hs, c->gdiag_small.as<float>(), c->stream));
+    }
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    c->has_lr = true;
+    return STLQ_MI355_OK;
+}
+
+int stlq_mi355_beam_search_large_root(stlq_mi355_ctx* c, const float* X, const float* xC_small, int64_t n,
+                                      int H_beam, const uint32_t* forced_root, int root_mode, uint32_t* cluster_id,
+                                      uint8_t* B_small, float* best_err) {
+    RC_TRY(CheckCtx(c));
+    if (!c->has_lr) return Fail(STLQ_MI355_ERR_STATE, "large-root codebooks not set");
+    (void)X;
+    (void)xC_small;
+    (void)n;
+    (void)H_beam;
+    (void)forced_root;
+    (void)root_mode;
+    (void)cluster_id;
+    (void)B_small;
+    (void)best_err;
+    return Fail(STLQ_MI355_ERR_UNSUPPORTED, "large-root beam search is not available yet");
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------------------------
+// Device-buffer helpers (include/stlq_mi355_tools.h).
+extern "C" {
+
+int stlq_mi355_dev_alloc(stlq_mi355_ctx* c, size_t bytes, void** out) {
+    RC_TRY(CheckCtx(c));
+    if (!out) return Fail(STLQ_MI355_ERR_INVALID, "out is null");
+    *out = nullptr;
+    HIP_TRY(hipMalloc(out, bytes ? bytes : 256));
+    return STLQ_MI355_OK;
+}
+
+int stlq_mi355_dev_free(stlq_mi355_ctx* c, void* p) {
+    RC_TRY(CheckCtx(c));
+    if (p) {
+        HIP_TRY(hipStreamSynchronize(c->stream));
+        HIP_TRY(hipFree(p));
+    }
+    return STLQ_MI355_OK;
+}
+
+int stlq_mi355_copy_h2d(stlq_mi355_ctx* c, void* dst, const void* src, size_t bytes) {
+    RC_TRY(CheckCtx(c));
+    HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, c->stream));
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    return STLQ_MI355_OK;
+}
+
+int stlq_mi355_copy_d2h(stlq_mi355_ctx* c, void* dst, const void* src, size_t bytes) {
+    RC_TRY(CheckCtx(c));
+    HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    return STLQ_MI355_OK;
+}
+
+int stlq_mi355_dev_copy_kernel(stlq_mi355_ctx* c, void* dst, const void* src, size_t bytes) {
+    RC_TRY(CheckCtx(c));
+    if (bytes % 16 != 0) return Fail(STLQ_MI355_ERR_INVALID, "bytes must be a multiple of 16");
+    HIP_TRY(LaunchCopy16(dst, src, bytes / 16, c->stream));
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    return STLQ_MI355_OK;
+}
+
+int stlq_mi355_synchronize(stlq_mi355_ctx* c) {
+    RC_TRY(CheckCtx(c));
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    return STLQ_MI355_OK;
+}
+
+int stlq_mi355_device_info(stlq_mi355_ctx* c, char* name, int name_len, int* cu_count) {
+    RC_TRY(CheckCtx(c));
+    hipDeviceProp_t prop;
+    HIP_TRY(hipGetDeviceProperties(&prop, c->device));
+    if (name && name_len > 0) {
+        std::strncpy(name, prop.gcnArchName, static_cast<size_t>(name_len) - 1);
+        name[name_len - 1] = '\0';
+    }
+    if (cu_count) *cu_count = prop.multiProcessorCount;
+    return STLQ_MI355_OK;
+}
+
+}  // extern "C"

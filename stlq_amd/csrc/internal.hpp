@@ -1,0 +1,122 @@
+// Internal declarations shared by the HIP translation units of libstlq_mi355.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+
+namespace stlq_mi355 {
+
+constexpr int kMaxM = 20;     // include/stlq/core/model_limits.h:5
+constexpr int kMaxK = 256;    // uint8 codes (include/stlq/common/types.h:20-32)
+constexpr int kMaxBeam = 64;  // slot state lives in one wave64 lane per slot
+constexpr int kWave = 64;
+constexpr int kBeamWavesPerBlock = 4;  // one vector per wave, four vectors per workgroup
+
+// Packed upper-triangular index of R(r, c), r <= c < m (row-major rows of decreasing length).
+__host__ __device__ inline int TriIdx(int m, int r, int c) { return r * m - (r * (r - 1)) / 2 + (c - r); }
+__host__ __device__ inline int TriSize(int m) { return m * (m + 1) / 2; }
+__host__ __device__ inline int CodeStride(int m) { return (m + 3) & ~3; }
+
+// Beam state of one tile of vectors, slot-major (vector i, slot s at i*Hb + s).
+struct BeamState {
+    float* err = nullptr;        // [n*Hb]
+    uint8_t* code = nullptr;     // [n*Hb*CodeStride(m)]
+    float* coef = nullptr;       // [n*Hb*m]
+    float* R = nullptr;          // [n*Hb*TriSize(m)]
+    uint32_t* root = nullptr;    // [n*Hb] (large-root only)
+    int* curH = nullptr;         // [n]
+};
+
+// Gram access for the prefix-LS cross terms. A_t(k) of a beam with prefix codes code_t is
+// row[(off_t + code_t) * ld + offL + k] of a row-major matrix whose element (r, c) is the
+// reference's G(r, c) (linear_algebra.h:17-19 GAt(G, row=flat_t, col=flat)).
+// Large-root: t = 0 reads row `root` of G0S (h0 x Hs, row-major), t >= 1 reads G_small.
+struct GramView {
+    const float* G = nullptr;    // row-major H x H (or Hs x Hs)
+    int ld = 0;
+    const float* G0S = nullptr;  // large-root only: row-major h0 x Hs
+    int off[kMaxM] = {};         // flat offset of each layer inside G's index space
+};
+
+struct LayerArgs {
+    GramView gram;
+    const float* xC = nullptr;    // [n*ldx] per-vector <x, c_f> rows (xC_small for large-root)
+    int64_t ldx = 0;
+    const float* nx2 = nullptr;   // [n]
+    const float* gdiag = nullptr; // G diagonal over the same flat index space
+    BeamState in, out;
+    int64_t n = 0;
+    int m = 0, Hb = 0, K = 0, offL = 0;
+    // final pick (last layer): codes [n*m] (or B_small [n*(m-1)] for large-root), best_err [n]
+    uint8_t* codes_out = nullptr;
+    float* best_err = nullptr;
+    uint32_t* cluster_out = nullptr;
+    int is_last = 0;
+};
+
+struct RootArgs {
+    const float* scores = nullptr;  // [n*ldx] root scores <x, c0_r> (nullable when forced)
+    int64_t ldx = 0;
+    const float* nx2 = nullptr;
+    const float* norm0 = nullptr;   // [h0]
+    const uint32_t* forced = nullptr;
+    BeamState out;
+    int64_t n = 0;
+    int m = 0, Hb = 0, h0 = 0, root_slots = 0;
+    uint8_t* codes_out = nullptr;
+    float* best_err = nullptr;
+    uint32_t* cluster_out = nullptr;
+    int is_last = 0;
+};
+
+// ---- launchers (each defined in the .hip file that holds the kernel) ----
+hipError_t LaunchGram(const float* C, int d, int H, float* G_rm, hipStream_t s);
+hipError_t LaunchCross(const float* C0, int h0, const float* Cs, int Hs, int d, float* G0S_rm, hipStream_t s);
+hipError_t LaunchNorms(const float* C, int d, int H, float* norm2, float* invnorm, hipStream_t s);
+hipError_t LaunchDiag(const float* G_rm, int H, float* diag, hipStream_t s);
+hipError_t LaunchTranspose(const float* in, int rows, int cols, float* out, hipStream_t s);
+hipError_t LaunchXNorm2(const float* X, int d, int64_t n, float* out, hipStream_t s);
+hipError_t LaunchGemmXc(const float* X, int64_t n, int d, const float* C, int H, float* xC, int64_t ldx,
+                        hipStream_t s);
+
+hipError_t LaunchBeamLayer0(const LayerArgs& a, hipStream_t s);
+hipError_t LaunchBeamLayer(int L, bool large_root, const LayerArgs& a, hipStream_t s);
+hipError_t LaunchRootSeed(const RootArgs& a, hipStream_t s);
+
+struct LsArgs {
+    const float* xC = nullptr;
+    int64_t ldx = 0;
+    const float* G_rm = nullptr;
+    int H = 0;
+    int m = 0;
+    int off[kMaxM] = {};
+    const uint8_t* codes = nullptr;  // [n*m]
+    float* a = nullptr;              // [n*m]
+    const float* nx2 = nullptr;
+    float* cost = nullptr;
+    int* fails = nullptr;            // device counter
+    int64_t n = 0;
+};
+hipError_t LaunchLsAll(const LsArgs& a, hipStream_t s);
+hipError_t LaunchCosts(const LsArgs& a, hipStream_t s);
+
+struct IcmArgs {
+    LsArgs ls;                       // codes (mutable through codes_rw), a, cost, nx2
+    uint8_t* codes_rw = nullptr;
+    const float* G_cm = nullptr;     // column-major reference G: G(row, col) at [col*H + row]
+    const float* invnorm = nullptr;
+    uint8_t* active = nullptr;       // [n]
+    uint8_t* changed = nullptr;      // [n]
+    int* fails = nullptr;
+    int j = 0;                       // layer updated by this launch
+    int use_abs = 1;
+    int hj = 0;
+};
+hipError_t LaunchIcmLayer(const IcmArgs& a, hipStream_t s);
+hipError_t LaunchIcmDeactivate(uint8_t* active, const uint8_t* changed, int64_t n, hipStream_t s);
+hipError_t LaunchFill8(uint8_t* p, uint8_t v, int64_t n, hipStream_t s);
+hipError_t LaunchCopy16(void* dst, const void* src, size_t n16, hipStream_t s);
+
+}  // namespace stlq_mi355

@@ -1,0 +1,161 @@
+// xC = C_all^T X on fp32 MFMA (v_mfma_f32_16x16x4_f32): the codeword-distance contraction
+// (StreamKernelProvider::Gemm call sites encoder_encode_base.inc:86-90,
+// encode_base_streaming.cpp:846/2610; cuBLAS in the reference, kernel_provider_cuda_stream_impl.inc:392-444).
+//
+// Output layout is the reference's xC column: for vector i, xC[i*ldx + f] = <x_i, c_f>.
+// Both operands are K-contiguous (d), so the kernel is an "NT" GEMM: rows = vectors,
+// cols = codewords. A 256-thread workgroup computes a 128x128 tile; each wave owns a 64x64
+// sub-tile as 4x4 MFMA blocks. d is staged through LDS in slices of 16 with double buffering;
+// inside a slice each lane's float4 LDS read feeds four consecutive MFMAs (k = 4s + lane/16),
+// so the accumulation order over k is strictly ascending in blocks of 4.
+#include "internal.hpp"
+
+namespace stlq_mi355 {
+namespace {
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+constexpr int kBM = 128;
+constexpr int kBN = 128;
+constexpr int kBK = 16;
+constexpr int kLdsStride = kBK + 4;  // 20 floats: conflict-free float4 reads across 8 rows
+
+struct Staged {
+    float v[2][4];
+};
+
+// Loads this thread's share of a 128 x 16 slice (2 rows x 4 consecutive k) of a K-contiguous
+// matrix with `rows` rows and row length d.
+__device__ __forceinline__ void LoadSlice(const float* __restrict__ M, int64_t rows, int d, int64_t r0,
+                                          int k0, bool vec4, Staged& st) {
+    const int t = threadIdx.x;
+    const int quad = t & 3;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        const int64_t row = r0 + (t >> 2) + 64 * q;
+        const int k = k0 + 4 * quad;
+        if (row < rows && vec4 && k + 3 < d) {
+            const float4 x = *reinterpret_cast<const float4*>(M + row * d + k);
+            st.v[q][0] = x.x;
+            st.v[q][1] = x.y;
+            st.v[q][2] = x.z;
+            st.v[q][3] = x.w;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) st.v[q][e] = (row < rows && k + e < d) ? M[row * d + k + e] : 0.0f;
+        }
+    }
+}
+
+// Stores a staged slice into LDS with k permuted: local k = 4s + g lands at position 4g + s.
+__device__ __forceinline__ void StoreSlice(float (*S)[kLdsStride], const Staged& st) {
+    const int t = threadIdx.x;
+    const int quad = t & 3;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        const int row = (t >> 2) + 64 * q;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) S[row][4 * e + quad] = st.v[q][e];
+    }
+}
+
+__global__ __launch_bounds__(256) void GemmXcKernel(const float* __restrict__ X, int64_t n, int d,
+                                                     const float* __restrict__ C, int H,
+                                                     float* __restrict__ xC, int64_t ldx,
+                                                     int tiles_h, int64_t tiles_total,
+                                                     int64_t per_xcd) {
+    __shared__ float As[2][kBM][kLdsStride];
+    __shared__ float Bs[2][kBN][kLdsStride];
+
+    // XCD-aware tile order: workgroups are dispatched round-robin over the 8 XCDs, so block b
+    // runs on XCD b % 8. Give each XCD a contiguous run of tiles so the 128-vector slices of X
+    // that neighbouring codeword tiles share stay in that XCD's L2.
+    const int64_t b = blockIdx.x;
+    const int64_t tile = (b & 7) * per_xcd + (b >> 3);
+    if (tile >= tiles_total) return;
+    const int64_t tx = tile / tiles_h;
+    const int th = static_cast<int>(tile - tx * tiles_h);
+    const int64_t i0 = tx * kBM;
+    const int64_t h0 = static_cast<int64_t>(th) * kBN;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int g = lane >> 4, r16 = lane & 15;
+    const bool vec4 = (d & 3) == 0;
+
+    floatx4 acc[4][4];
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[a][c] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    const int nk = (d + kBK - 1) / kBK;
+    Staged sa, sb;
+    LoadSlice(X, n, d, i0, 0, vec4, sa);
+    LoadSlice(C, H, d, h0, 0, vec4, sb);
+    StoreSlice(As[0], sa);
+    StoreSlice(Bs[0], sb);
+    __syncthreads();
+
+    for (int kt = 0; kt < nk; ++kt) {
+        const int cur = kt & 1;
+        const bool more = kt + 1 < nk;
+        if (more) {
+            LoadSlice(X, n, d, i0, (kt + 1) * kBK, vec4, sa);
+            LoadSlice(C, H, d, h0, (kt + 1) * kBK, vec4, sb);
+        }
+        floatx4 af[4], bf[4];
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+            af[a] = *reinterpret_cast<const floatx4*>(&As[cur][wm * 64 + a * 16 + r16][4 * g]);
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+            bf[c] = *reinterpret_cast<const floatx4*>(&Bs[cur][wn * 64 + c * 16 + r16][4 * g]);
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int a = 0; a < 4; ++a)
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    acc[a][c] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[a][s], bf[c][s], acc[a][c], 0, 0, 0);
+        if (more) {
+            StoreSlice(As[cur ^ 1], sa);
+            StoreSlice(Bs[cur ^ 1], sb);
+        }
+        __syncthreads();
+    }
+
+    // D block (a, c): lane holds rows 4g..4g+3 of column r16.
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int64_t row = i0 + wm * 64 + a * 16 + 4 * g + r;
+            if (row >= n) continue;
+            float* dst = xC + row * ldx;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const int64_t col = h0 + wn * 64 + c * 16 + r16;
+                if (col < H) dst[col] = acc[a][c][r];
+            }
+        }
+    }
+}
+
+}  // namespace
+
+hipError_t LaunchGemmXc(const float* X, int64_t n, int d, const float* C, int H, float* xC, int64_t ldx,
+                        hipStream_t s) {
+    if (n <= 0 || H <= 0) return hipSuccess;
+    const int tiles_h = (H + kBN - 1) / kBN;
+    const int64_t tiles_x = (n + kBM - 1) / kBM;
+    const int64_t total = tiles_x * tiles_h;
+    const int64_t per_xcd = (total + 7) / 8;
+    const int64_t blocks = per_xcd * 8;
+    hipLaunchKernelGGL(GemmXcKernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, X, n, d, C, H, xC,
+                       ldx, tiles_h, total, per_xcd);
+    return hipGetLastError();
+}
+
+}  // namespace stlq_mi355

@@ -1,0 +1,299 @@
+// Per-vector least-squares refit, cost, and ICM layer sweeps.
+//
+//  * LsAllKernel     SolveLeastSquaresAll (src/quantizer/least_squares.cpp:406-565)
+//  * CostsKernel     ComputeCosts / SampleCost (src/quantizer/cost_utils.cpp:112-158)
+//  * IcmLayerKernel  one layer of RunIcm (src/quantizer/icm.cpp:249-329)
+//
+// The Cholesky is the hand-written one of least_squares.cpp:44-84 (row-major upper factor,
+// true division, retry with diagonal bumps 1e-6, 1e-5, 1e-4). Its failure test is the
+// reference's `sum <= 1e-6` for m in {5,10}; for other m the reference calls LAPACK spotrf,
+// whose failure test (pivot <= 0 or NaN) is used here with the same hand-written arithmetic.
+#include "internal.hpp"
+
+namespace stlq_mi355 {
+namespace {
+
+constexpr float kEps = 1e-6f;
+constexpr float kInfF = __builtin_huge_valf();
+
+template <int M>
+__device__ __forceinline__ bool CholUpper(float (&A)[M * M]) {
+    constexpr bool kLapackTest = !(M == 5 || M == 10);
+#pragma unroll
+    for (int k = 0; k < M; ++k) {
+        float sum = A[k * M + k];
+#pragma unroll
+        for (int j = 0; j < k; ++j) {
+            const float v = A[j * M + k];
+            sum = sum - v * v;
+        }
+        if (kLapackTest ? !(sum > 0.0f) : (sum <= kEps)) return false;
+        const float diag = sqrtf(sum);
+        A[k * M + k] = diag;
+#pragma unroll
+        for (int i = k + 1; i < M; ++i) {
+            float s = A[k * M + i];
+#pragma unroll
+            for (int j = 0; j < k; ++j) s = s - A[j * M + k] * A[j * M + i];
+            A[k * M + i] = s / diag;
+        }
+    }
+    return true;
+}
+
+template <int M>
+__device__ __forceinline__ void SolveUpper(const float (&A)[M * M], const float (&b)[M], float (&x)[M]) {
+    float y[M];
+#pragma unroll
+    for (int i = 0; i < M; ++i) {
+        float s = b[i];
+#pragma unroll
+        for (int k = 0; k < i; ++k) s = s - A[k * M + i] * y[k];
+        y[i] = s / A[i * M + i];
+    }
+#pragma unroll
+    for (int i = M - 1; i >= 0; --i) {
+        float s = y[i];
+#pragma unroll
+        for (int k = i + 1; k < M; ++k) s = s - A[i * M + k] * x[k];
+        x[i] = s / A[i * M + i];
+    }
+}
+
+// SolveLeastSquaresSampleFixed (least_squares.cpp:86-129) for one vector.
+template <int M>
+__device__ __forceinline__ bool SolveLs(const LsArgs& p, const float* __restrict__ xCi, const int (&flat)[M],
+                                        float (&x)[M]) {
+    float A[M * M];
+    float b[M];
+    auto fill = [&](float lambda) {
+#pragma unroll
+        for (int q = 0; q < M * M; ++q) A[q] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < M; ++j) {
+            b[j] = xCi[flat[j]];
+#pragma unroll
+            for (int k = 0; k <= j; ++k) A[k * M + j] = p.G_rm[static_cast<int64_t>(flat[k]) * p.H + flat[j]];
+            A[j * M + j] = A[j * M + j] + lambda;
+        }
+    };
+    fill(0.0f);
+    bool ok = CholUpper<M>(A);
+    if (!ok) {
+        float bump = kEps;
+        for (int attempt = 0; attempt < 3 && !ok; ++attempt) {
+            fill(bump);
+            ok = CholUpper<M>(A);
+            bump = bump * 10.0f;
+        }
+    }
+    if (!ok) return false;
+    SolveUpper<M>(A, b, x);
+    return true;
+}
+
+// SampleCost (cost_utils.cpp:112-137): nx2 - 2*sum a_l xC_l + sum_l sum_k a_l a_k G(l,k).
+template <int M>
+__device__ __forceinline__ float Cost(const LsArgs& p, const float* __restrict__ xCi, const int (&flat)[M],
+                                      const float (&a)[M], float nx2) {
+    float term1 = 0.0f, term2 = 0.0f;
+#pragma unroll
+    for (int l = 0; l < M; ++l) {
+        const float al = a[l];
+        term1 = term1 + al * xCi[flat[l]];
+        const float* Grow = p.G_rm + static_cast<int64_t>(flat[l]) * p.H;
+#pragma unroll
+        for (int k = 0; k < M; ++k) term2 = term2 + (al * a[k]) * Grow[flat[k]];
+    }
+    return nx2 - 2.0f * term1 + term2;
+}
+
+template <int M>
+__device__ __forceinline__ void Flats(const LsArgs& p, const uint8_t* __restrict__ c, int (&flat)[M]) {
+#pragma unroll
+    for (int l = 0; l < M; ++l) flat[l] = p.off[l] + c[l];
+}
+
+template <int M>
+__global__ __launch_bounds__(256) void LsAllKernel(LsArgs p) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= p.n) return;
+    int flat[M];
+    Flats<M>(p, p.codes + i * M, flat);
+    const float* xCi = p.xC + i * p.ldx;
+    float x[M];
+    float* ai = p.a + i * M;
+    if (SolveLs<M>(p, xCi, flat, x)) {
+#pragma unroll
+        for (int l = 0; l < M; ++l) ai[l] = x[l];
+    } else {
+#pragma unroll
+        for (int l = 0; l < M; ++l) ai[l] = 0.0f;  // least_squares.cpp:452-455
+        if (p.fails) atomicAdd(p.fails, 1);
+    }
+}
+
+template <int M>
+__global__ __launch_bounds__(256) void CostsKernel(LsArgs p) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= p.n) return;
+    int flat[M];
+    Flats<M>(p, p.codes + i * M, flat);
+    float a[M];
+#pragma unroll
+    for (int l = 0; l < M; ++l) a[l] = p.a[i * M + l];
+    p.cost[i] = Cost<M>(p, p.xC + i * p.ldx, flat, a, p.nx2[i]);
+}
+
+__device__ __forceinline__ float ReadLane(float v, int l) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+template <int CTRL>
+__device__ __forceinline__ float Dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float WaveMax(float v) {
+    v = fmaxf(v, Dpp<0xB1>(v));
+    v = fmaxf(v, Dpp<0x4E>(v));
+    v = fmaxf(v, Dpp<0x141>(v));
+    v = fmaxf(v, Dpp<0x140>(v));
+    return fmaxf(fmaxf(ReadLane(v, 0), ReadLane(v, 16)), fmaxf(ReadLane(v, 32), ReadLane(v, 48)));
+}
+
+// One ICM layer update (icm.cpp:259-328), one wave per vector. Lanes score codes
+// t = lane + 64*jj of layer j:
+//   val(t) = (xC(start+t) - sum_{l != j} a_l G(start+t, flat_l)) * invnorm(start+t)
+// (subtractions in ascending l), pick the first maximum of val (or |val|), and if it differs
+// from the current code, re-solve LS and accept iff new_cost + 1e-6 < cost.
+template <int M>
+__global__ __launch_bounds__(256) void IcmLayerKernel(IcmArgs q) {
+    const LsArgs& p = q.ls;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * 4 + wave;
+    if (i >= p.n) return;
+    if (!q.active[i]) return;
+    const int j = q.j, hj = q.hj;
+    const int start = p.off[j];
+    uint8_t* ci = q.codes_rw + i * M;
+    float* ai = p.a + i * M;
+    const float* xCi = p.xC + i * p.ldx;
+    int flat[M];
+    float a[M];
+#pragma unroll
+    for (int l = 0; l < M; ++l) {
+        flat[l] = p.off[l] + ci[l];
+        a[l] = ai[l];
+    }
+    const int old_code = ci[j];
+
+    float best_val = -kInfF;
+    int best_t = 0x7fffffff;
+    for (int t0 = 0; t0 < hj; t0 += 64) {
+        const int t = t0 + lane;
+        float score = -kInfF;
+        if (t < hj) {
+            float tmp = xCi[start + t];
+#pragma unroll
+            for (int l = 0; l < M; ++l) {
+                if (l == j) continue;
+                tmp = tmp - a[l] * q.G_cm[static_cast<int64_t>(flat[l]) * p.H + start + t];
+            }
+            const float val = tmp * q.invnorm[start + t];
+            score = q.use_abs ? fabsf(val) : val;
+            if (__builtin_isnan(score)) score = -kInfF;  // NaN never wins a strict '>' scan
+        }
+        // first maximum over this chunk, then over chunks in order (strict '>' keeps the earlier)
+        const float mx = WaveMax(score);
+        if (mx > best_val) {
+            const uint64_t eq = __ballot(t < hj && score == mx);
+            best_val = mx;
+            best_t = t0 + static_cast<int>(__builtin_ctzll(eq));
+        }
+    }
+    const int best_code = (best_val > -kInfF) ? best_t : old_code;
+    if (best_code == old_code) return;
+    if (lane != 0) return;
+
+    int nflat[M];
+#pragma unroll
+    for (int l = 0; l < M; ++l) nflat[l] = (l == j) ? start + best_code : flat[l];
+    float x[M];
+    if (!SolveLs<M>(p, xCi, nflat, x)) {
+        atomicAdd(q.fails, 1);
+        return;  // icm.cpp:313-318: roll back (nothing was written)
+    }
+    const float new_cost = Cost<M>(p, xCi, nflat, x, p.nx2[i]);
+    if (new_cost + kEps < p.cost[i]) {
+        ci[j] = static_cast<uint8_t>(best_code);
+#pragma unroll
+        for (int l = 0; l < M; ++l) ai[l] = x[l];
+        p.cost[i] = new_cost;
+        q.changed[i] = 1;
+    }
+}
+
+__global__ void DeactivateKernel(uint8_t* active, const uint8_t* changed, int64_t n) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < n && active[i] && !changed[i]) active[i] = 0;
+}
+
+#define STLQ_LAUNCH_M(KER, M_, grid, block, s, a) \
+    hipLaunchKernelGGL((KER<M_>), grid, block, 0, s, a)
+
+#define STLQ_SWITCH_M(KER, m, grid, block, s, a)                  \
+    switch (m) {                                                  \
+        case 1: STLQ_LAUNCH_M(KER, 1, grid, block, s, a); break;  \
+        case 2: STLQ_LAUNCH_M(KER, 2, grid, block, s, a); break;  \
+        case 3: STLQ_LAUNCH_M(KER, 3, grid, block, s, a); break;  \
+        case 4: STLQ_LAUNCH_M(KER, 4, grid, block, s, a); break;  \
+        case 5: STLQ_LAUNCH_M(KER, 5, grid, block, s, a); break;  \
+        case 6: STLQ_LAUNCH_M(KER, 6, grid, block, s, a); break;  \
+        case 7: STLQ_LAUNCH_M(KER, 7, grid, block, s, a); break;  \
+        case 8: STLQ_LAUNCH_M(KER, 8, grid, block, s, a); break;  \
+        case 9: STLQ_LAUNCH_M(KER, 9, grid, block, s, a); break;  \
+        case 10: STLQ_LAUNCH_M(KER, 10, grid, block, s, a); break; \
+        case 11: STLQ_LAUNCH_M(KER, 11, grid, block, s, a); break; \
+        case 12: STLQ_LAUNCH_M(KER, 12, grid, block, s, a); break; \
+        case 13: STLQ_LAUNCH_M(KER, 13, grid, block, s, a); break; \
+        case 14: STLQ_LAUNCH_M(KER, 14, grid, block, s, a); break; \
+        case 15: STLQ_LAUNCH_M(KER, 15, grid, block, s, a); break; \
+        case 16: STLQ_LAUNCH_M(KER, 16, grid, block, s, a); break; \
+        case 17: STLQ_LAUNCH_M(KER, 17, grid, block, s, a); break; \
+        case 18: STLQ_LAUNCH_M(KER, 18, grid, block, s, a); break; \
+        case 19: STLQ_LAUNCH_M(KER, 19, grid, block, s, a); break; \
+        case 20: STLQ_LAUNCH_M(KER, 20, grid, block, s, a); break; \
+        default: return hipErrorInvalidValue;                     \
+    }
+
+}  // namespace
+
+hipError_t LaunchLsAll(const LsArgs& a, hipStream_t s) {
+    if (a.n <= 0) return hipSuccess;
+    const dim3 grid(static_cast<unsigned>((a.n + 255) / 256)), block(256);
+    STLQ_SWITCH_M(LsAllKernel, a.m, grid, block, s, a);
+    return hipGetLastError();
+}
+
+hipError_t LaunchCosts(const LsArgs& a, hipStream_t s) {
+    if (a.n <= 0) return hipSuccess;
+    const dim3 grid(static_cast<unsigned>((a.n + 255) / 256)), block(256);
+    STLQ_SWITCH_M(CostsKernel, a.m, grid, block, s, a);
+    return hipGetLastError();
+}
+
+hipError_t LaunchIcmLayer(const IcmArgs& a, hipStream_t s) {
+    if (a.ls.n <= 0) return hipSuccess;
+    const dim3 grid(static_cast<unsigned>((a.ls.n + 3) / 4)), block(256);
+    STLQ_SWITCH_M(IcmLayerKernel, a.ls.m, grid, block, s, a);
+    return hipGetLastError();
+}
+
+hipError_t LaunchIcmDeactivate(uint8_t* active, const uint8_t* changed, int64_t n, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(DeactivateKernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s, active,
+                       changed, n);
+    return hipGetLastError();
+}
+
+}  // namespace stlq_mi355

@@ -1,0 +1,351 @@
+"""HIP encoder vs the CPU oracle, through the C ABI.
+
+Bar: bit-exact wherever both sides see the same inputs (precomp, ||x||^2, beam codes and
+selected errors given the same xC/G/||x||^2, LS coefficients, costs, ICM); for the end-to-end
+encode, whose xC comes from fp32 MFMA on the GPU and from a sequential CPU dot product in the
+oracle: codes differ on at most 0.1% of vectors, only where the two
+code tuples' fp64 costs tie within 1e-5 relative, and per-vector fp64 MSE within 1e-5 relative.
+"""
+import numpy as np
+import pytest
+
+from stlq_amd.encoder import EncodeConfig
+from tests.helpers import parity, random_problem, rvq_problem
+
+pytestmark = pytest.mark.gpu
+
+
+def _set(ctx, C, h):
+    ctx.set_codebooks(C, h)
+    return ctx.get_precomp()
+
+
+def _bits(a):
+    return np.ascontiguousarray(a).view(np.uint32)
+
+
+def test_precomp_bit_exact(ctx, orc):
+    X, C = rvq_problem(1, 100, 37, 3, 40)
+    h = [40, 40, 40]
+    G, inv = _set(ctx, C, h)
+    Go, invo = orc.build_precomp(C, h)
+    assert np.array_equal(_bits(G), _bits(Go))
+    assert np.array_equal(_bits(inv), _bits(invo))
+
+
+def test_xnorm_bit_exact(ctx, orc):
+    X, C = random_problem(2, 3001, 130, [8, 8], x_scale=50.0)
+    ctx.set_codebooks(C, [8, 8])
+    assert np.array_equal(_bits(ctx.xnorm2(X)), _bits(orc.xnorm2(X)))
+
+
+@pytest.mark.parametrize("n,d,H", [(1000, 128, 2048), (777, 96, 300), (130, 7, 48), (257, 960, 512)])
+def test_gemm_xc_close(ctx, orc, n, d, H):
+    rng = np.random.default_rng(n + d)
+    X = (rng.standard_normal((n, d)) * 3).astype(np.float32)
+    C = rng.standard_normal((H, d)).astype(np.float32)
+    ctx.set_codebooks(C, [256] * (H // 256) + ([H % 256] if H % 256 else []))
+    xg = ctx.gemm_xc(X)
+    x64 = X.astype(np.float64) @ C.astype(np.float64).T
+    scale = np.sqrt(np.sum(X.astype(np.float64) ** 2, 1))[:, None] * np.sqrt(np.sum(C.astype(np.float64) ** 2, 1))[None, :]
+    assert np.max(np.abs(xg - x64) / scale) < 4 * d * 2.0 ** -24
+
+
+BEAM_CASES = [
+    # name, seed, n, d, h_vec, H_beam, kind
+    ("m2_K16_b4", 10, 800, 12, [16, 16], 4, "gauss"),
+    ("m4_K32_b1", 11, 800, 24, [32] * 4, 1, "gauss"),
+    ("m4_K256_b4_c1", 12, 600, 128, [256] * 4, 4, "gauss"),
+    ("m8_K256_b16_c2", 13, 500, 128, [256] * 8, 16, "desc"),
+    ("m8_K256_b16_sphere", 14, 400, 96, [256] * 8, 16, "sphere"),
+    ("m5_K100_b64", 15, 300, 20, [100, 90, 80, 70, 60], 64, "gauss"),
+    ("m3_K7_b40", 16, 500, 6, [7, 9, 5], 40, "gauss"),
+    ("m10_K64_b8", 17, 300, 40, [64] * 10, 8, "gauss"),
+    ("m16_K256_b8_decay", 18, 120, 64, [256] * 16, 8, "decay"),
+    ("m1_K200_b3", 19, 500, 16, [200], 3, "gauss"),
+    ("m6_K65_b33", 20, 300, 30, [65, 130, 200, 3, 256, 64], 33, "gauss"),
+]
+
+
+def _beam_case(seed, n, d, h, kind):
+    if kind == "gauss" and max(h) < 100:
+        return random_problem(seed, n, d, h, x_scale=2.0)
+    if len(set(h)) == 1:
+        return rvq_problem(seed, n, d, len(h), h[0], kind=kind, train_n=max(2000, 4 * h[0]), iters=4)
+    return random_problem(seed, n, d, h, x_scale=2.0)
+
+
+@pytest.mark.parametrize("name,seed,n,d,h,Hb,kind", BEAM_CASES, ids=[c[0] for c in BEAM_CASES])
+def test_beam_bit_exact_given_same_inputs(ctx, orc, name, seed, n, d, h, Hb, kind):
+    X, C = _beam_case(seed, n, d, h, kind)
+    G, inv = _set(ctx, C, h)
+    nx2 = orc.xnorm2(X)
+    xC = orc.gemm_xc(C, X)
+    codes_o, err_o = orc.beam_search(nx2, xC, G, h, Hb)
+    codes_g, err_g = ctx.beam_search(xC, Hb, nx2=nx2)
+    bad = np.nonzero(np.any(codes_o != codes_g, axis=1))[0]
+    assert bad.size == 0, (name, bad[:10], codes_o[bad[:3]], codes_g[bad[:3]])
+    assert np.array_equal(_bits(err_o), _bits(err_g))
+
+
+def test_beam_from_gpu_xc_bit_exact(ctx, orc):
+    """The oracle fed the GPU's own xC, G and ||x||^2 reproduces the GPU encode exactly."""
+    X, C = rvq_problem(21, 2000, 128, 8, 256, kind="desc", train_n=3000, iters=4)
+    h = [256] * 8
+    G, inv = _set(ctx, C, h)
+    xg = ctx.gemm_xc(X)
+    nx = ctx.xnorm2(X)
+    codes_g, _, _, _ = ctx.encode(X, EncodeConfig(H_beam=16, icm_iters=0, want_coeffs=False))
+    codes_o, _ = orc.beam_search(nx, xg, G, h, 16)
+    assert np.array_equal(codes_g, codes_o)
+
+
+DEGENERATE = ["dup_within_layer", "dup_across_layers", "zero_codeword", "zero_layer", "zero_root_layer",
+              "tiny_codebook", "scaled_copies"]
+
+
+@pytest.mark.parametrize("case", DEGENERATE)
+def test_beam_degenerate_bit_exact(ctx, orc, case):
+    """Exact ties, skipped candidates (alpha == 0, denom == 0), non-finite beam errors and the
+    all-skipped fallback follow the reference's slot rules bit for bit."""
+    rng = np.random.default_rng(100 + DEGENERATE.index(case))
+    d, h = 10, [12, 12, 12, 12]
+    C = rng.standard_normal((48, d)).astype(np.float32)
+    X = (rng.standard_normal((400, d)) * 2).astype(np.float32)
+    if case == "dup_within_layer":
+        C[3] = C[7]
+        C[12 + 5] = C[12 + 1]
+        C[24 + 0] = C[24 + 11]
+    elif case == "dup_across_layers":
+        C[12 + 4] = C[2]
+        C[24 + 4] = C[2]
+        C[36 + 9] = C[12 + 4]
+    elif case == "zero_codeword":
+        C[5] = 0
+        C[12 + 0] = 0
+        C[36 + 11] = 0
+    elif case == "zero_layer":
+        C[24:36] = 0
+    elif case == "zero_root_layer":
+        C[0:12] = 0
+    elif case == "tiny_codebook":
+        h = [2, 1, 3, 2]
+        C = C[:8]
+    elif case == "scaled_copies":
+        C[12 + 3] = 2.0 * C[1]
+        C[24 + 6] = -0.5 * C[12 + 8]
+    G, inv = _set(ctx, C, h)
+    nx2 = orc.xnorm2(X)
+    xC = orc.gemm_xc(C, X)
+    for Hb in (1, 2, 5, 16):
+        codes_o, err_o = orc.beam_search(nx2, xC, G, h, Hb)
+        codes_g, err_g = ctx.beam_search(xC, Hb, nx2=nx2)
+        assert np.array_equal(codes_o, codes_g), (case, Hb)
+        assert np.array_equal(_bits(err_o), _bits(err_g)), (case, Hb)
+
+
+def test_beam_user_precomp_nonsymmetric(ctx, orc):
+    """set_precomp with a caller's G: every read uses the reference's G(row, col) element."""
+    X, C = random_problem(22, 500, 16, [20, 20, 20], x_scale=2.0)
+    h = [20, 20, 20]
+    G, inv = orc.build_precomp(C, h)
+    Gp = G.copy()
+    rng = np.random.default_rng(3)
+    Gp += (rng.standard_normal(G.shape) * 1e-3).astype(np.float32)  # no longer symmetric
+    ctx.set_precomp(C, h, Gp, inv)
+    G2, _ = ctx.get_precomp()
+    assert np.array_equal(G2, Gp)
+    nx2 = orc.xnorm2(X)
+    xC = orc.gemm_xc(C, X)
+    codes_o, err_o = orc.beam_search(nx2, xC, Gp, h, 6)
+    codes_g, err_g = ctx.beam_search(xC, 6, nx2=nx2)
+    assert np.array_equal(codes_o, codes_g)
+    assert np.array_equal(_bits(err_o), _bits(err_g))
+    codes_i, a_i, cost_i, _ = orc.icm(xC, Gp, inv, h, nx2, codes_o, 2, True, 5)
+    codes_j, a_j, cost_j = ctx.icm(xC, codes_o, 2, True, 5, nx2=nx2)
+    assert np.array_equal(codes_i, codes_j)
+    assert np.array_equal(_bits(a_i), _bits(a_j))
+
+
+@pytest.mark.parametrize("m", [1, 3, 4, 5, 8, 10, 16])
+def test_ls_and_costs_bit_exact(ctx, orc, m):
+    h = [32] * m
+    X, C = random_problem(30 + m, 1500, 24, h, x_scale=2.0)
+    G, inv = _set(ctx, C, h)
+    nx2 = orc.xnorm2(X)
+    xC = orc.gemm_xc(C, X)
+    codes = np.random.default_rng(m).integers(0, 32, size=(1500, m)).astype(np.uint8)
+    codes[7, :] = codes[7, 0]  # tuples that need the retry bumps: same code index in every layer
+    a_o, f_o = orc.solve_ls_all(xC, G, h, codes)
+    a_g, f_g = ctx.solve_ls_all(xC, codes)
+    assert f_o == f_g
+    assert np.array_equal(_bits(a_o), _bits(a_g))
+    c_o = orc.compute_costs(xC, G, h, codes, a_o, nx2)
+    c_g = ctx.compute_costs(xC, codes, a_o, nx2)
+    assert np.array_equal(_bits(c_o), _bits(c_g))
+
+
+@pytest.mark.parametrize("use_abs", [True, False])
+@pytest.mark.parametrize("m,K,d,iters", [(8, 256, 96, 2), (5, 64, 32, 4), (10, 32, 40, 3)])
+def test_icm_bit_exact(ctx, orc, use_abs, m, K, d, iters):
+    h = [K] * m
+    X, C = rvq_problem(40 + m, 1200, d, m, K, kind="sphere" if d == 96 else "gauss", train_n=max(2000, 4 * K), iters=4)
+    G, inv = _set(ctx, C, h)
+    nx2 = orc.xnorm2(X)
+    xC = orc.gemm_xc(C, X)
+    codes0, _ = orc.beam_search(nx2, xC, G, h, 2)
+    seed = 38251450
+    co, ao, so, fo = orc.icm(xC, G, inv, h, nx2, codes0, iters, use_abs, seed)
+    cg, ag, sg = ctx.icm(xC, codes0, iters, use_abs, seed, nx2=nx2)
+    assert np.any(co != codes0)
+    assert np.array_equal(co, cg)
+    assert np.array_equal(_bits(ao), _bits(ag))
+    assert np.array_equal(_bits(so), _bits(sg))
+
+
+def _oracle_encode(orc, X, C, h, Hb, icm_iters=0, use_abs=True, seed=38251450, gemm_mode=1):
+    G, inv = orc.build_precomp(C, h)
+    nx2 = orc.xnorm2(X)
+    xC = orc.gemm_xc(C, X, mode=gemm_mode)
+    codes, err = orc.beam_search(nx2, xC, G, h, Hb)
+    if icm_iters:
+        codes, a, cost, _ = orc.icm(xC, G, inv, h, nx2, codes, icm_iters, use_abs, seed)
+    else:
+        a, _ = orc.solve_ls_all(xC, G, h, codes)
+        cost = orc.compute_costs(xC, G, h, codes, a, nx2)
+    return codes, a, cost
+
+
+def _scaled_config(cfg):
+    from stlq_amd import workloads
+
+    w = workloads.CONFIGS[cfg]
+    n = {"C1": 20000, "C2": 4000, "C3": 4000, "C4": 1000}[cfg]
+    mix = workloads.Mixture(w.kind, w.d, w.n_comp, w.seed)
+    Xtr = mix.sample(10_000_000, 4000 if w.d < 900 else 2000)
+    C = workloads.residual_codebooks(Xtr, w.m, w.K, 4, w.seed + 5, spherical=(w.kind == "sphere"))
+    X = mix.sample(0, n)
+    return w, X, C, [w.K] * w.m
+
+
+@pytest.mark.parametrize("cfg", ["C1", "C2", "C3", "C4"])
+def test_encode_end_to_end_bit_exact(ctx, orc, cfg):
+    """Scaled-down benchmark configurations, GPU end to end (MFMA xC, beam, [ICM], LS, cost)
+    vs the oracle end to end with xC accumulated in the device GEMM's fused k order:
+    codes, coefficients and costs are identical."""
+    w, X, C, h = _scaled_config(cfg)
+    ctx.set_codebooks(C, h)
+    cfgc = EncodeConfig(H_beam=w.H_beam, icm_iters=w.icm_iters, want_coeffs=True)
+    codes_g, a_g, cost_g, (bm, fm) = ctx.encode(X, cfgc, want_mse=True)
+    codes_o, a_o, cost_o = _oracle_encode(orc, X, C, h, w.H_beam, w.icm_iters, gemm_mode=1)
+    bad = np.nonzero(np.any(codes_o != codes_g, axis=1))[0]
+    assert bad.size == 0, (cfg, bad.size, bad[:10])
+    assert np.array_equal(_bits(a_o), _bits(a_g))
+    assert np.array_equal(_bits(cost_o), _bits(cost_g))
+    assert np.isfinite(bm) and np.isfinite(fm) and fm <= bm * (1 + 1e-6)
+    want_fm = np.mean(np.maximum(cost_o.astype(np.float64), 0.0))
+    assert abs(fm - want_fm) <= 1e-9 * abs(want_fm)
+
+
+@pytest.mark.parametrize("cfg", ["C1", "C2", "C3", "C4"])
+def test_encode_parity_unfused_oracle_xc(ctx, orc, cfg):
+    """Sensitivity to the GEMM summation order (the reference's BLAS order is unpinned): against
+    an oracle whose xC is a non-fused sequential dot, the codes differ only on cost ties —
+    every differing vector's two tuples have fp64 LS costs equal within 1e-5 relative — and on
+    at most 0.1% of the vectors (1% for the 1000-vector d=960 case, where a single tie is 0.1%)."""
+    w, X, C, h = _scaled_config(cfg)
+    ctx.set_codebooks(C, h)
+    cfgc = EncodeConfig(H_beam=w.H_beam, icm_iters=w.icm_iters, want_coeffs=True)
+    codes_g, _, _, _ = ctx.encode(X, cfgc)
+    codes_o, _, _ = _oracle_encode(orc, X, C, h, w.H_beam, w.icm_iters, gemm_mode=0)
+    rep = parity(orc, X, C, h, codes_o, codes_g, max_frac=(1e-2 if cfg == "C4" else 1e-3))
+    assert rep["ok"], rep
+
+
+def test_encode_device_matches_host(ctx, orc):
+    X, C = rvq_problem(50, 3000, 64, 6, 128, train_n=2000, iters=3)
+    h = [128] * 6
+    ctx.set_codebooks(C, h)
+    cfg = EncodeConfig(H_beam=8, icm_iters=1, want_coeffs=True)
+    codes_h, a_h, cost_h, _ = ctx.encode(X, cfg)
+    n, d, m = X.shape[0], X.shape[1], 6
+    dX = ctx.dev_alloc(X.nbytes)
+    dc = ctx.dev_alloc(n * m)
+    da = ctx.dev_alloc(n * m * 4)
+    ds = ctx.dev_alloc(n * 4)
+    try:
+        ctx.h2d(dX, X)
+        ctx.encode_device(dX, n, cfg, dc, da, ds)
+        ctx.synchronize()
+        codes_d = ctx.d2h(np.empty((n, m), np.uint8), dc)
+        a_d = ctx.d2h(np.empty((n, m), np.float32), da)
+        cost_d = ctx.d2h(np.empty(n, np.float32), ds)
+    finally:
+        for p in (dX, dc, da, ds):
+            ctx.dev_free(p)
+    assert np.array_equal(codes_h, codes_d)
+    assert np.array_equal(_bits(a_h), _bits(a_d))
+    assert np.array_equal(_bits(cost_h), _bits(cost_d))
+    t = ctx.last_timings()
+    assert t.n == n and t.gemm_ms > 0 and t.beam_ms > 0
+
+
+def test_tiled_encode_matches_single_tile(ctx, orc, monkeypatch):
+    """Splitting the encode into workspace-bounded tiles does not change any result
+    (mirrors tests/test_streaming_encode_base.cpp:253-268)."""
+    X, C = rvq_problem(51, 5000, 32, 4, 64, train_n=2000, iters=3)
+    h = [64] * 4
+    ctx.set_codebooks(C, h)
+    cfg = EncodeConfig(H_beam=4, icm_iters=2, want_coeffs=True)
+    codes1, a1, cost1, _ = ctx.encode(X, cfg)
+    monkeypatch.setenv("STLQ_MI355_WORKSPACE_GB", "0.0005")  # ~1k-vector tiles
+    codes2, a2, cost2, _ = ctx.encode(X, cfg)
+    assert np.array_equal(codes1, codes2)
+    assert np.array_equal(_bits(a1), _bits(a2))
+    assert np.array_equal(_bits(cost1), _bits(cost2))
+
+
+@pytest.mark.parametrize("chunk", [1000, 1777, 5000])
+def test_stream_matches_in_memory(ctx, chunk):
+    from stlq_amd import workloads
+
+    mix = workloads.Mixture("desc", 32, 64, 9)
+    X = mix.sample(0, 5000)
+    C = workloads.residual_codebooks(mix.sample(1_000_000, 2000), 4, 64, 3, 4)
+    h = [64] * 4
+    ctx.set_codebooks(C, h)
+    cfg = EncodeConfig(H_beam=4, icm_iters=1, want_coeffs=True)
+    codes, a, cost, _ = ctx.encode(X, cfg)
+    got_c = np.zeros_like(codes)
+    got_a = np.zeros_like(a)
+    got_s = np.zeros_like(cost)
+    seen = []
+
+    def fill(first, count, out):
+        out[:] = X[first:first + count]
+
+    def sink(first, count, c, av, cv):
+        seen.append(first)
+        got_c[first:first + count] = c
+        got_a[first:first + count] = av
+        got_s[first:first + count] = cv
+
+    st = ctx.encode_stream(X.shape[0], chunk, cfg, fill, sink)
+    assert seen == sorted(seen) and len(seen) == -(-5000 // chunk)
+    assert st.chunks == len(seen)
+    assert np.array_equal(codes, got_c)
+    assert np.array_equal(_bits(a), _bits(got_a))
+    assert np.array_equal(_bits(cost), _bits(got_s))
+
+
+def test_errors_are_reported(ctx):
+    from stlq_amd._lib import StlqError
+
+    X, C = random_problem(60, 10, 8, [4, 4])
+    ctx.set_codebooks(C, [4, 4])
+    with pytest.raises(StlqError, match="H_beam"):
+        ctx.beam_search(np.zeros((10, 8), np.float32), 65, nx2=np.ones(10, np.float32))
+    with pytest.raises(StlqError, match="ils_iters"):
+        ctx.encode(X, EncodeConfig(H_beam=2, icm_iters=0, ils_iters=3))
+    with pytest.raises(StlqError):
+        ctx.set_codebooks(np.zeros((300, 8), np.float32), [300])
