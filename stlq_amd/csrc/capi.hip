@@ -103,7 +103,7 @@ struct stlq_mi355_ctx {
 
     // Work buffers (grown on demand, reused across calls).
     DevBuf X, nx2, xC, codes, a, cost, best, fails, active, changed, mse, gam0, roots, scores;
-    DevBuf st_err[2], st_code[2], st_coef[2], st_R[2], st_root[2], st_curH[2];
+    DevBuf st_rec[2], st_curH[2];
 
     std::vector<TileEvents> tiles;
     std::vector<hipEvent_t> event_pool;
@@ -158,8 +158,7 @@ int ValidateLayers(int d, int m, const int* h_vec, int first_max) {
 
 // Per-vector device bytes of one encode tile.
 int64_t PerVectorBytes(int d, int m, int H, int Hb) {
-    const int64_t state = static_cast<int64_t>(Hb) *
-                          (4 + CodeStride(m) + 4 * m + 4 * TriSize(m) + 4);
+    const int64_t state = static_cast<int64_t>(Hb) * 4 * BeamRecordStride(m);
     return 4LL * d + 4 + 4LL * H + m + 4LL * m + 4 + 4 + 2 + 8 + 2 * (state + 4);
 }
 
@@ -174,11 +173,7 @@ int64_t TileVectors(int64_t n, int d, int m, int H, int Hb) {
 int EnsureState(stlq_mi355_ctx* c, int64_t n, int m, int Hb) {
     const size_t slots = static_cast<size_t>(n) * Hb;
     for (int b = 0; b < 2; ++b) {
-        HIP_TRY(c->st_err[b].Ensure(slots * 4));
-        HIP_TRY(c->st_code[b].Ensure(slots * CodeStride(m)));
-        HIP_TRY(c->st_coef[b].Ensure(slots * 4 * m));
-        HIP_TRY(c->st_R[b].Ensure(slots * 4 * TriSize(m)));
-        HIP_TRY(c->st_root[b].Ensure(slots * 4));
+        HIP_TRY(c->st_rec[b].Ensure(slots * 4 * BeamRecordStride(m)));
         HIP_TRY(c->st_curH[b].Ensure(static_cast<size_t>(n) * 4));
     }
     return STLQ_MI355_OK;
@@ -186,11 +181,7 @@ int EnsureState(stlq_mi355_ctx* c, int64_t n, int m, int Hb) {
 
 BeamState StateOf(stlq_mi355_ctx* c, int b) {
     BeamState s;
-    s.err = c->st_err[b].as<float>();
-    s.code = c->st_code[b].as<uint8_t>();
-    s.coef = c->st_coef[b].as<float>();
-    s.R = c->st_R[b].as<float>();
-    s.root = c->st_root[b].as<uint32_t>();
+    s.rec = c->st_rec[b].as<float>();
     s.curH = c->st_curH[b].as<int>();
     return s;
 }
@@ -420,11 +411,7 @@ int stlq_mi355_ctx_destroy(stlq_mi355_ctx* c) {
     if (c->g_shared) c->G_cm.p = nullptr;
     for (DevBuf* b : bufs) b->Release();
     for (int b = 0; b < 2; ++b) {
-        c->st_err[b].Release();
-        c->st_code[b].Release();
-        c->st_coef[b].Release();
-        c->st_R[b].Release();
-        c->st_root[b].Release();
+        c->st_rec[b].Release();
         c->st_curH[b].Release();
     }
     for (hipEvent_t e : c->event_pool) (void)hipEventDestroy(e);

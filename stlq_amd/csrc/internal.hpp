@@ -19,15 +19,14 @@ __host__ __device__ inline int TriIdx(int m, int r, int c) { return r * m - (r *
 __host__ __device__ inline int TriSize(int m) { return m * (m + 1) / 2; }
 __host__ __device__ inline int CodeStride(int m) { return (m + 3) & ~3; }
 
-// Beam state of one tile of vectors, slot-major (vector i, slot s at i*Hb + s).
+// Beam state of one tile of vectors, slot-major (vector i, slot s at i*Hb + s). Each slot is
+// one record of BeamRecordStride(m) dwords: [err, coef[m], packed R (TriSize(m)),
+// codes (CodeStride(m) bytes), root id, padding to 16 bytes].
 struct BeamState {
-    float* err = nullptr;        // [n*Hb]
-    uint8_t* code = nullptr;     // [n*Hb*CodeStride(m)]
-    float* coef = nullptr;       // [n*Hb*m]
-    float* R = nullptr;          // [n*Hb*TriSize(m)]
-    uint32_t* root = nullptr;    // [n*Hb] (large-root only)
+    float* rec = nullptr;        // [n*Hb*BeamRecordStride(m)]
     int* curH = nullptr;         // [n]
 };
+int BeamRecordStride(int m);
 
 // Gram access for the prefix-LS cross terms. A_t(k) of a beam with prefix codes code_t is
 // row[(off_t + code_t) * ld + offL + k] of a row-major matrix whose element (r, c) is the

@@ -2,15 +2,24 @@
 // for the full precomp, :728-992 for the large-root expansion).
 //
 // Mapping: one wave64 owns one vector. For every live beam (slot order) the 64 lanes evaluate
-// the layer's codewords k = lane + 64*j with the reference's exact arithmetic (no FMA
-// contraction, IEEE division, same operation order), so every candidate error is bit-identical
-// to the CPU encoder's given the same xC, G and ||x||^2. The reference keeps the beam with a
-// streaming "replace the first worst slot" rule (beam_search.cpp:101-113, :320-333); lanes
-// 0..H_beam-1 hold those slots and the wave replays the rule in scan order: a ballot finds the
-// next candidate that beats the current worst, it is written into the worst slot, and the worst
-// is recomputed with a DPP max reduction. The surviving candidates are then re-evaluated once
-// (same arithmetic, so same bits) to build the next layer's codes, LS coefficients and
-// Cholesky factor.
+// the layer's codewords k = lane + 64*j with the reference's arithmetic (no FMA contraction, same
+// operation order, IEEE-exact quotients), so every candidate error is bit-identical to the CPU
+// encoder's given the same xC, G and ||x||^2. The beam's prefix state (error, LS coefficients,
+// packed Cholesky factor, codes) is one contiguous record, read with scalar loads because it is
+// wave-uniform. The reference keeps the beam with a streaming "replace the first worst slot"
+// rule (beam_search.cpp:101-113, :320-333); lanes 0..H_beam-1 hold those slots and the wave
+// replays the rule in scan order: a ballot finds the next candidate that beats the current
+// worst, it is written into the worst slot, and the worst is recomputed with DPP max
+// reductions. The surviving candidates are then re-evaluated once (same arithmetic, same bits)
+// to build the next layer's records.
+//
+// Quotients by the Cholesky diagonal. Within one beam every forward/backward step divides by
+// the same R(i,i), so y = RN(1/R(i,i)) is computed once with an IEEE division and each quotient
+// s/R(i,i) is formed as q0 = s*y, r = fma(R(i,i), q0, -s), q = fma(-r, y, q0). With y the
+// correctly rounded reciprocal this correction returns the correctly rounded quotient
+// (Markstein's theorem) as long as nothing over- or underflows; the kernel takes it only when
+// R(i,i) lies in [2^-20, 2^20] and every numerator magnitude in [2^-100, 2^100], and otherwise
+// re-evaluates the chunk with IEEE division. tests/division_check.c verifies the identity.
 #include "internal.hpp"
 
 namespace stlq_mi355 {
@@ -22,34 +31,46 @@ constexpr int kMaxChunks = kMaxK / kWave;  // 4 chunks of 64 codewords
 __device__ __forceinline__ float ReadLane(float v, int l) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
 }
-__device__ __forceinline__ int ReadLaneI(int v, int l) { return __builtin_amdgcn_readlane(v, l); }
 
 template <int CTRL>
 __device__ __forceinline__ float Dpp(float v) {
     return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, 0xF, 0xF, false));
 }
 
-// Max over the 64 lanes, returned wave-uniform. quad_perm(1,0,3,2), quad_perm(2,3,0,1),
-// row_half_mirror, row_mirror reduce each 16-lane row; the four row results are combined.
-__device__ __forceinline__ float WaveMax(float v) {
+// Max over a 16-lane row, broadcast to every lane of the row: quad_perm(1,0,3,2),
+// quad_perm(2,3,0,1), row_half_mirror, row_mirror.
+__device__ __forceinline__ float RowMax(float v) {
     v = fmaxf(v, Dpp<0xB1>(v));
     v = fmaxf(v, Dpp<0x4E>(v));
     v = fmaxf(v, Dpp<0x141>(v));
-    v = fmaxf(v, Dpp<0x140>(v));
-    return fmaxf(fmaxf(ReadLane(v, 0), ReadLane(v, 16)), fmaxf(ReadLane(v, 32), ReadLane(v, 48)));
+    return fmaxf(v, Dpp<0x140>(v));
 }
-__device__ __forceinline__ float WaveMin(float v) {
+__device__ __forceinline__ float RowMin(float v) {
     v = fminf(v, Dpp<0xB1>(v));
     v = fminf(v, Dpp<0x4E>(v));
     v = fminf(v, Dpp<0x141>(v));
-    v = fminf(v, Dpp<0x140>(v));
-    return fminf(fminf(ReadLane(v, 0), ReadLane(v, 16)), fminf(ReadLane(v, 32), ReadLane(v, 48)));
+    return fminf(v, Dpp<0x140>(v));
+}
+// Wave-uniform max/min over the first `rows` 16-lane rows.
+__device__ __forceinline__ float SlotMax(float v, int rows) {
+    v = RowMax(v);
+    float r = ReadLane(v, 0);
+    if (rows > 1) r = fmaxf(r, ReadLane(v, 16));
+    if (rows > 2) r = fmaxf(fmaxf(r, ReadLane(v, 32)), ReadLane(v, 48));
+    return r;
+}
+__device__ __forceinline__ float SlotMin(float v, int rows) {
+    v = RowMin(v);
+    float r = ReadLane(v, 0);
+    if (rows > 1) r = fminf(r, ReadLane(v, 16));
+    if (rows > 2) r = fminf(fminf(r, ReadLane(v, 32)), ReadLane(v, 48));
+    return r;
 }
 
 // RecomputeWorst (beam_search.cpp:101-113): scan from slot 0 keeping the first slot whose error
 // is strictly greater. Comparisons with NaN are false, so a NaN in slot 0 pins the worst to
 // (NaN, 0) and a NaN elsewhere is never chosen.
-__device__ __forceinline__ void RecomputeWorst(float s_err, int Hb, int lane, float& worst, int& widx) {
+__device__ __forceinline__ void RecomputeWorst(float s_err, int Hb, int rows, int lane, float& worst, int& widx) {
     const float e0 = ReadLane(s_err, 0);
     if (__builtin_isnan(e0)) {
         worst = e0;
@@ -58,7 +79,7 @@ __device__ __forceinline__ void RecomputeWorst(float s_err, int Hb, int lane, fl
     }
     const bool in = lane < Hb;
     const float v = (in && !__builtin_isnan(s_err)) ? s_err : -kInfF;
-    const float mx = WaveMax(v);
+    const float mx = SlotMax(v, rows);
     const uint64_t eq = __ballot(in && s_err == mx);
     widx = static_cast<int>(__builtin_ctzll(eq));
     worst = mx;
@@ -67,7 +88,7 @@ __device__ __forceinline__ void RecomputeWorst(float s_err, int Hb, int lane, fl
 // Replays the streaming top-H over one chunk of 64 candidates in lane (= scan) order.
 // Candidate `lane` is eligible when ok; it is inserted when !(e >= worst)
 // (beam_search.cpp:320: `if (e >= worst_err) continue;`).
-__device__ __forceinline__ void ReplayChunk(bool ok, float e, int cand_base, int Hb, int lane,
+__device__ __forceinline__ void ReplayChunk(bool ok, float e, int cand_base, int Hb, int rows, int lane,
                                             float& s_err, int& s_cand, float& worst, int& widx) {
     uint64_t mask = __ballot(ok && !(e >= worst));
     while (mask) {
@@ -77,7 +98,7 @@ __device__ __forceinline__ void ReplayChunk(bool ok, float e, int cand_base, int
             s_err = ev;
             s_cand = cand_base + l;
         }
-        RecomputeWorst(s_err, Hb, lane, worst, widx);
+        RecomputeWorst(s_err, Hb, rows, lane, worst, widx);
         const uint64_t later = (l >= 63) ? 0ull : (~0ull << (l + 1));
         mask = __ballot(ok && !(e >= worst)) & later;
     }
@@ -90,33 +111,67 @@ __device__ __forceinline__ int BestSlot(float err, int curH, int lane) {
     if (__builtin_isnan(e0)) return 0;
     const bool in = lane < curH;
     const float v = (in && !__builtin_isnan(err)) ? err : kInfF;
-    const float mn = WaveMin(v);
+    const float mn = SlotMin(v, (curH + 15) >> 4);
     const uint64_t eq = __ballot(in && err == mn);
     return eq ? static_cast<int>(__builtin_ctzll(eq)) : 0;
 }
+
+// Record layout of one beam slot (dword offsets); RecStride(m) dwords per slot.
+struct Rec {
+    int coef, R, code, root, stride;
+    __host__ __device__ explicit Rec(int m) {
+        coef = 1;
+        R = 1 + m;
+        code = R + TriSize(m);
+        root = code + CodeStride(m) / 4;
+        stride = (root + 1 + 3) & ~3;
+    }
+};
+
+__device__ __forceinline__ int CodeAt(const float* rec, int code_off, int t) {
+    const uint32_t w = reinterpret_cast<const uint32_t*>(rec + code_off)[t >> 2];
+    return static_cast<int>((w >> (8 * (t & 3))) & 0xFFu);
+}
+
+// Quotient s/d given y = RN(1/d): exact when `safe` (see the file comment).
+__device__ __forceinline__ float QuotFast(float s, float d, float y, bool& safe) {
+    const float q0 = s * y;
+    const float r = __builtin_fmaf(d, q0, -s);
+    const float q = __builtin_fmaf(-r, y, q0);
+    const float as = __builtin_fabsf(s);
+    safe = safe && (as >= 0x1p-100f) && (as <= 0x1p100f);
+    return q;
+}
+
+__device__ __forceinline__ bool DiagFastOk(float d) { return d >= 0x1p-20f && d <= 0x1p20f; }
 
 // One prefix-LS candidate (beam_search.cpp:291-318): forward U^T y = A, backward U v = y
 // (linear_algebra.cpp:57-77; the large-root expansion multiplies by 1/diag instead,
 // beam_search.cpp:544-547/569-572), delta = A.v, eta = A.a_old, then
 // a_last = (gamma - eta)/(alpha - delta), e = max(E_old - diff*a_last, 0).
-template <int L, bool RECIP, typename RFn, typename RinvFn>
-__device__ __forceinline__ void EvalCand(RFn R, RinvFn rinv, const float (&A)[L], const float (&aold)[L],
-                                         float E_old, float alpha, float gamma, float (&y)[L],
-                                         float (&v)[L], float& e, float& denom, float& a_last,
-                                         bool& ok) {
+// MODE 0: IEEE division; 1: Markstein quotient with reciprocal table `rinv` (sets `safe`);
+// 2: reciprocal multiply (large-root semantics).
+template <int L, int MODE, typename RFn>
+__device__ __forceinline__ void EvalCand(RFn R, const float (&rinv)[L], const float (&A)[L], const float (&aold)[L],
+                                         float E_old, float alpha, float gamma, float (&y)[L], float (&v)[L],
+                                         float& e, float& denom, float& a_last, bool& ok, bool& safe) {
 #pragma unroll
     for (int r = 0; r < L; ++r) {
         float s = A[r];
 #pragma unroll
         for (int j = 0; j < r; ++j) s = s - R(j, r) * y[j];
-        y[r] = RECIP ? s * rinv(r) : s / R(r, r);
+        if (MODE == 0) y[r] = s / R(r, r);
+        else if (MODE == 1) y[r] = QuotFast(s, R(r, r), rinv[r], safe);
+        else y[r] = s * rinv[r];
     }
 #pragma unroll
     for (int r = L - 1; r >= 0; --r) {
         float s = y[r];
 #pragma unroll
         for (int j = r + 1; j < L; ++j) s = s - R(r, j) * v[j];
-        v[r] = RECIP ? s * rinv(r) : s / R(r, r);
+        if (MODE == 0) v[r] = s / R(r, r);
+        else if (MODE == 1) v[r] = QuotFast(s, R(r, r), rinv[r], safe);
+        else v[r] = s * rinv[r];
     }
     float delta = 0.0f, eta = 0.0f;
 #pragma unroll
@@ -139,7 +194,8 @@ __global__ __launch_bounds__(256) void Layer0Kernel(LayerArgs p) {
     const int64_t i = static_cast<int64_t>(blockIdx.x) * kBeamWavesPerBlock + wave;
     if (i >= p.n) return;
     const int m = p.m, Hb = p.Hb, K = p.K, off0 = p.offL;
-    const int TRI = TriSize(m), CS = CodeStride(m);
+    const int rows = (Hb + 15) >> 4;
+    const Rec rc(m);
     const float nx2 = p.nx2[i];
     const float* xCi = p.xC + i * p.ldx;
 
@@ -156,7 +212,7 @@ __global__ __launch_bounds__(256) void Layer0Kernel(LayerArgs p) {
         const float gamma = act ? xCi[off0 + k] : 0.0f;
         const float a1 = gamma / alpha;
         const float e1 = nx2 - gamma * a1;
-        ReplayChunk(ok, e1, kWave * j, Hb, lane, s_err, s_cand, worst, widx);
+        ReplayChunk(ok, e1, kWave * j, Hb, rows, lane, s_err, s_cand, worst, widx);
     }
 
     const int curH = __popcll(__ballot(lane < Hb && s_err < kInfF));  // CountFinite, no max(1,.)
@@ -171,11 +227,12 @@ __global__ __launch_bounds__(256) void Layer0Kernel(LayerArgs p) {
         r00 = sqrtf(alpha);
     }
     if (lane < Hb) {
-        const int64_t so = i * Hb + lane;
-        p.out.err[so] = s_err;
-        p.out.code[so * CS] = c0;
-        p.out.coef[so * m] = a0;
-        p.out.R[so * TRI] = r00;
+        float* rec = p.out.rec + (i * Hb + lane) * rc.stride;
+        rec[0] = s_err;
+        rec[rc.coef] = a0;
+        rec[rc.R] = r00;
+        reinterpret_cast<uint32_t*>(rec + rc.code)[0] = c0;
+        reinterpret_cast<uint32_t*>(rec)[rc.root] = 0u;
     }
     if (lane == 0) p.out.curH[i] = curH;
     if (p.is_last) {
@@ -188,24 +245,28 @@ __global__ __launch_bounds__(256) void Layer0Kernel(LayerArgs p) {
 }
 
 // Layers L >= 1. LR selects the large-root cross-term source and reciprocal solves.
-template <int L, bool LR>
+// FULL: the layer has exactly 256 codewords (no partial chunk).
+template <int L, bool LR, bool FULL>
 __global__ __launch_bounds__(256) void LayerKernel(LayerArgs p) {
-    constexpr bool RECIP = LR;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const int64_t i = static_cast<int64_t>(blockIdx.x) * kBeamWavesPerBlock + wave;
     if (i >= p.n) return;
-    const int m = p.m, Hb = p.Hb, K = p.K, offL = p.offL;
-    const int TRI = TriSize(m), CS = CodeStride(m);
-    const int64_t ld = p.gram.ld;
+    const int m = p.m, Hb = p.Hb, K = FULL ? kMaxK : p.K, offL = p.offL;
+    const int rows = (Hb + 15) >> 4;
+    const Rec rc(m);
+    const int ld = p.gram.ld;
     const float* xCi = p.xC + i * p.ldx;
-    const int nch = (K + kWave - 1) / kWave;
+    const int nch = FULL ? kMaxChunks : (K + kWave - 1) / kWave;
+    const float* __restrict__ recs_in = p.in.rec + i * Hb * rc.stride;
+    float* __restrict__ recs_out = p.out.rec + i * Hb * rc.stride;
+    const float* __restrict__ G = p.gram.G + offL + lane;
 
     float gam[kMaxChunks], alp[kMaxChunks];
 #pragma unroll
     for (int j = 0; j < kMaxChunks; ++j) {
         const int k = lane + kWave * j;
-        const bool act = j < nch && k < K;
+        const bool act = FULL || (j < nch && k < K);
         gam[j] = act ? xCi[offL + k] : 0.0f;
         alp[j] = act ? p.gdiag[offL + k] : 0.0f;
     }
@@ -217,54 +278,78 @@ __global__ __launch_bounds__(256) void LayerKernel(LayerArgs p) {
     const int curH = p.in.curH[i];
 
     for (int h = 0; h < curH; ++h) {
-        const int64_t sb = i * Hb + h;
-        const float E_old = p.in.err[sb];
-        const float* Rp = p.in.R + sb * TRI;
-        const float* ap = p.in.coef + sb * m;
-        const uint8_t* cp = p.in.code + sb * CS;
+        const float* rec = recs_in + h * rc.stride;
+        const float E_old = rec[0];
         float aold[L];
-        const float* rows[L];
-#pragma unroll
-        for (int t = 0; t < L; ++t) {
-            aold[t] = ap[t];
-            if (LR && t == 0) {
-                rows[t] = p.gram.G0S + static_cast<int64_t>(p.in.root[sb]) * ld + offL;
-            } else {
-                rows[t] = p.gram.G + static_cast<int64_t>(p.gram.off[t] + cp[t]) * ld + offL;
-            }
-        }
         float Rv[L][L];
         float Ri[L];
+        const float* rowp[L];
+#pragma unroll
+        for (int t = 0; t < L; ++t) {
+            aold[t] = rec[rc.coef + t];
+            if (LR && t == 0) {
+                const uint32_t root = reinterpret_cast<const uint32_t*>(rec)[rc.root];
+                rowp[t] = p.gram.G0S + static_cast<int64_t>(root) * ld + offL + lane;
+            } else {
+                rowp[t] = G + static_cast<uint32_t>(p.gram.off[t] + CodeAt(rec, rc.code, t)) * static_cast<uint32_t>(ld);
+            }
+        }
+        bool diag_fast = !LR;
 #pragma unroll
         for (int r = 0; r < L; ++r) {
 #pragma unroll
-            for (int c = r; c < L; ++c) Rv[r][c] = Rp[TriIdx(m, r, c)];
-            Ri[r] = RECIP ? 1.0f / Rv[r][r] : 0.0f;
+            for (int c = r; c < L; ++c) Rv[r][c] = rec[rc.R + TriIdx(m, r, c)];
+            Ri[r] = 1.0f / Rv[r][r];
+            diag_fast = diag_fast && DiagFastOk(Rv[r][r]);
         }
         auto Rf = [&](int r, int c) { return Rv[r][c]; };
-        auto Rif = [&](int r) { return Ri[r]; };
+
+        float A[kMaxChunks][L];
+#pragma unroll
+        for (int j = 0; j < kMaxChunks; ++j) {
+#pragma unroll
+            for (int t = 0; t < L; ++t) {
+                const bool act = FULL || (j < nch && lane + kWave * j < K);
+                A[j][t] = act ? rowp[t][kWave * j] : 0.0f;
+            }
+        }
 
         float ech[kMaxChunks];
         bool okc[kMaxChunks];
+        bool safe = true;
 #pragma unroll
         for (int j = 0; j < kMaxChunks; ++j) {
             ech[j] = kInfF;
             okc[j] = false;
-            if (j < nch) {
-                const int k = lane + kWave * j;
-                const bool act = k < K;
-                float A[L];
+            if (!FULL && j >= nch) continue;
+            float y[L], v[L], denom, a_last, e;
+            bool ok;
+            if (LR) {
+                EvalCand<L, 2>(Rf, Ri, A[j], aold, E_old, alp[j], gam[j], y, v, e, denom, a_last, ok, safe);
+            } else if (diag_fast) {
+                EvalCand<L, 1>(Rf, Ri, A[j], aold, E_old, alp[j], gam[j], y, v, e, denom, a_last, ok, safe);
+            } else {
+                EvalCand<L, 0>(Rf, Ri, A[j], aold, E_old, alp[j], gam[j], y, v, e, denom, a_last, ok, safe);
+            }
+            ech[j] = e;
+            okc[j] = ok && (FULL || (j < nch && lane + kWave * j < K));
+        }
+        if (!LR && diag_fast && __ballot(!safe) != 0ull) {
+            // A numerator left the range where the reciprocal-corrected quotient is exact:
+            // re-evaluate this beam's chunks with IEEE division (rare).
 #pragma unroll
-                for (int t = 0; t < L; ++t) A[t] = act ? rows[t][k] : 0.0f;
-                float y[L], v[L], denom, a_last;
-                bool ok;
-                EvalCand<L, RECIP>(Rf, Rif, A, aold, E_old, alp[j], gam[j], y, v, ech[j], denom, a_last, ok);
-                okc[j] = act && ok;
+            for (int j = 0; j < kMaxChunks; ++j) {
+                if (!FULL && j >= nch) continue;
+                float y[L], v[L], denom, a_last, e;
+                bool ok, unused = true;
+                EvalCand<L, 0>(Rf, Ri, A[j], aold, E_old, alp[j], gam[j], y, v, e, denom, a_last, ok, unused);
+                ech[j] = e;
+                okc[j] = ok && (FULL || (j < nch && lane + kWave * j < K));
             }
         }
 #pragma unroll
         for (int j = 0; j < kMaxChunks; ++j) {
-            if (j < nch) ReplayChunk(okc[j], ech[j], h * K + kWave * j, Hb, lane, s_err, s_cand, worst, widx);
+            if (FULL || j < nch) ReplayChunk(okc[j], ech[j], h * K + kWave * j, Hb, rows, lane, s_err, s_cand, worst, widx);
         }
     }
 
@@ -280,51 +365,33 @@ __global__ __launch_bounds__(256) void LayerKernel(LayerArgs p) {
         const int nh = min(curH, Hb);
         outH = max(1, nh);
         if (lane < nh) {
-            const int64_t si = i * Hb + lane;
-            const int64_t so = si;
-            out_err = p.in.err[si];
-            const uint8_t* cp = p.in.code + si * CS;
-            const float* ap = p.in.coef + si * m;
-            const float* Rp = p.in.R + si * TRI;
-            uint8_t* co = p.out.code + so * CS;
-            float* ao = p.out.coef + so * m;
-            float* Ro = p.out.R + so * TRI;
+            const float* ri = recs_in + lane * rc.stride;
+            float* ro = recs_out + lane * rc.stride;
+            out_err = ri[0];
 #pragma unroll
             for (int t = 0; t < L; ++t) {
-                ncode[t] = cp[t];
-                co[t] = cp[t];
-                ao[t] = ap[t];
+                ncode[t] = static_cast<uint8_t>(CodeAt(ri, rc.code, t));
+                ro[rc.coef + t] = ri[rc.coef + t];
             }
-            co[L] = 0;
-            ao[L] = 0.0f;
+            ro[rc.coef + L] = 0.0f;
 #pragma unroll
             for (int r = 0; r < L; ++r) {
 #pragma unroll
-                for (int c = r; c < L; ++c) Ro[TriIdx(m, r, c)] = Rp[TriIdx(m, r, c)];
-                Ro[TriIdx(m, r, L)] = 0.0f;
+                for (int c = r; c < L; ++c) ro[rc.R + TriIdx(m, r, c)] = ri[rc.R + TriIdx(m, r, c)];
+                ro[rc.R + TriIdx(m, r, L)] = 0.0f;
             }
-            Ro[TriIdx(m, L, L)] = 0.0f;
-            if (LR) {
-                nroot = p.in.root[si];
-                p.out.root[so] = nroot;
-            }
+            ro[rc.R + TriIdx(m, L, L)] = 0.0f;
+            nroot = reinterpret_cast<const uint32_t*>(ri)[rc.root];
         } else if (nh == 0 && lane == 0) {
             // No beam at all (layer 0 had no finite candidate): the reference's next-buffer slot 0
             // keeps its never-written (zero) state with error +inf.
-            const int64_t so = i * Hb;
-            uint8_t* co = p.out.code + so * CS;
-            float* ao = p.out.coef + so * m;
-            float* Ro = p.out.R + so * TRI;
+            float* ro = recs_out;
 #pragma unroll
-            for (int t = 0; t <= L; ++t) {
-                co[t] = 0;
-                ao[t] = 0.0f;
-            }
+            for (int t = 0; t <= L; ++t) ro[rc.coef + t] = 0.0f;
 #pragma unroll
             for (int r = 0; r <= L; ++r)
 #pragma unroll
-                for (int c = r; c <= L; ++c) Ro[TriIdx(m, r, c)] = 0.0f;
-            if (LR) p.out.root[so] = 0;
+                for (int c = r; c <= L; ++c) ro[rc.R + TriIdx(m, r, c)] = 0.0f;
         }
     } else {
         outH = max(1, newH);
@@ -332,57 +399,67 @@ __global__ __launch_bounds__(256) void LayerKernel(LayerArgs p) {
         if (live) {
             const int src = s_cand / K;
             const int k = s_cand - src * K;
-            const int64_t si = i * Hb + src;
-            const int64_t so = i * Hb + lane;
-            const float* Rp = p.in.R + si * TRI;
-            const float* ap = p.in.coef + si * m;
-            const uint8_t* cp = p.in.code + si * CS;
+            const float* ri = recs_in + src * rc.stride;
+            float* ro = recs_out + lane * rc.stride;
             float Rv[L][L], Ri[L], aold[L], A[L];
-            if (LR) nroot = p.in.root[si];
+            nroot = reinterpret_cast<const uint32_t*>(ri)[rc.root];
 #pragma unroll
             for (int r = 0; r < L; ++r) {
 #pragma unroll
-                for (int c = r; c < L; ++c) Rv[r][c] = Rp[TriIdx(m, r, c)];
-                Ri[r] = RECIP ? 1.0f / Rv[r][r] : 0.0f;
+                for (int c = r; c < L; ++c) Rv[r][c] = ri[rc.R + TriIdx(m, r, c)];
+                Ri[r] = 1.0f / Rv[r][r];
             }
 #pragma unroll
             for (int t = 0; t < L; ++t) {
-                aold[t] = ap[t];
-                ncode[t] = cp[t];
+                aold[t] = ri[rc.coef + t];
+                const int ct = CodeAt(ri, rc.code, t);
+                ncode[t] = static_cast<uint8_t>(ct);
                 const float* row = (LR && t == 0)
                                        ? p.gram.G0S + static_cast<int64_t>(nroot) * ld + offL
-                                       : p.gram.G + static_cast<int64_t>(p.gram.off[t] + cp[t]) * ld + offL;
+                                       : p.gram.G + static_cast<int64_t>(p.gram.off[t] + ct) * ld + offL;
                 A[t] = row[k];
             }
             ncode[L] = static_cast<uint8_t>(k);
             auto Rf = [&](int r, int c) { return Rv[r][c]; };
-            auto Rif = [&](int r) { return Ri[r]; };
             float y[L], v[L], e, denom, a_last;
-            bool ok;
-            EvalCand<L, RECIP>(Rf, Rif, A, aold, p.in.err[si], p.gdiag[offL + k], xCi[offL + k], y, v, e,
-                               denom, a_last, ok);
-            out_err = s_err;
-            uint8_t* co = p.out.code + so * CS;
-            float* ao = p.out.coef + so * m;
-            float* Ro = p.out.R + so * TRI;
-#pragma unroll
-            for (int t = 0; t < L; ++t) {
-                co[t] = ncode[t];
-                ao[t] = aold[t] - v[t] * a_last;
+            bool ok, unused = true;
+            // IEEE division here: it is the quotient the fast path reproduces when it is taken.
+            if (LR) {
+                EvalCand<L, 2>(Rf, Ri, A, aold, ri[0], p.gdiag[offL + k], xCi[offL + k], y, v, e, denom, a_last, ok,
+                               unused);
+            } else {
+                EvalCand<L, 0>(Rf, Ri, A, aold, ri[0], p.gdiag[offL + k], xCi[offL + k], y, v, e, denom, a_last, ok,
+                               unused);
             }
-            co[L] = ncode[L];
-            ao[L] = a_last;
+            out_err = s_err;
+#pragma unroll
+            for (int t = 0; t < L; ++t) ro[rc.coef + t] = aold[t] - v[t] * a_last;
+            ro[rc.coef + L] = a_last;
 #pragma unroll
             for (int r = 0; r < L; ++r) {
 #pragma unroll
-                for (int c = r; c < L; ++c) Ro[TriIdx(m, r, c)] = Rv[r][c];
-                Ro[TriIdx(m, r, L)] = y[r];
+                for (int c = r; c < L; ++c) ro[rc.R + TriIdx(m, r, c)] = Rv[r][c];
+                ro[rc.R + TriIdx(m, r, L)] = y[r];
             }
-            Ro[TriIdx(m, L, L)] = sqrtf(denom);
-            if (LR) p.out.root[so] = nroot;
+            ro[rc.R + TriIdx(m, L, L)] = sqrtf(denom);
         }
     }
-    if (lane < Hb) p.out.err[i * Hb + lane] = out_err;
+    if (lane < Hb) {
+        float* ro = recs_out + lane * rc.stride;
+        ro[0] = out_err;
+        uint32_t* cw = reinterpret_cast<uint32_t*>(ro + rc.code);
+#pragma unroll
+        for (int w = 0; w <= L / 4; ++w) {
+            uint32_t word = 0;
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                const int t = 4 * w + b;
+                if (t <= L) word |= static_cast<uint32_t>(ncode[t]) << (8 * b);
+            }
+            cw[w] = word;
+        }
+        reinterpret_cast<uint32_t*>(ro)[rc.root] = nroot;
+    }
     if (lane == 0) p.out.curH[i] = outH;
 
     if (p.is_last) {
@@ -404,15 +481,21 @@ __global__ __launch_bounds__(256) void LayerKernel(LayerArgs p) {
 template <int L>
 hipError_t LaunchL(bool lr, const LayerArgs& a, hipStream_t s) {
     const unsigned blocks = static_cast<unsigned>((a.n + kBeamWavesPerBlock - 1) / kBeamWavesPerBlock);
+    const dim3 block(kWave * kBeamWavesPerBlock);
+    const bool full = a.K == kMaxK;
     if (lr) {
-        hipLaunchKernelGGL((LayerKernel<L, true>), dim3(blocks), dim3(kWave * kBeamWavesPerBlock), 0, s, a);
+        if (full) hipLaunchKernelGGL((LayerKernel<L, true, true>), dim3(blocks), block, 0, s, a);
+        else hipLaunchKernelGGL((LayerKernel<L, true, false>), dim3(blocks), block, 0, s, a);
     } else {
-        hipLaunchKernelGGL((LayerKernel<L, false>), dim3(blocks), dim3(kWave * kBeamWavesPerBlock), 0, s, a);
+        if (full) hipLaunchKernelGGL((LayerKernel<L, false, true>), dim3(blocks), block, 0, s, a);
+        else hipLaunchKernelGGL((LayerKernel<L, false, false>), dim3(blocks), block, 0, s, a);
     }
     return hipGetLastError();
 }
 
 }  // namespace
+
+int BeamRecordStride(int m) { return Rec(m).stride; }
 
 hipError_t LaunchBeamLayer0(const LayerArgs& a, hipStream_t s) {
     if (a.n <= 0) return hipSuccess;
