@@ -957,17 +957,118 @@ int stlq_mi355_beam_search_large_root(stlq_mi355_ctx* c, const float* X, const f
                                       int H_beam, const uint32_t* forced_root, int root_mode, uint32_t* cluster_id,
                                       uint8_t* B_small, float* best_err) {
     RC_TRY(CheckCtx(c));
-    if (!c->has_lr) return Fail(STLQ_MI355_ERR_STATE, "large-root codebooks not set");
-    (void)X;
-    (void)xC_small;
-    (void)n;
-    (void)H_beam;
-    (void)forced_root;
-    (void)root_mode;
-    (void)cluster_id;
-    (void)B_small;
-    (void)best_err;
-    return Fail(STLQ_MI355_ERR_UNSUPPORTED, "large-root beam search is not available yet");
+    if (!c->has_lr) return Fail(STLQ_MI355_ERR_STATE, "large-root codebooks not set (call stlq_mi355_set_large_root)");
+    const int Hb = std::max(1, H_beam);
+    RC_TRY(CheckBeam(Hb));
+    if (root_mode != 0 && root_mode != 1) return Fail(STLQ_MI355_ERR_INVALID, "root_mode must be 0 or 1");
+    const int m = c->lr_m, Hs = c->Hs, h0 = c->h0, d = c->lr_d;
+    if (n < 0 || (n > 0 && (!X || !cluster_id || (m > 1 && !B_small))))
+        return Fail(STLQ_MI355_ERR_INVALID, "bad arguments");
+    if (n == 0) return STLQ_MI355_OK;
+    if (forced_root) {
+        for (int64_t i = 0; i < n; ++i)
+            if (forced_root[i] >= static_cast<uint32_t>(h0))
+                return Fail(STLQ_MI355_ERR_INVALID, "forced root " + std::to_string(forced_root[i]) + " of vector " +
+                                                        std::to_string(i) + " >= h0");
+    }
+    c->ResetTimings();
+    const bool need_scores = forced_root == nullptr;
+    const int stride = BeamRecordStride(m);
+    const int64_t per = 4LL * d + 4 + 4LL * std::max(Hs, 1) + (need_scores ? 4LL * h0 : 8) +
+                        2 * (4LL * Hb * stride + 4) + m + 12;
+    int64_t tile = std::max<int64_t>(EnvWorkspaceBytes() / per, 1024);
+    tile = std::min<int64_t>(tile, n);
+    HIP_TRY(c->X.Ensure(static_cast<size_t>(tile) * d * 4));
+    HIP_TRY(c->nx2.Ensure(static_cast<size_t>(tile) * 4));
+    HIP_TRY(c->xC.Ensure(static_cast<size_t>(tile) * std::max(Hs, 1) * 4));
+    HIP_TRY(c->scores.Ensure(static_cast<size_t>(tile) * (need_scores ? h0 : 1) * 4));
+    HIP_TRY(c->roots.Ensure(static_cast<size_t>(tile) * 4 * 2));
+    HIP_TRY(c->codes.Ensure(static_cast<size_t>(tile) * std::max(m - 1, 1)));
+    HIP_TRY(c->best.Ensure(static_cast<size_t>(tile) * 4));
+    RC_TRY(EnsureState(c, tile, m, Hb));
+    uint32_t* d_roots = c->roots.as<uint32_t>();
+    uint32_t* d_cluster = d_roots + tile;
+    for (int64_t t0 = 0; t0 < n; t0 += tile) {
+        const int64_t nt = std::min(tile, n - t0);
+        hipStream_t s = c->stream;
+        HIP_TRY(hipMemcpyAsync(c->X.p, X + t0 * d, static_cast<size_t>(nt) * d * 4, hipMemcpyHostToDevice, s));
+        HIP_TRY(LaunchXNorm2(c->X.as<float>(), d, nt, c->nx2.as<float>(), s));
+        if (Hs > 0) {
+            if (xC_small) {
+                HIP_TRY(hipMemcpyAsync(c->xC.p, xC_small + t0 * Hs, static_cast<size_t>(nt) * Hs * 4,
+                                       hipMemcpyHostToDevice, s));
+            } else {
+                HIP_TRY(LaunchGemmXc(c->X.as<float>(), nt, d, c->Cs.as<float>(), Hs, c->xC.as<float>(), Hs, s));
+            }
+        }
+        TileEvents te;
+        te.n = nt;
+        te.e[0] = te.e[1] = te.e[2] = c->NextEvent();
+        HIP_TRY(hipEventRecord(te.e[0], s));
+        RootArgs ra;
+        ra.nx2 = c->nx2.as<float>();
+        ra.norm0 = c->norm0.as<float>();
+        ra.out = StateOf(c, 0);
+        ra.n = nt;
+        ra.m = m;
+        ra.Hb = Hb;
+        ra.h0 = h0;
+        ra.is_last = (m == 1);
+        ra.cluster_out = d_cluster;
+        ra.best_err = c->best.as<float>();
+        if (forced_root) {
+            HIP_TRY(hipMemcpyAsync(d_roots, forced_root + t0, static_cast<size_t>(nt) * 4, hipMemcpyHostToDevice, s));
+            HIP_TRY(LaunchGatherRootDot(c->X.as<float>(), d, c->C0.as<float>(), d_roots, nt, c->scores.as<float>(), s));
+            ra.scores = c->scores.as<float>();
+            ra.ldx = 1;
+            ra.forced = d_roots;
+            ra.root_slots = 1;
+        } else {
+            HIP_TRY(LaunchGemmXc(c->X.as<float>(), nt, d, c->C0.as<float>(), h0, c->scores.as<float>(), h0, s));
+            te.gemm_launches = 1;
+            ra.scores = c->scores.as<float>();
+            ra.ldx = h0;
+            ra.root_slots = root_mode == 1 ? 1 : Hb;
+        }
+        HIP_TRY(LaunchRootSeed(ra, s));
+        LayerArgs a;
+        a.gram.G = c->G_small.as<float>();
+        a.gram.ld = Hs;
+        a.gram.G0S = c->G0S.as<float>();
+        for (int l = 0; l < m; ++l) a.gram.off[l] = c->soff[l];
+        a.xC = c->xC.as<float>();
+        a.ldx = Hs;
+        a.nx2 = c->nx2.as<float>();
+        a.gdiag = c->gdiag_small.as<float>();
+        a.n = nt;
+        a.m = m;
+        a.Hb = Hb;
+        a.codes_out = c->codes.as<uint8_t>();
+        a.cluster_out = d_cluster;
+        a.best_err = c->best.as<float>();
+        int cur = 0;
+        for (int L = 1; L < m; ++L) {
+            a.in = StateOf(c, cur);
+            a.out = StateOf(c, cur ^ 1);
+            a.K = c->lr_h[L];
+            a.offL = c->soff[L];
+            a.is_last = (L == m - 1);
+            HIP_TRY(LaunchBeamLayer(L, true, a, s));
+            cur ^= 1;
+            ++te.beam_launches;
+        }
+        te.e[3] = te.e[4] = te.e[5] = te.e[6] = c->NextEvent();
+        HIP_TRY(hipEventRecord(te.e[3], s));
+        c->tiles.push_back(te);
+        HIP_TRY(hipMemcpyAsync(cluster_id + t0, d_cluster, static_cast<size_t>(nt) * 4, hipMemcpyDeviceToHost, s));
+        if (m > 1)
+            HIP_TRY(hipMemcpyAsync(B_small + t0 * (m - 1), c->codes.p, static_cast<size_t>(nt) * (m - 1),
+                                   hipMemcpyDeviceToHost, s));
+        if (best_err)
+            HIP_TRY(hipMemcpyAsync(best_err + t0, c->best.p, static_cast<size_t>(nt) * 4, hipMemcpyDeviceToHost, s));
+        HIP_TRY(hipStreamSynchronize(s));
+    }
+    return STLQ_MI355_OK;
 }
 
 }  // extern "C"

@@ -83,6 +83,8 @@ hipError_t LaunchGemmXc(const float* X, int64_t n, int d, const float* C, int H,
 hipError_t LaunchBeamLayer0(const LayerArgs& a, hipStream_t s);
 hipError_t LaunchBeamLayer(int L, bool large_root, const LayerArgs& a, hipStream_t s);
 hipError_t LaunchRootSeed(const RootArgs& a, hipStream_t s);
+hipError_t LaunchGatherRootDot(const float* X, int d, const float* C0, const uint32_t* roots, int64_t n, float* out,
+                               hipStream_t s);
 
 struct LsArgs {
     const float* xC = nullptr;

@@ -478,6 +478,94 @@ __global__ __launch_bounds__(256) void LayerKernel(LayerArgs p) {
     }
 }
 
+// Root candidates of the large-root beam (beam_search.cpp:639-709) seeded into beam records the
+// way BeamSearchPrefixLSLargeRootExpandFromRootCandidates does (:760-793).
+//  forced != null: the vector's root is given; its gamma is p.scores[i] (a 1-wide score row).
+//  otherwise: streaming top-`root_slots` over ascending root codes of the score row
+//  (root_slots == 1 forces the nearest root).
+// e1 = ||x||^2 - gamma*(gamma/alpha), alpha = ||c0||^2, alpha == 0 skipped. A slot is seeded when
+// its error is not +inf (NaN is seeded, as `errs0[h] >= inf` is false for NaN); curH = max(1, #seeded).
+__global__ __launch_bounds__(256) void RootSeedKernel(RootArgs p) {
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * kBeamWavesPerBlock + wave;
+    if (i >= p.n) return;
+    const int m = p.m, Hb = p.Hb, rs = p.root_slots;
+    const int rows = (rs + 15) >> 4;
+    const Rec rc(m);
+    const float nx2 = p.nx2[i];
+    float s_err = kInfF;
+    int s_cand = -1;
+    if (p.forced) {
+        if (lane == 0) {
+            const int code = static_cast<int>(p.forced[i]);
+            const float alpha = p.norm0[code];
+            if (alpha != 0.0f) {
+                const float gamma = p.scores[i * p.ldx];
+                const float a1 = gamma / alpha;
+                s_err = nx2 - gamma * a1;
+                s_cand = code;
+            }
+        }
+    } else {
+        float worst = kInfF;
+        int widx = 0;
+        const float* sc = p.scores + i * p.ldx;
+        for (int c0 = 0; c0 < p.h0; c0 += kWave) {
+            const int code = c0 + lane;
+            const bool act = code < p.h0;
+            const float alpha = act ? p.norm0[code] : 0.0f;
+            const bool ok = act && alpha != 0.0f;
+            const float gamma = act ? sc[code] : 0.0f;
+            const float a1 = gamma / alpha;
+            const float e1 = nx2 - gamma * a1;
+            ReplayChunk(ok, e1, c0, rs, rows, lane, s_err, s_cand, worst, widx);
+        }
+    }
+    const bool seeded = lane < rs && !(s_err >= kInfF);
+    const int curH = max(1, __popcll(__ballot(seeded)));
+    float a0 = 0.0f, r00 = 0.0f;
+    uint32_t root = 0;
+    if (seeded) {
+        root = static_cast<uint32_t>(s_cand);
+        const float alpha = p.norm0[s_cand];
+        const float gamma = p.forced ? p.scores[i * p.ldx] : p.scores[i * p.ldx + s_cand];
+        a0 = gamma / alpha;
+        r00 = sqrtf(alpha);
+    }
+    if (lane < Hb) {
+        float* rec = p.out.rec + (i * Hb + lane) * rc.stride;
+        rec[0] = seeded ? s_err : kInfF;
+        rec[rc.coef] = a0;
+        rec[rc.R] = r00;
+        reinterpret_cast<uint32_t*>(rec + rc.code)[0] = 0u;
+        reinterpret_cast<uint32_t*>(rec)[rc.root] = root;
+    }
+    if (lane == 0) p.out.curH[i] = curH;
+    if (p.is_last) {  // m == 1: the root is the whole code
+        const int best = BestSlot(seeded ? s_err : kInfF, curH, lane);
+        if (lane == best) {
+            p.cluster_out[i] = root;
+            if (p.best_err) p.best_err[i] = seeded ? s_err : kInfF;
+        }
+    }
+}
+
+// gamma of a given root per vector: fused k-ordered dot product s = fma(c0[r], x[r], s), the
+// accumulation order of the MFMA score GEMM, so forced and scanned roots see the same gamma.
+__global__ __launch_bounds__(256) void GatherRootDotKernel(const float* __restrict__ X, int d,
+                                                           const float* __restrict__ C0,
+                                                           const uint32_t* __restrict__ roots, int64_t n,
+                                                           float* __restrict__ out) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float* x = X + i * d;
+    const float* c = C0 + static_cast<int64_t>(roots[i]) * d;
+    float s = 0.0f;
+    for (int r = 0; r < d; ++r) s = __builtin_fmaf(c[r], x[r], s);
+    out[i] = s;
+}
+
 template <int L>
 hipError_t LaunchL(bool lr, const LayerArgs& a, hipStream_t s) {
     const unsigned blocks = static_cast<unsigned>((a.n + kBeamWavesPerBlock - 1) / kBeamWavesPerBlock);
@@ -496,6 +584,21 @@ hipError_t LaunchL(bool lr, const LayerArgs& a, hipStream_t s) {
 }  // namespace
 
 int BeamRecordStride(int m) { return Rec(m).stride; }
+
+hipError_t LaunchRootSeed(const RootArgs& a, hipStream_t s) {
+    if (a.n <= 0) return hipSuccess;
+    const unsigned blocks = static_cast<unsigned>((a.n + kBeamWavesPerBlock - 1) / kBeamWavesPerBlock);
+    hipLaunchKernelGGL(RootSeedKernel, dim3(blocks), dim3(kWave * kBeamWavesPerBlock), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t LaunchGatherRootDot(const float* X, int d, const float* C0, const uint32_t* roots, int64_t n, float* out,
+                               hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(GatherRootDotKernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s, X, d, C0,
+                       roots, n, out);
+    return hipGetLastError();
+}
 
 hipError_t LaunchBeamLayer0(const LayerArgs& a, hipStream_t s) {
     if (a.n <= 0) return hipSuccess;

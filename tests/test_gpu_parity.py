@@ -349,3 +349,44 @@ def test_errors_are_reported(ctx):
         ctx.encode(X, EncodeConfig(H_beam=2, icm_iters=0, ils_iters=3))
     with pytest.raises(StlqError):
         ctx.set_codebooks(np.zeros((300, 8), np.float32), [300])
+
+
+LARGE_ROOT_CASES = [
+    # name, seed, n, d, h0, small layers, H_beam, mode ("forced" | "nearest" | "topH")
+    ("lr_topH_small", 70, 600, 24, 300, [64, 64, 64], 8, "topH"),
+    ("lr_nearest", 71, 600, 32, 1000, [128, 128, 128, 128], 16, "nearest"),
+    ("lr_forced", 72, 600, 32, 1000, [256, 256, 256], 32, "forced"),
+    ("lr_c5_shape", 73, 300, 128, 4096, [256] * 6, 32, "nearest"),
+    ("lr_m1", 74, 400, 16, 500, [], 4, "topH"),
+]
+
+
+@pytest.mark.parametrize("name,seed,n,d,h0,small,Hb,mode", LARGE_ROOT_CASES, ids=[c[0] for c in LARGE_ROOT_CASES])
+def test_large_root_bit_exact(ctx, orc, name, seed, n, d, h0, small, Hb, mode):
+    """BeamSearchPrefixLSLargeRoot (beam_search.cpp:579-992): root candidates from the MFMA score
+    GEMM (or a forced root), expansion with reciprocal-scaled solves; cluster ids, small codes
+    and selected errors are identical to the oracle's."""
+    from stlq_amd import workloads
+
+    mix = workloads.Mixture("desc" if d >= 32 else "gauss", d, 256, seed)
+    rng = np.random.default_rng(seed)
+    C0 = mix.sample(5_000_000, h0)
+    Xtr = mix.sample(1_000_000, 3000)
+    Cs = workloads.residual_codebooks(Xtr - C0[rng.integers(0, h0, 3000)], len(small), small[0], 3, seed + 1) \
+        if small else np.zeros((0, d), np.float32)
+    X = mix.sample(0, n)
+    h = [h0] + small
+    ctx.set_large_root(C0, Cs, h)
+    forced = rng.integers(0, h0, n).astype(np.uint32) if mode == "forced" else None
+    root_mode = 1 if mode == "nearest" else 0
+    cid_g, Bs_g, err_g = ctx.beam_search_large_root(X, Hb, forced_root=forced, root_mode=root_mode)
+    norm0, Gs, G0S = orc.build_precomp_large_root(C0, Cs if small else np.zeros((1, d), np.float32))
+    nx2 = orc.xnorm2(X)
+    xs = orc.gemm_xc(Cs, X, mode=1) if small else np.zeros((n, 1), np.float32)
+    cid_o, Bs_o, err_o = orc.beam_search_large_root(X, nx2, C0, norm0, xs, Gs, G0S, h, Hb, forced_root=forced,
+                                                    root_mode=root_mode)
+    assert np.array_equal(cid_o, cid_g), (name, np.nonzero(cid_o != cid_g)[0][:10])
+    assert np.array_equal(Bs_o, Bs_g)
+    assert np.array_equal(_bits(err_o), _bits(err_g))
+    if mode == "forced":
+        assert np.array_equal(cid_g, forced)
