@@ -143,26 +143,51 @@ int stlq_mi355_encode_device(stlq_mi355_ctx* ctx, const float* dX, int64_t n,
                              const stlq_mi355_encode_params* params, uint8_t* dcodes,
                              float* da, float* dcost, void* stream);
 
-/* Streaming encode (EncodeBaseStreamingF32, src/quantizer/encode_base_streaming.cpp:4544-4579,
- * tile loop :2534-2620): vectors are produced by `fill` into pinned host chunks of `chunk`
- * vectors, copied to the device through two buffers on a copy stream (double-buffered
- * hipMemcpyAsync) while the previous chunk encodes, and the codes (plus a and cost when
- * want_coeffs) are handed to `sink` in order. fill/sink return 0 on success. */
-typedef int (*stlq_mi355_fill_fn)(void* user, int64_t first, int64_t count, float* dst);
+/* Streaming encode (EncodeBaseStreaming / EncodeBaseStreamingF32,
+ * src/quantizer/encode_base_streaming.cpp:1913 and :4544-4579, tile loop :2534-2620): vectors
+ * are produced by `fill` into pinned host chunks of `chunk` vectors, copied to the device
+ * through two buffers on a copy stream (double-buffered hipMemcpyAsync) while the previous chunk
+ * encodes on the context stream, and the results are handed to `sink` in chunk order.
+ *  input_u8: fill writes uint8 vectors (d bytes each) that the device widens to fp32
+ *            (ConvertU8ToF32AndRotatePtr with R = I, kernel_provider_cuda_stream_impl.inc:3730+);
+ *            otherwise fp32 (d floats each).
+ *  large_root: encode with the large-root codebooks (stlq_mi355_set_large_root): the beam of
+ *            BeamSearchPrefixLSLargeRoot with root_mode 0 (top-H_beam roots) or 1 (nearest
+ *            root); the chunk output then carries cluster_id, B_small and best_err.
+ *            Otherwise the full-precomp EncodeBase of `encode` (codes, and a/cost when wanted).
+ * fill/sink return 0 on success. */
+typedef struct stlq_mi355_stream_params {
+    stlq_mi355_encode_params encode;
+    int input_u8;
+    int large_root;
+    int root_mode;
+} stlq_mi355_stream_params;
+
+typedef struct stlq_mi355_chunk_out {
+    const uint8_t* codes;       /* full precomp: m x count */
+    const float* a;             /* full precomp with coefficients: m x count, else NULL */
+    const float* cost;          /* full precomp with coefficients: count, else NULL */
+    const uint32_t* cluster_id; /* large root: count */
+    const uint8_t* B_small;     /* large root: (m-1) x count */
+    const float* best_err;      /* large root: count */
+} stlq_mi355_chunk_out;
+
+typedef int (*stlq_mi355_fill_fn)(void* user, int64_t first, int64_t count, void* dst);
 typedef int (*stlq_mi355_sink_fn)(void* user, int64_t first, int64_t count,
-                                  const uint8_t* codes, const float* a, const float* cost);
+                                  const stlq_mi355_chunk_out* out);
 
 typedef struct stlq_mi355_stream_stats {
     double wall_ms;      /* whole call */
     double h2d_ms;       /* sum of H2D copy durations (copy stream) */
-    double compute_ms;   /* sum of encode durations (compute stream) */
+    double compute_ms;   /* sum of chunk encode durations incl. result D2H (context stream) */
     double fill_ms;      /* host time inside fill callbacks */
+    double sink_ms;      /* host time inside sink callbacks */
     double h2d_bytes;
     int64_t chunks;
 } stlq_mi355_stream_stats;
 
 int stlq_mi355_encode_stream(stlq_mi355_ctx* ctx, int64_t n_total, int64_t chunk,
-                             const stlq_mi355_encode_params* params, stlq_mi355_fill_fn fill,
+                             const stlq_mi355_stream_params* params, stlq_mi355_fill_fn fill,
                              stlq_mi355_sink_fn sink, void* user,
                              stlq_mi355_stream_stats* stats);
 

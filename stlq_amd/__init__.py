@@ -17,6 +17,7 @@ from .encoder import (  # noqa: F401
     DynamicIcmWithIlsAbsNoNormal,
     DynamicIcmWithIlsNoAbsNoNormal,
     EncodeBase,
+    EncodeBaseStreaming,
     EncodeBaseStreamingF32,
     EncodeConfig,
     SolveLeastSquaresAll,

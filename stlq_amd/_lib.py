@@ -51,19 +51,40 @@ class Timings(ctypes.Structure):
     ]
 
 
+class StreamParams(ctypes.Structure):
+    _fields_ = [
+        ("encode", EncodeParams),
+        ("input_u8", ctypes.c_int),
+        ("large_root", ctypes.c_int),
+        ("root_mode", ctypes.c_int),
+    ]
+
+
+class ChunkOut(ctypes.Structure):
+    _fields_ = [
+        ("codes", _u8p),
+        ("a", _f32p),
+        ("cost", _f32p),
+        ("cluster_id", _u32p),
+        ("B_small", _u8p),
+        ("best_err", _f32p),
+    ]
+
+
 class StreamStats(ctypes.Structure):
     _fields_ = [
         ("wall_ms", ctypes.c_double),
         ("h2d_ms", ctypes.c_double),
         ("compute_ms", ctypes.c_double),
         ("fill_ms", ctypes.c_double),
+        ("sink_ms", ctypes.c_double),
         ("h2d_bytes", ctypes.c_double),
         ("chunks", ctypes.c_int64),
     ]
 
 
-FILL_FN = ctypes.CFUNCTYPE(ctypes.c_int, _vp, ctypes.c_int64, ctypes.c_int64, _f32p)
-SINK_FN = ctypes.CFUNCTYPE(ctypes.c_int, _vp, ctypes.c_int64, ctypes.c_int64, _u8p, _f32p, _f32p)
+FILL_FN = ctypes.CFUNCTYPE(ctypes.c_int, _vp, ctypes.c_int64, ctypes.c_int64, _vp)
+SINK_FN = ctypes.CFUNCTYPE(ctypes.c_int, _vp, ctypes.c_int64, ctypes.c_int64, ctypes.POINTER(ChunkOut))
 
 # Every symbol the public headers declare, with its (argtypes, restype).
 SIGNATURES = {
@@ -82,7 +103,7 @@ SIGNATURES = {
     "stlq_mi355_icm": ([_vp, _f32p, _f32p, _f32p, _i64, _int, _int, ctypes.c_uint32, _u8p, _f32p, _f32p], _int),
     "stlq_mi355_encode": ([_vp, _f32p, _i64, ctypes.POINTER(EncodeParams), _u8p, _f32p, _f32p, _f64p, _f64p], _int),
     "stlq_mi355_encode_device": ([_vp, _vp, _i64, ctypes.POINTER(EncodeParams), _vp, _vp, _vp, _vp], _int),
-    "stlq_mi355_encode_stream": ([_vp, _i64, _i64, ctypes.POINTER(EncodeParams), FILL_FN, SINK_FN, _vp,
+    "stlq_mi355_encode_stream": ([_vp, _i64, _i64, ctypes.POINTER(StreamParams), FILL_FN, SINK_FN, _vp,
                                   ctypes.POINTER(StreamStats)], _int),
     "stlq_mi355_last_timings": ([_vp, ctypes.POINTER(Timings)], _int),
     "stlq_mi355_set_large_root": ([_vp, _int, _int, _i32p, _f32p, _f32p], _int),

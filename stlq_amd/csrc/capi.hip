@@ -102,7 +102,7 @@ struct stlq_mi355_ctx {
     DevBuf C0, Cs, norm0, G_small, G0S, gdiag_small;
 
     // Work buffers (grown on demand, reused across calls).
-    DevBuf X, nx2, xC, codes, a, cost, best, fails, active, changed, mse, gam0, roots, scores;
+    DevBuf X, nx2, xC, xC_in, codes, a, cost, best, fails, active, changed, mse, gam0, roots, scores;
     DevBuf st_rec[2], st_curH[2];
 
     std::vector<TileEvents> tiles;
@@ -405,7 +405,7 @@ int stlq_mi355_ctx_destroy(stlq_mi355_ctx* c) {
     (void)hipStreamSynchronize(c->stream);
     (void)hipStreamSynchronize(c->copy_stream);
     DevBuf* bufs[] = {&c->C_all, &c->G_rm, &c->G_cm, &c->gdiag, &c->invnorm, &c->C0, &c->Cs, &c->norm0,
-                      &c->G_small, &c->G0S, &c->gdiag_small, &c->X, &c->nx2, &c->xC, &c->codes, &c->a,
+                      &c->G_small, &c->G0S, &c->gdiag_small, &c->X, &c->nx2, &c->xC, &c->xC_in, &c->codes, &c->a,
                       &c->cost, &c->best, &c->fails, &c->active, &c->changed, &c->mse, &c->gam0, &c->roots,
                       &c->scores};
     if (c->g_shared) c->G_cm.p = nullptr;
@@ -773,80 +773,118 @@ int stlq_mi355_last_timings(stlq_mi355_ctx* c, stlq_mi355_timings* out) {
     return STLQ_MI355_OK;
 }
 
+}  // extern "C"
+
+namespace {
+int CheckLargeRoot(stlq_mi355_ctx* c, int H_beam, int root_mode);
+int LargeRootTile(stlq_mi355_ctx* c, const float* dX, int64_t nt, int Hb, int root_mode, const uint32_t* d_forced,
+                  const float* dxC_given, uint32_t* d_cluster, uint8_t* d_codes, float* d_best, hipStream_t s,
+                  TileEvents* te);
+}  // namespace
+
+extern "C" {
+
 // ---------------------------------------------------------------------------------------------
 // Streaming encode: pinned host chunks -> two device buffers on the copy stream, encode on the
-// context stream, pinned outputs handed to the sink in order.
-int stlq_mi355_encode_stream(stlq_mi355_ctx* c, int64_t n_total, int64_t chunk, const stlq_mi355_encode_params* params,
+// context stream, pinned outputs handed to the sink in chunk order.
+int stlq_mi355_encode_stream(stlq_mi355_ctx* c, int64_t n_total, int64_t chunk, const stlq_mi355_stream_params* sp,
                              stlq_mi355_fill_fn fill, stlq_mi355_sink_fn sink, void* user,
                              stlq_mi355_stream_stats* stats) {
-    RC_TRY(CheckPre(c));
-    RC_TRY(CheckParams(params));
+    RC_TRY(CheckCtx(c));
+    if (!sp) return Fail(STLQ_MI355_ERR_INVALID, "params is null");
+    const bool lr = sp->large_root != 0;
+    if (lr) {
+        RC_TRY(CheckLargeRoot(c, sp->encode.H_beam, sp->root_mode));
+    } else {
+        RC_TRY(CheckPre(c));
+        RC_TRY(CheckParams(&sp->encode));
+    }
     if (n_total < 0 || chunk <= 0 || !fill || !sink) return Fail(STLQ_MI355_ERR_INVALID, "bad arguments");
     if (stats) std::memset(stats, 0, sizeof(*stats));
     if (n_total == 0) return STLQ_MI355_OK;
     c->ResetTimings();
     const auto t_begin = std::chrono::steady_clock::now();
-    const size_t m = static_cast<size_t>(c->m);
-    const size_t d = static_cast<size_t>(c->d);
+    const int Hb = std::max(1, sp->encode.H_beam);
+    const size_t m = static_cast<size_t>(lr ? c->lr_m : c->m);
+    const size_t d = static_cast<size_t>(lr ? c->lr_d : c->d);
+    const size_t esz = sp->input_u8 ? 1 : 4;
     chunk = std::min(chunk, n_total);
-    const bool want = params->want_coeffs || params->icm_iters > 0;
+    const size_t ch = static_cast<size_t>(chunk);
+    const bool want = !lr && (sp->encode.want_coeffs || sp->encode.icm_iters > 0);
+    const size_t code_b = lr ? std::max<size_t>(m - 1, 1) : m;
     struct Slot {
-        float* hX = nullptr;
+        void* hin = nullptr;
         uint8_t* hcodes = nullptr;
         float* ha = nullptr;
         float* hcost = nullptr;
-        DevBuf dX, dcodes, da, dcost;
+        uint32_t* hcluster = nullptr;
+        float* hbest = nullptr;
+        DevBuf din, dX, dcodes, da, dcost, dcluster, dbest;
         hipEvent_t copied = nullptr, done = nullptr, c0 = nullptr, c1 = nullptr, k0 = nullptr;
         int64_t first = 0, count = 0;
         bool busy = false;
     } slot[2];
     int rc = STLQ_MI355_OK;
-    auto cleanup = [&]() {
-        (void)hipStreamSynchronize(c->copy_stream);
-        (void)hipStreamSynchronize(c->stream);
-        for (Slot& s : slot) {
-            if (s.hX) (void)hipHostFree(s.hX);
-            if (s.hcodes) (void)hipHostFree(s.hcodes);
-            if (s.ha) (void)hipHostFree(s.ha);
-            if (s.hcost) (void)hipHostFree(s.hcost);
-            s.dX.Release();
-            s.dcodes.Release();
-            s.da.Release();
-            s.dcost.Release();
-            for (hipEvent_t e : {s.copied, s.done, s.c0, s.c1, s.k0})
-                if (e) (void)hipEventDestroy(e);
-        }
-    };
     auto hip_ok = [&](hipError_t e, const char* what) {
         if (e == hipSuccess) return true;
         rc = Fail(STLQ_MI355_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
         return false;
     };
-    for (Slot& s : slot) {
-        if (!hip_ok(hipHostMalloc(reinterpret_cast<void**>(&s.hX), chunk * d * 4, hipHostMallocDefault), "hipHostMalloc") ||
-            !hip_ok(hipHostMalloc(reinterpret_cast<void**>(&s.hcodes), chunk * m, hipHostMallocDefault), "hipHostMalloc") ||
-            !hip_ok(hipHostMalloc(reinterpret_cast<void**>(&s.ha), want ? chunk * m * 4 : 4, hipHostMallocDefault), "hipHostMalloc") ||
-            !hip_ok(hipHostMalloc(reinterpret_cast<void**>(&s.hcost), want ? chunk * 4 : 4, hipHostMallocDefault), "hipHostMalloc") ||
-            !hip_ok(s.dX.Ensure(chunk * d * 4), "hipMalloc") || !hip_ok(s.dcodes.Ensure(chunk * m), "hipMalloc") ||
-            !hip_ok(s.da.Ensure(want ? chunk * m * 4 : 4), "hipMalloc") ||
-            !hip_ok(s.dcost.Ensure(want ? chunk * 4 : 4), "hipMalloc") ||
-            !hip_ok(hipEventCreate(&s.copied), "hipEventCreate") || !hip_ok(hipEventCreate(&s.done), "hipEventCreate") ||
-            !hip_ok(hipEventCreate(&s.c0), "hipEventCreate") || !hip_ok(hipEventCreate(&s.c1), "hipEventCreate") ||
-            !hip_ok(hipEventCreate(&s.k0), "hipEventCreate")) {
+    auto cleanup = [&]() {
+        (void)hipStreamSynchronize(c->copy_stream);
+        (void)hipStreamSynchronize(c->stream);
+        for (Slot& sl : slot) {
+            for (void* p : {sl.hin, static_cast<void*>(sl.hcodes), static_cast<void*>(sl.ha), static_cast<void*>(sl.hcost),
+                            static_cast<void*>(sl.hcluster), static_cast<void*>(sl.hbest)})
+                if (p) (void)hipHostFree(p);
+            for (DevBuf* b : {&sl.din, &sl.dX, &sl.dcodes, &sl.da, &sl.dcost, &sl.dcluster, &sl.dbest}) b->Release();
+            for (hipEvent_t e : {sl.copied, sl.done, sl.c0, sl.c1, sl.k0})
+                if (e) (void)hipEventDestroy(e);
+        }
+    };
+    auto hmalloc = [&](void** p, size_t bytes) {
+        return hip_ok(hipHostMalloc(p, std::max<size_t>(bytes, 16), hipHostMallocDefault), "hipHostMalloc");
+    };
+    for (Slot& sl : slot) {
+        bool ok = hmalloc(&sl.hin, ch * d * esz) && hmalloc(reinterpret_cast<void**>(&sl.hcodes), ch * code_b) &&
+                  hip_ok(sl.din.Ensure(ch * d * esz), "hipMalloc") && hip_ok(sl.dcodes.Ensure(ch * code_b), "hipMalloc");
+        if (ok && sp->input_u8) ok = hip_ok(sl.dX.Ensure(ch * d * 4), "hipMalloc");
+        if (ok && want)
+            ok = hmalloc(reinterpret_cast<void**>(&sl.ha), ch * m * 4) && hmalloc(reinterpret_cast<void**>(&sl.hcost), ch * 4) &&
+                 hip_ok(sl.da.Ensure(ch * m * 4), "hipMalloc") && hip_ok(sl.dcost.Ensure(ch * 4), "hipMalloc");
+        if (ok && lr)
+            ok = hmalloc(reinterpret_cast<void**>(&sl.hcluster), ch * 4) && hmalloc(reinterpret_cast<void**>(&sl.hbest), ch * 4) &&
+                 hip_ok(sl.dcluster.Ensure(ch * 4), "hipMalloc") && hip_ok(sl.dbest.Ensure(ch * 4), "hipMalloc");
+        for (hipEvent_t* e : {&sl.copied, &sl.done, &sl.c0, &sl.c1, &sl.k0})
+            if (ok) ok = hip_ok(hipEventCreate(e), "hipEventCreate");
+        if (!ok) {
             cleanup();
             return rc;
         }
     }
-    double fill_ms = 0.0, h2d_ms = 0.0, comp_ms = 0.0, h2d_bytes = 0.0;
+    double fill_ms = 0.0, sink_ms = 0.0, h2d_ms = 0.0, comp_ms = 0.0, h2d_bytes = 0.0;
     int64_t nchunks = 0;
-    auto drain = [&](Slot& s) -> bool {
-        if (!s.busy) return true;
-        if (!hip_ok(hipEventSynchronize(s.done), "hipEventSynchronize")) return false;
+    auto drain = [&](Slot& sl) -> bool {
+        if (!sl.busy) return true;
+        if (!hip_ok(hipEventSynchronize(sl.done), "hipEventSynchronize")) return false;
         float ms = 0.0f;
-        if (hip_ok(hipEventElapsedTime(&ms, s.c0, s.c1), "hipEventElapsedTime")) h2d_ms += ms;
-        if (hip_ok(hipEventElapsedTime(&ms, s.k0, s.done), "hipEventElapsedTime")) comp_ms += ms;
-        s.busy = false;
-        if (sink(user, s.first, s.count, s.hcodes, want ? s.ha : nullptr, want ? s.hcost : nullptr) != 0) {
+        if (hip_ok(hipEventElapsedTime(&ms, sl.c0, sl.c1), "hipEventElapsedTime")) h2d_ms += ms;
+        if (hip_ok(hipEventElapsedTime(&ms, sl.k0, sl.done), "hipEventElapsedTime")) comp_ms += ms;
+        sl.busy = false;
+        stlq_mi355_chunk_out out{};
+        if (lr) {
+            out.cluster_id = sl.hcluster;
+            out.B_small = m > 1 ? sl.hcodes : nullptr;
+            out.best_err = sl.hbest;
+        } else {
+            out.codes = sl.hcodes;
+            out.a = want ? sl.ha : nullptr;
+            out.cost = want ? sl.hcost : nullptr;
+        }
+        const auto s0 = std::chrono::steady_clock::now();
+        const int src = sink(user, sl.first, sl.count, &out);
+        sink_ms += std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - s0).count();
+        if (src != 0) {
             rc = Fail(STLQ_MI355_ERR_CALLBACK, "sink callback failed");
             return false;
         }
@@ -854,51 +892,59 @@ int stlq_mi355_encode_stream(stlq_mi355_ctx* c, int64_t n_total, int64_t chunk, 
     };
     int64_t ci = 0;
     for (int64_t first = 0; first < n_total; first += chunk, ++ci) {
-        Slot& s = slot[ci & 1];
-        // Reuse of this slot's pinned and device buffers waits for its previous chunk.
-        if (!drain(s)) break;
-        s.first = first;
-        s.count = std::min(chunk, n_total - first);
+        Slot& sl = slot[ci & 1];
+        if (!drain(sl)) break;  // the slot's buffers are free once its previous chunk is done
+        sl.first = first;
+        sl.count = std::min(chunk, n_total - first);
+        const size_t cnt = static_cast<size_t>(sl.count);
         const auto f0 = std::chrono::steady_clock::now();
-        if (fill(user, s.first, s.count, s.hX) != 0) {
+        if (fill(user, sl.first, sl.count, sl.hin) != 0) {
             rc = Fail(STLQ_MI355_ERR_CALLBACK, "fill callback failed");
             break;
         }
         fill_ms += std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - f0).count();
-        const size_t xb = static_cast<size_t>(s.count) * d * 4;
-        if (!hip_ok(hipEventRecord(s.c0, c->copy_stream), "hipEventRecord") ||
-            !hip_ok(hipMemcpyAsync(s.dX.p, s.hX, xb, hipMemcpyHostToDevice, c->copy_stream), "hipMemcpyAsync") ||
-            !hip_ok(hipEventRecord(s.c1, c->copy_stream), "hipEventRecord") ||
-            !hip_ok(hipEventRecord(s.copied, c->copy_stream), "hipEventRecord") ||
-            !hip_ok(hipStreamWaitEvent(c->stream, s.copied, 0), "hipStreamWaitEvent") ||
-            !hip_ok(hipEventRecord(s.k0, c->stream), "hipEventRecord"))
+        const size_t xb = cnt * d * esz;
+        if (!hip_ok(hipEventRecord(sl.c0, c->copy_stream), "hipEventRecord") ||
+            !hip_ok(hipMemcpyAsync(sl.din.p, sl.hin, xb, hipMemcpyHostToDevice, c->copy_stream), "hipMemcpyAsync") ||
+            !hip_ok(hipEventRecord(sl.c1, c->copy_stream), "hipEventRecord") ||
+            !hip_ok(hipEventRecord(sl.copied, c->copy_stream), "hipEventRecord") ||
+            !hip_ok(hipStreamWaitEvent(c->stream, sl.copied, 0), "hipStreamWaitEvent") ||
+            !hip_ok(hipEventRecord(sl.k0, c->stream), "hipEventRecord"))
             break;
         h2d_bytes += static_cast<double>(xb);
-        EncodeOut o{s.dcodes.as<uint8_t>(), want ? s.da.as<float>() : nullptr, want ? s.dcost.as<float>() : nullptr,
-                    nullptr};
-        rc = EncodeTile(c, s.dX.as<float>(), s.count, *params, o, c->stream, false);
+        const float* dX = sl.din.as<float>();
+        if (sp->input_u8) {
+            if (!hip_ok(LaunchU8ToF32(sl.din.as<uint8_t>(), sl.dX.as<float>(), cnt * d, c->stream), "U8ToF32")) break;
+            dX = sl.dX.as<float>();
+        }
+        if (lr) {
+            rc = LargeRootTile(c, dX, sl.count, Hb, sp->root_mode, nullptr, nullptr, sl.dcluster.as<uint32_t>(),
+                               sl.dcodes.as<uint8_t>(), sl.dbest.as<float>(), c->stream, nullptr);
+        } else {
+            EncodeOut o{sl.dcodes.as<uint8_t>(), want ? sl.da.as<float>() : nullptr, want ? sl.dcost.as<float>() : nullptr,
+                        nullptr};
+            rc = EncodeTile(c, dX, sl.count, sp->encode, o, c->stream, false);
+        }
         if (rc != STLQ_MI355_OK) break;
-        if (!hip_ok(hipMemcpyAsync(s.hcodes, s.dcodes.p, static_cast<size_t>(s.count) * m, hipMemcpyDeviceToHost,
-                                   c->stream), "hipMemcpyAsync"))
+        if (!hip_ok(hipMemcpyAsync(sl.hcodes, sl.dcodes.p, cnt * code_b, hipMemcpyDeviceToHost, c->stream), "hipMemcpyAsync"))
             break;
-        if (want && (!hip_ok(hipMemcpyAsync(s.ha, s.da.p, static_cast<size_t>(s.count) * m * 4, hipMemcpyDeviceToHost,
-                                            c->stream), "hipMemcpyAsync") ||
-                     !hip_ok(hipMemcpyAsync(s.hcost, s.dcost.p, static_cast<size_t>(s.count) * 4,
-                                            hipMemcpyDeviceToHost, c->stream), "hipMemcpyAsync")))
+        if (want && (!hip_ok(hipMemcpyAsync(sl.ha, sl.da.p, cnt * m * 4, hipMemcpyDeviceToHost, c->stream), "hipMemcpyAsync") ||
+                     !hip_ok(hipMemcpyAsync(sl.hcost, sl.dcost.p, cnt * 4, hipMemcpyDeviceToHost, c->stream), "hipMemcpyAsync")))
             break;
-        if (!hip_ok(hipEventRecord(s.done, c->stream), "hipEventRecord")) break;
-        s.busy = true;
+        if (lr && (!hip_ok(hipMemcpyAsync(sl.hcluster, sl.dcluster.p, cnt * 4, hipMemcpyDeviceToHost, c->stream), "hipMemcpyAsync") ||
+                   !hip_ok(hipMemcpyAsync(sl.hbest, sl.dbest.p, cnt * 4, hipMemcpyDeviceToHost, c->stream), "hipMemcpyAsync")))
+            break;
+        if (!hip_ok(hipEventRecord(sl.done, c->stream), "hipEventRecord")) break;
+        sl.busy = true;
         ++nchunks;
         // Hand the previous chunk to the sink while this one copies and encodes.
-        Slot& prev = slot[(ci + 1) & 1];
-        if (!drain(prev)) break;
+        if (!drain(slot[(ci + 1) & 1])) break;
     }
     if (rc == STLQ_MI355_OK) {
         for (int k = 0; k < 2 && rc == STLQ_MI355_OK; ++k) {
-            // drain in chunk order: the older busy slot first
             Slot* older = nullptr;
-            for (Slot& s : slot)
-                if (s.busy && (!older || s.first < older->first)) older = &s;
+            for (Slot& sl : slot)
+                if (sl.busy && (!older || sl.first < older->first)) older = &sl;
             if (older && !drain(*older)) break;
         }
     }
@@ -908,6 +954,7 @@ int stlq_mi355_encode_stream(stlq_mi355_ctx* c, int64_t n_total, int64_t chunk, 
         stats->h2d_ms = h2d_ms;
         stats->compute_ms = comp_ms;
         stats->fill_ms = fill_ms;
+        stats->sink_ms = sink_ms;
         stats->h2d_bytes = h2d_bytes;
         stats->chunks = nchunks;
     }
@@ -916,6 +963,124 @@ int stlq_mi355_encode_stream(stlq_mi355_ctx* c, int64_t n_total, int64_t chunk, 
 
 // ---------------------------------------------------------------------------------------------
 // Large root.
+}  // extern "C"
+
+namespace {
+
+int CheckLargeRoot(stlq_mi355_ctx* c, int H_beam, int root_mode) {
+    RC_TRY(CheckCtx(c));
+    if (!c->has_lr) return Fail(STLQ_MI355_ERR_STATE, "large-root codebooks not set (call stlq_mi355_set_large_root)");
+    RC_TRY(CheckBeam(std::max(1, H_beam)));
+    if (root_mode != 0 && root_mode != 1) return Fail(STLQ_MI355_ERR_INVALID, "root_mode must be 0 or 1");
+    return STLQ_MI355_OK;
+}
+
+int64_t LargeRootTileVectors(stlq_mi355_ctx* c, int64_t n, int Hb, bool forced) {
+    const int m = c->lr_m;
+    const int64_t per = 4LL * c->lr_d + 4 + 8LL * std::max(c->Hs, 1) + (forced ? 8 : 4LL * c->h0) +
+                        2 * (4LL * Hb * BeamRecordStride(m) + 4) + m + 16;
+    int64_t t = std::max<int64_t>(EnvWorkspaceBytes() / per, 1024);
+    return std::min<int64_t>(t, std::max<int64_t>(n, 1));
+}
+
+// One tile of BeamSearchPrefixLSLargeRoot on device-resident fp32 X (nt x d): ||x||^2, xC_small
+// (MFMA GEMM unless given), root candidates (forced root, nearest root or top-H roots from the
+// MFMA score GEMM), then the expansion layers. Outputs cluster ids, B_small ((m-1) x nt) and the
+// selected errors, all device pointers.
+int LargeRootTile(stlq_mi355_ctx* c, const float* dX, int64_t nt, int Hb, int root_mode, const uint32_t* d_forced,
+                  const float* dxC_given, uint32_t* d_cluster, uint8_t* d_codes, float* d_best, hipStream_t s,
+                  TileEvents* te) {
+    const int m = c->lr_m, Hs = c->Hs, h0 = c->h0, d = c->lr_d;
+    HIP_TRY(c->nx2.Ensure(static_cast<size_t>(nt) * 4));
+    HIP_TRY(c->xC.Ensure(static_cast<size_t>(nt) * std::max(Hs, 1) * 4));
+    HIP_TRY(c->scores.Ensure(static_cast<size_t>(nt) * (d_forced ? 1 : h0) * 4));
+    RC_TRY(EnsureState(c, nt, m, Hb));
+    auto rec = [&](int k) -> hipError_t {
+        if (!te) return hipSuccess;
+        te->e[k] = c->NextEvent();
+        return hipEventRecord(te->e[k], s);
+    };
+    if (te) te->n = nt;
+    HIP_TRY(rec(0));
+    HIP_TRY(LaunchXNorm2(dX, d, nt, c->nx2.as<float>(), s));
+    HIP_TRY(rec(1));
+    const float* dxs = dxC_given;
+    if (Hs > 0 && !dxs) {
+        HIP_TRY(LaunchGemmXc(dX, nt, d, c->Cs.as<float>(), Hs, c->xC.as<float>(), Hs, s));
+        dxs = c->xC.as<float>();
+        if (te) ++te->gemm_launches;
+    }
+    RootArgs ra;
+    ra.nx2 = c->nx2.as<float>();
+    ra.norm0 = c->norm0.as<float>();
+    ra.out = StateOf(c, 0);
+    ra.n = nt;
+    ra.m = m;
+    ra.Hb = Hb;
+    ra.h0 = h0;
+    ra.is_last = (m == 1);
+    ra.cluster_out = d_cluster;
+    ra.best_err = d_best;
+    ra.scores = c->scores.as<float>();
+    if (d_forced) {
+        HIP_TRY(LaunchGatherRootDot(dX, d, c->C0.as<float>(), d_forced, nt, c->scores.as<float>(), s));
+        ra.ldx = 1;
+        ra.forced = d_forced;
+        ra.root_slots = 1;
+    } else {
+        HIP_TRY(LaunchGemmXc(dX, nt, d, c->C0.as<float>(), h0, c->scores.as<float>(), h0, s));
+        if (te) ++te->gemm_launches;
+        ra.ldx = h0;
+        ra.root_slots = root_mode == 1 ? 1 : Hb;
+    }
+    HIP_TRY(rec(2));
+    HIP_TRY(LaunchRootSeed(ra, s));
+    if (te) {
+        te->lay[0] = te->e[2];
+        te->lay[1] = c->NextEvent();
+        te->layers = 1;
+        HIP_TRY(hipEventRecord(te->lay[1], s));
+    }
+    LayerArgs a;
+    a.gram.G = c->G_small.as<float>();
+    a.gram.ld = Hs;
+    a.gram.G0S = c->G0S.as<float>();
+    for (int l = 0; l < m; ++l) a.gram.off[l] = c->soff[l];
+    a.xC = dxs;
+    a.ldx = Hs;
+    a.nx2 = c->nx2.as<float>();
+    a.gdiag = c->gdiag_small.as<float>();
+    a.n = nt;
+    a.m = m;
+    a.Hb = Hb;
+    a.codes_out = d_codes;
+    a.cluster_out = d_cluster;
+    a.best_err = d_best;
+    int cur = 0;
+    for (int L = 1; L < m; ++L) {
+        a.in = StateOf(c, cur);
+        a.out = StateOf(c, cur ^ 1);
+        a.K = c->lr_h[L];
+        a.offL = c->soff[L];
+        a.is_last = (L == m - 1);
+        HIP_TRY(LaunchBeamLayer(L, true, a, s));
+        cur ^= 1;
+        if (te) {
+            ++te->beam_launches;
+            te->lay[L + 1] = c->NextEvent();
+            te->layers = L + 1;
+            HIP_TRY(hipEventRecord(te->lay[L + 1], s));
+        }
+    }
+    HIP_TRY(rec(3));
+    if (te) te->e[4] = te->e[5] = te->e[6] = te->e[3];
+    return STLQ_MI355_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
 int stlq_mi355_set_large_root(stlq_mi355_ctx* c, int d, int m, const int* h_vec, const float* C0,
                               const float* C_small) {
     RC_TRY(CheckCtx(c));
@@ -956,109 +1121,40 @@ int stlq_mi355_set_large_root(stlq_mi355_ctx* c, int d, int m, const int* h_vec,
 int stlq_mi355_beam_search_large_root(stlq_mi355_ctx* c, const float* X, const float* xC_small, int64_t n,
                                       int H_beam, const uint32_t* forced_root, int root_mode, uint32_t* cluster_id,
                                       uint8_t* B_small, float* best_err) {
-    RC_TRY(CheckCtx(c));
-    if (!c->has_lr) return Fail(STLQ_MI355_ERR_STATE, "large-root codebooks not set (call stlq_mi355_set_large_root)");
+    RC_TRY(CheckLargeRoot(c, H_beam, root_mode));
     const int Hb = std::max(1, H_beam);
-    RC_TRY(CheckBeam(Hb));
-    if (root_mode != 0 && root_mode != 1) return Fail(STLQ_MI355_ERR_INVALID, "root_mode must be 0 or 1");
-    const int m = c->lr_m, Hs = c->Hs, h0 = c->h0, d = c->lr_d;
+    const int m = c->lr_m, Hs = c->Hs, d = c->lr_d;
     if (n < 0 || (n > 0 && (!X || !cluster_id || (m > 1 && !B_small))))
         return Fail(STLQ_MI355_ERR_INVALID, "bad arguments");
     if (n == 0) return STLQ_MI355_OK;
     if (forced_root) {
         for (int64_t i = 0; i < n; ++i)
-            if (forced_root[i] >= static_cast<uint32_t>(h0))
+            if (forced_root[i] >= static_cast<uint32_t>(c->h0))
                 return Fail(STLQ_MI355_ERR_INVALID, "forced root " + std::to_string(forced_root[i]) + " of vector " +
                                                         std::to_string(i) + " >= h0");
     }
     c->ResetTimings();
-    const bool need_scores = forced_root == nullptr;
-    const int stride = BeamRecordStride(m);
-    const int64_t per = 4LL * d + 4 + 4LL * std::max(Hs, 1) + (need_scores ? 4LL * h0 : 8) +
-                        2 * (4LL * Hb * stride + 4) + m + 12;
-    int64_t tile = std::max<int64_t>(EnvWorkspaceBytes() / per, 1024);
-    tile = std::min<int64_t>(tile, n);
+    const int64_t tile = LargeRootTileVectors(c, n, Hb, forced_root != nullptr);
     HIP_TRY(c->X.Ensure(static_cast<size_t>(tile) * d * 4));
-    HIP_TRY(c->nx2.Ensure(static_cast<size_t>(tile) * 4));
-    HIP_TRY(c->xC.Ensure(static_cast<size_t>(tile) * std::max(Hs, 1) * 4));
-    HIP_TRY(c->scores.Ensure(static_cast<size_t>(tile) * (need_scores ? h0 : 1) * 4));
     HIP_TRY(c->roots.Ensure(static_cast<size_t>(tile) * 4 * 2));
     HIP_TRY(c->codes.Ensure(static_cast<size_t>(tile) * std::max(m - 1, 1)));
     HIP_TRY(c->best.Ensure(static_cast<size_t>(tile) * 4));
-    RC_TRY(EnsureState(c, tile, m, Hb));
+    if (xC_small) HIP_TRY(c->xC_in.Ensure(static_cast<size_t>(tile) * std::max(Hs, 1) * 4));
     uint32_t* d_roots = c->roots.as<uint32_t>();
     uint32_t* d_cluster = d_roots + tile;
+    hipStream_t s = c->stream;
     for (int64_t t0 = 0; t0 < n; t0 += tile) {
         const int64_t nt = std::min(tile, n - t0);
-        hipStream_t s = c->stream;
         HIP_TRY(hipMemcpyAsync(c->X.p, X + t0 * d, static_cast<size_t>(nt) * d * 4, hipMemcpyHostToDevice, s));
-        HIP_TRY(LaunchXNorm2(c->X.as<float>(), d, nt, c->nx2.as<float>(), s));
-        if (Hs > 0) {
-            if (xC_small) {
-                HIP_TRY(hipMemcpyAsync(c->xC.p, xC_small + t0 * Hs, static_cast<size_t>(nt) * Hs * 4,
-                                       hipMemcpyHostToDevice, s));
-            } else {
-                HIP_TRY(LaunchGemmXc(c->X.as<float>(), nt, d, c->Cs.as<float>(), Hs, c->xC.as<float>(), Hs, s));
-            }
-        }
-        TileEvents te;
-        te.n = nt;
-        te.e[0] = te.e[1] = te.e[2] = c->NextEvent();
-        HIP_TRY(hipEventRecord(te.e[0], s));
-        RootArgs ra;
-        ra.nx2 = c->nx2.as<float>();
-        ra.norm0 = c->norm0.as<float>();
-        ra.out = StateOf(c, 0);
-        ra.n = nt;
-        ra.m = m;
-        ra.Hb = Hb;
-        ra.h0 = h0;
-        ra.is_last = (m == 1);
-        ra.cluster_out = d_cluster;
-        ra.best_err = c->best.as<float>();
-        if (forced_root) {
+        if (forced_root)
             HIP_TRY(hipMemcpyAsync(d_roots, forced_root + t0, static_cast<size_t>(nt) * 4, hipMemcpyHostToDevice, s));
-            HIP_TRY(LaunchGatherRootDot(c->X.as<float>(), d, c->C0.as<float>(), d_roots, nt, c->scores.as<float>(), s));
-            ra.scores = c->scores.as<float>();
-            ra.ldx = 1;
-            ra.forced = d_roots;
-            ra.root_slots = 1;
-        } else {
-            HIP_TRY(LaunchGemmXc(c->X.as<float>(), nt, d, c->C0.as<float>(), h0, c->scores.as<float>(), h0, s));
-            te.gemm_launches = 1;
-            ra.scores = c->scores.as<float>();
-            ra.ldx = h0;
-            ra.root_slots = root_mode == 1 ? 1 : Hb;
-        }
-        HIP_TRY(LaunchRootSeed(ra, s));
-        LayerArgs a;
-        a.gram.G = c->G_small.as<float>();
-        a.gram.ld = Hs;
-        a.gram.G0S = c->G0S.as<float>();
-        for (int l = 0; l < m; ++l) a.gram.off[l] = c->soff[l];
-        a.xC = c->xC.as<float>();
-        a.ldx = Hs;
-        a.nx2 = c->nx2.as<float>();
-        a.gdiag = c->gdiag_small.as<float>();
-        a.n = nt;
-        a.m = m;
-        a.Hb = Hb;
-        a.codes_out = c->codes.as<uint8_t>();
-        a.cluster_out = d_cluster;
-        a.best_err = c->best.as<float>();
-        int cur = 0;
-        for (int L = 1; L < m; ++L) {
-            a.in = StateOf(c, cur);
-            a.out = StateOf(c, cur ^ 1);
-            a.K = c->lr_h[L];
-            a.offL = c->soff[L];
-            a.is_last = (L == m - 1);
-            HIP_TRY(LaunchBeamLayer(L, true, a, s));
-            cur ^= 1;
-            ++te.beam_launches;
-        }
-        te.e[3] = te.e[4] = te.e[5] = te.e[6] = c->NextEvent();
-        HIP_TRY(hipEventRecord(te.e[3], s));
+        if (xC_small)
+            HIP_TRY(hipMemcpyAsync(c->xC_in.p, xC_small + t0 * Hs, static_cast<size_t>(nt) * Hs * 4,
+                                   hipMemcpyHostToDevice, s));
+        TileEvents te;
+        RC_TRY(LargeRootTile(c, c->X.as<float>(), nt, Hb, root_mode, forced_root ? d_roots : nullptr,
+                             xC_small ? c->xC_in.as<float>() : nullptr, d_cluster, c->codes.as<uint8_t>(),
+                             c->best.as<float>(), s, &te));
         c->tiles.push_back(te);
         HIP_TRY(hipMemcpyAsync(cluster_id + t0, d_cluster, static_cast<size_t>(nt) * 4, hipMemcpyDeviceToHost, s));
         if (m > 1)

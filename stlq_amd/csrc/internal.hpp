@@ -119,5 +119,6 @@ hipError_t LaunchIcmLayer(const IcmArgs& a, hipStream_t s);
 hipError_t LaunchIcmDeactivate(uint8_t* active, const uint8_t* changed, int64_t n, hipStream_t s);
 hipError_t LaunchFill8(uint8_t* p, uint8_t v, int64_t n, hipStream_t s);
 hipError_t LaunchCopy16(void* dst, const void* src, size_t n16, hipStream_t s);
+hipError_t LaunchU8ToF32(const uint8_t* in, float* out, size_t count, hipStream_t s);
 
 }  // namespace stlq_mi355

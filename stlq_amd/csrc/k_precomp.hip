@@ -137,7 +137,28 @@ __global__ __launch_bounds__(256) void Copy16Kernel(uint4* __restrict__ dst, con
     for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n16; i += stride) dst[i] = src[i];
 }
 
+// uint8 -> fp32 widening of a streamed chunk (U8ToF32Kernel1D, kernel_provider_cuda_stream_kernels.inc:16),
+// four bytes per thread per iteration.
+__global__ __launch_bounds__(256) void U8ToF32Kernel(const uint8_t* __restrict__ in, float* __restrict__ out, size_t count) {
+    const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x * 4;
+    for (size_t i = (static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 4; i < count; i += stride) {
+        if (i + 3 < count) {
+            const uchar4 v = *reinterpret_cast<const uchar4*>(in + i);
+            *reinterpret_cast<float4*>(out + i) = make_float4(v.x, v.y, v.z, v.w);
+        } else {
+            for (size_t k = i; k < count; ++k) out[k] = static_cast<float>(in[k]);
+        }
+    }
+}
+
 }  // namespace
+
+hipError_t LaunchU8ToF32(const uint8_t* in, float* out, size_t count, hipStream_t s) {
+    if (count == 0) return hipSuccess;
+    const size_t blocks = std::min<size_t>((count / 4 + 255) / 256 + 1, 256 * 64);
+    hipLaunchKernelGGL(U8ToF32Kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, in, out, count);
+    return hipGetLastError();
+}
 
 hipError_t LaunchCopy16(void* dst, const void* src, size_t n16, hipStream_t s) {
     if (n16 == 0) return hipSuccess;

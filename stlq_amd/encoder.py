@@ -234,27 +234,46 @@ class Context:
         return buf.value.decode(), cu.value
 
     # ---- streaming -----------------------------------------------------------------------
-    def encode_stream(self, n_total, chunk, cfg: EncodeConfig, fill, sink):
-        """fill(first, count, out_view (count, d) float32) and sink(first, count, codes, a, cost)."""
-        d, m = self.d, self.m
-        want = cfg.want_coeffs or cfg.icm_iters > 0
+    def encode_stream(self, n_total, chunk, cfg: EncodeConfig, fill, sink, input_u8=False, large_root=False,
+                      root_mode=1):
+        """Streaming encode. fill(first, count, out) fills `out` ((count, d) float32, or uint8 when
+        input_u8). sink(first, count, result) receives a dict of numpy copies: full precomp ->
+        codes (and a, cost when coefficients are wanted); large root -> cluster_id, B_small, best_err."""
+        if large_root:
+            d, m = self.lr[0], len(self.lr[1])
+        else:
+            d, m = self.d, self.m
+        want = (not large_root) and (cfg.want_coeffs or cfg.icm_iters > 0)
+        dt = np.uint8 if input_u8 else np.float32
+        ctype = ctypes.c_uint8 if input_u8 else ctypes.c_float
         err = []
 
         def _fill(user, first, count, dst):
             try:
-                view = np.ctypeslib.as_array(dst, shape=(count * d,)).reshape(count, d)
+                buf = ctypes.cast(dst, ctypes.POINTER(ctype))
+                view = np.ctypeslib.as_array(buf, shape=(count * d,)).reshape(count, d)
+                assert view.dtype == dt
                 fill(int(first), int(count), view)
                 return 0
             except Exception as e:  # surfaced after the call
                 err.append(e)
                 return 1
 
-        def _sink(user, first, count, codes, a, cost):
+        def _sink(user, first, count, outp):
             try:
-                c = np.ctypeslib.as_array(codes, shape=(count * m,)).reshape(count, m).copy()
-                av = np.ctypeslib.as_array(a, shape=(count * m,)).reshape(count, m).copy() if want else None
-                cv = np.ctypeslib.as_array(cost, shape=(count,)).copy() if want else None
-                sink(int(first), int(count), c, av, cv)
+                o = outp.contents
+                res = {}
+                if large_root:
+                    res["cluster_id"] = np.ctypeslib.as_array(o.cluster_id, shape=(count,)).copy()
+                    res["B_small"] = (np.ctypeslib.as_array(o.B_small, shape=(count * (m - 1),)).reshape(count, m - 1).copy()
+                                      if m > 1 else np.zeros((count, 0), np.uint8))
+                    res["best_err"] = np.ctypeslib.as_array(o.best_err, shape=(count,)).copy()
+                else:
+                    res["codes"] = np.ctypeslib.as_array(o.codes, shape=(count * m,)).reshape(count, m).copy()
+                    if want:
+                        res["a"] = np.ctypeslib.as_array(o.a, shape=(count * m,)).reshape(count, m).copy()
+                        res["cost"] = np.ctypeslib.as_array(o.cost, shape=(count,)).copy()
+                sink(int(first), int(count), res)
                 return 0
             except Exception as e:
                 err.append(e)
@@ -262,7 +281,7 @@ class Context:
 
         f, s = _lib.FILL_FN(_fill), _lib.SINK_FN(_sink)
         st = StreamStats()
-        p = cfg.to_c()
+        p = _lib.StreamParams(cfg.to_c(), int(bool(input_u8)), int(bool(large_root)), int(root_mode))
         rc = self.lib.stlq_mi355_encode_stream(self.h, int(n_total), int(chunk), ctypes.byref(p), f, s, None,
                                                ctypes.byref(st))
         if err:
@@ -350,8 +369,14 @@ def EncodeBase(ctx: Context, X, cfg: EncodeConfig):
 
 
 def EncodeBaseStreamingF32(ctx: Context, n_total, chunk, cfg: EncodeConfig, fill, sink):
-    """src/quantizer/encode_base_streaming.cpp:4544-4579: pinned chunks, double-buffered H2D."""
+    """src/quantizer/encode_base_streaming.cpp:4544-4579: fp32 chunks, double-buffered H2D."""
     return ctx.encode_stream(n_total, chunk, cfg, fill, sink)
+
+
+def EncodeBaseStreaming(ctx: Context, n_total, chunk, cfg: EncodeConfig, fill, sink, root_mode=1):
+    """src/quantizer/encode_base_streaming.cpp:1913 (large pipeline): uint8 chunks widened on the
+    device, large-root beam; sink gets cluster_id, B_small and best_err per chunk."""
+    return ctx.encode_stream(n_total, chunk, cfg, fill, sink, input_u8=True, large_root=True, root_mode=root_mode)
 
 
 def BuildPrecompLargeRoot(ctx: Context, C0, C_small, h_vec):

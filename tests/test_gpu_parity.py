@@ -324,11 +324,11 @@ def test_stream_matches_in_memory(ctx, chunk):
     def fill(first, count, out):
         out[:] = X[first:first + count]
 
-    def sink(first, count, c, av, cv):
+    def sink(first, count, res):
         seen.append(first)
-        got_c[first:first + count] = c
-        got_a[first:first + count] = av
-        got_s[first:first + count] = cv
+        got_c[first:first + count] = res["codes"]
+        got_a[first:first + count] = res["a"]
+        got_s[first:first + count] = res["cost"]
 
     st = ctx.encode_stream(X.shape[0], chunk, cfg, fill, sink)
     assert seen == sorted(seen) and len(seen) == -(-5000 // chunk)
@@ -390,3 +390,35 @@ def test_large_root_bit_exact(ctx, orc, name, seed, n, d, h0, small, Hb, mode):
     assert np.array_equal(_bits(err_o), _bits(err_g))
     if mode == "forced":
         assert np.array_equal(cid_g, forced)
+
+
+@pytest.mark.parametrize("chunk", [700, 2500])
+def test_stream_large_root_u8_matches_in_memory(ctx, chunk):
+    """Streaming large-root encode of uint8 chunks (EncodeBaseStreaming's u8 path) equals the
+    in-memory large-root beam on the widened vectors."""
+    from stlq_amd import workloads
+
+    mix = workloads.Mixture("desc", 64, 128, 81)
+    X = mix.sample(0, 4000)
+    Xu8 = X.astype(np.uint8)
+    rng = np.random.default_rng(5)
+    C0 = mix.sample(5_000_000, 2048)
+    Cs = workloads.residual_codebooks(mix.sample(1_000_000, 3000) - C0[rng.integers(0, 2048, 3000)], 5, 256, 3, 7)
+    h = [2048] + [256] * 5
+    ctx.set_large_root(C0, Cs, h)
+    cid, Bs, err = ctx.beam_search_large_root(Xu8.astype(np.float32), 8, root_mode=1)
+    got = {"cluster_id": np.zeros_like(cid), "B_small": np.zeros_like(Bs), "best_err": np.zeros_like(err)}
+
+    def fill(first, count, out):
+        out[:] = Xu8[first:first + count]
+
+    def sink(first, count, res):
+        for k in got:
+            got[k][first:first + count] = res[k]
+
+    st = ctx.encode_stream(4000, chunk, EncodeConfig(H_beam=8, icm_iters=0), fill, sink, input_u8=True,
+                           large_root=True, root_mode=1)
+    assert st.chunks == -(-4000 // chunk) and st.h2d_bytes == 4000 * 64
+    assert np.array_equal(got["cluster_id"], cid)
+    assert np.array_equal(got["B_small"], Bs)
+    assert np.array_equal(_bits(got["best_err"]), _bits(err))
