@@ -41,9 +41,12 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=1)
-    ap.add_argument("--n", type=int, default=1_000_000)
+    ap.add_argument("--n", type=int, default=0, help="vectors (0 = the configuration's size)")
     ap.add_argument("--cpu-sample", type=int, default=100_000,
                     help="vectors timed on the CPU oracle (0 = skip)")
+    ap.add_argument("--config", default="C2", choices=["C1", "C2", "C3", "C4", "C5"],
+                    help="benchmark configuration; C2 is the headline, the others are extra measurements")
+    ap.add_argument("--chunk", type=int, default=4_000_000, help="C5 streaming chunk (vectors)")
     ap.add_argument("--calib-copy-mb", type=int, default=0,
                     help="after the timed steps, run a plain copy kernel of this many MiB "
                          "(traffic reference for hardware counters)")
@@ -56,19 +59,22 @@ def main():
     from stlq_amd import workloads
     from stlq_amd.encoder import Context, EncodeConfig
 
-    w = workloads.CONFIGS["C2"]
-    n = int(args.n)
+    w = workloads.CONFIGS[args.config]
+    if args.config == "C5":
+        return bench_stream_large_root(args, w)
+    n = int(args.n) or w.n
     t0 = time.perf_counter()
     mix = workloads.Mixture(w.kind, w.d, w.n_comp, w.seed)
     X = mix.sample(0, n)
     C = workloads.make_codebooks(w)
     h = [w.K] * w.m
-    log(f"workload generated in {time.perf_counter() - t0:.1f}s: n={n} d={w.d} M={w.m} K={w.K} beam={w.H_beam}")
+    log(f"workload {w.name} generated in {time.perf_counter() - t0:.1f}s: n={n} d={w.d} M={w.m} K={w.K} "
+        f"beam={w.H_beam} icm={w.icm_iters}")
 
     ctx = Context(0)
     dev_name, cus = ctx.device_info()
     ctx.set_codebooks(C, h)
-    cfg = EncodeConfig(H_beam=w.H_beam, icm_iters=0, want_coeffs=True)
+    cfg = EncodeConfig(H_beam=w.H_beam, icm_iters=w.icm_iters, want_coeffs=True)
     dX = ctx.dev_alloc(X.nbytes)
     dcodes = ctx.dev_alloc(n * w.m)
     da = ctx.dev_alloc(n * w.m * 4)
@@ -80,7 +86,7 @@ def main():
         ctx.synchronize()
         log(f"warmup step {k + 1}/{args.warmup} done")
 
-    gemm_ms = beam_ms = total_ms = 0.0
+    gemm_ms = beam_ms = total_ms = icm_ms = 0.0
     layer_ms = np.zeros(20)
     launches = 0
     ctx.synchronize()
@@ -90,6 +96,7 @@ def main():
         t = ctx.last_timings()  # waits for this step's events
         gemm_ms += t.gemm_ms
         beam_ms += t.beam_ms
+        icm_ms += t.icm_ms
         total_ms += t.total_ms
         layer_ms += np.array(t.layer_ms[:20])
         launches += t.gemm_launches
@@ -125,11 +132,23 @@ def main():
         "gemm_ms": gemm_ms / steps,
         "beam_ms": beam_ms / steps,
         "beam_layer_ms": [round(x / steps, 3) for x in layer_ms[:M]],
+        "icm_ms": icm_ms / steps,
         "device_total_ms": total_ms / steps,
     }
 
+    metric = ("vectors encoded/sec (d=128,M=8,K=256,B=16)" if args.config == "C2" else
+              f"vectors encoded/sec (d={d},M={M},K={K},B={B}" + (f",ICM={w.icm_iters})" if w.icm_iters else ")"))
+    workload = {
+        "C1": "100k vectors d=128 (1024-component GMM, centres N(0,1), sigma 0.3), M=4 x K=256, beam 4",
+        "C2": "1M descriptor-like vectors d=128 (4096-component GMM, clipped/rounded to [0,255], fp32), "
+              "M=8 x K=256 residual k-means codebooks, beam 16, no ICM, LS refit + cost",
+        "C3": "1M unit-norm vectors d=96 (8192-component spherical mixture, 0.2 rad), spherical k-means "
+              "M=8 x K=256, beam 16 + 2 ICM sweeps (|score|), LS refit + cost",
+        "C4": "500k vectors d=960 (2048 components, per-dim variance 1/(1+i/64)), M=16 x K=256, beam 8, "
+              "LS refit + cost",
+    }[args.config]
     out = {
-        "metric": "vectors encoded/sec (d=128,M=8,K=256,B=16)",
+        "metric": metric,
         "value": value,
         "unit": "vectors/s",
         "n_gpus": 1,
@@ -141,11 +160,8 @@ def main():
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic",
-        "config": {
-            "workload": "1M descriptor-like vectors d=128 (4096-component GMM, clipped/rounded to [0,255], fp32), "
-                        "M=8 x K=256 residual k-means codebooks, beam 16, no ICM, LS refit + cost",
-            "n": n, "d": d, "M": M, "K": K, "H_beam": B, "icm_iters": 0,
-        },
+        "config": {"workload": workload, "name": args.config, "n": n, "d": d, "M": M, "K": K, "H_beam": B,
+                   "icm_iters": w.icm_iters},
         "roofline": {
             "kernel": f"beam layer L={last} (LayerKernel<{last}>)",
             "bound": "hbm",
@@ -185,8 +201,12 @@ def main():
         t_gemm = time.perf_counter() - tc
         codes_o, _ = orc.beam_search(nx2, xC, G, h, B, nthreads=threads)
         t_beam = time.perf_counter() - tc - t_gemm
-        a_o, _ = orc.solve_ls_all(xC, G, h, codes_o, nthreads=threads)
-        cost_o = orc.compute_costs(xC, G, h, codes_o, a_o, nx2, nthreads=threads)
+        if w.icm_iters:
+            codes_o, a_o, cost_o, _ = orc.icm(xC, G, inv, h, nx2, codes_o, w.icm_iters, True, cfg.seed,
+                                              nthreads=threads)
+        else:
+            a_o, _ = orc.solve_ls_all(xC, G, h, codes_o, nthreads=threads)
+            cost_o = orc.compute_costs(xC, G, h, codes_o, a_o, nx2, nthreads=threads)
         t_cpu = time.perf_counter() - tc
         log(f"cpu oracle: {ns} vectors in {t_cpu:.1f}s on {threads} threads")
         cpu_model = ""
@@ -203,8 +223,9 @@ def main():
             "unit": "vectors/s",
             "cores": threads,
             "kind": "port",
-            "sample": f"first {ns} vectors of the same workload; ||x||^2 + xC + beam + LS refit + cost; "
-                      f"stages s: xC {t_gemm:.2f}, beam {t_beam:.2f}, ls+cost {t_cpu - t_gemm - t_beam:.2f}; "
+            "sample": f"first {ns} vectors of the same workload; ||x||^2 + xC + beam + "
+                      f"{'ICM ' if w.icm_iters else ''}LS refit + cost; "
+                      f"stages s: xC {t_gemm:.2f}, beam {t_beam:.2f}, rest {t_cpu - t_gemm - t_beam:.2f}; "
                       f"cpu: {cpu_model}",
         }
         same = np.all(codes[:ns] == codes_o, axis=1)
@@ -216,6 +237,131 @@ def main():
 
     for p in (dX, dcodes, da, dcost):
         ctx.dev_free(p)
+    ctx.close()
+    print(json.dumps(out), flush=True)
+
+
+def bench_stream_large_root(args, w):
+    """C5: streaming encode of uint8-valued descriptor vectors in pinned chunks, nearest root of a
+    65,536-codeword root codebook forced, then 16 residual codebooks x 256, beam 32."""
+    from stlq_amd import workloads
+    from stlq_amd.encoder import Context, EncodeConfig
+
+    h0 = int(w.extra["h0"])
+    chunk = int(args.chunk)
+    n = int(args.n) or 2 * chunk
+    chunk = min(chunk, n)
+    t0 = time.perf_counter()
+    mix = workloads.Mixture(w.kind, w.d, w.n_comp, w.seed)
+    pool = mix.sample(0, chunk).astype(np.uint8)  # values are already integers in [0, 255]
+    C0, Cs = workloads.make_large_root(w, h0, w.m - 1)
+    h = [h0] + [w.K] * (w.m - 1)
+    log(f"workload C5 generated in {time.perf_counter() - t0:.1f}s: stream n={n} chunk={chunk} d={w.d} "
+        f"h0={h0} small={w.m - 1}x{w.K} beam={w.H_beam}")
+    ctx = Context(0)
+    dev_name, cus = ctx.device_info()
+    ctx.set_large_root(C0, Cs, h)
+    cfg = EncodeConfig(H_beam=w.H_beam, icm_iters=0, want_coeffs=False)
+    P = pool.shape[0]
+    keep = min(2000, chunk)
+    first_codes = {}
+
+    def fill(first, count, out):
+        # chunk c replays the pool rotated by a chunk-dependent offset (distinct rows per chunk)
+        off = (first // chunk) * 7919 % P
+        k = min(count, P - off)
+        out[:k] = pool[off:off + k]
+        if k < count:
+            out[k:] = pool[:count - k]
+
+    def sink(first, count, res):
+        if first == 0:
+            first_codes["cid"] = res["cluster_id"][:keep].copy()
+            first_codes["Bs"] = res["B_small"][:keep].copy()
+
+    warm = min(chunk, 100_000)
+    ctx.encode_stream(warm, warm, cfg, fill, sink, input_u8=True, large_root=True, root_mode=1)
+    log("warmup stream done")
+    t_start = time.perf_counter()
+    st = ctx.encode_stream(n, chunk, cfg, fill, sink, input_u8=True, large_root=True, root_mode=1)
+    wall = time.perf_counter() - t_start
+    t = ctx.last_timings()
+    log(f"streamed {n} vectors in {wall:.2f}s ({st.chunks} chunks)")
+    M = w.m
+    last = M - 1
+    layer_ms = np.array(t.layer_ms[:20])
+    nch = max(st.chunks, 1)
+    avg_last_ms = layer_ms[last] / nch
+    sel_bytes = 4.0 * w.K * w.H_beam * chunk
+    beam_ach = sel_bytes / (avg_last_ms * 1e-3) / 1e9
+    h2d_gbs = st.h2d_bytes / (st.h2d_ms * 1e-3) / 1e9 if st.h2d_ms > 0 else None
+    out = {
+        "metric": "vectors encoded/sec (stream, d=128 uint8, forced nearest root h0=65536 + 16x256, B=32)",
+        "value": n / wall,
+        "unit": "vectors/s",
+        "n_gpus": 1,
+        "steps": 1,
+        "warmup": 1,
+        "ms_per_step": wall * 1000.0,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": f"streaming encode of {n} uint8-valued d=128 vectors (C2 generator) in {chunk}-vector "
+                               "pinned chunks, double-buffered H2D; nearest of 65,536 root codewords forced, then "
+                               "16 residual codebooks x 256, beam 32",
+                   "name": "C5", "n": n, "chunk": chunk, "d": w.d, "h0": h0, "M_small": M - 1, "K": w.K,
+                   "H_beam": w.H_beam},
+        "roofline": {
+            "kernel": f"large-root beam layer L={last} (LayerKernel<{last}, large root>)",
+            "bound": "hbm",
+            "achieved": beam_ach,
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": beam_ach / PEAK_HBM_GBS,
+            "traffic": None,
+            "algorithmic_bytes_per_launch": sel_bytes,
+            "avg_launch_ms": avg_last_ms,
+        },
+        "streaming": {
+            "h2d_GBps": h2d_gbs,
+            "h2d_bytes": st.h2d_bytes,
+            "h2d_ms": st.h2d_ms,
+            "compute_ms": st.compute_ms,
+            "fill_ms": st.fill_ms,
+            "sink_ms": st.sink_ms,
+            "wall_ms": st.wall_ms,
+            "gpu_busy_frac": st.compute_ms / st.wall_ms if st.wall_ms > 0 else None,
+        },
+        "stages": {
+            "gemm_ms_per_chunk": t.gemm_ms / nch,
+            "root_seed_ms_per_chunk": layer_ms[0] / nch,
+            "beam_layer_ms_per_chunk": [round(x / nch, 3) for x in layer_ms[:M]],
+            "device_total_ms_per_chunk": t.total_ms / nch,
+        },
+        "device": {"arch": dev_name, "cus": cus},
+    }
+    if args.cpu_sample > 0:
+        from oracle import oracle as orc
+
+        ns = min(args.cpu_sample, keep)
+        threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
+        Xs = pool[:ns].astype(np.float32)
+        norm0, Gs, G0S = orc.build_precomp_large_root(C0, Cs, nthreads=threads)
+        tc = time.perf_counter()
+        nx2 = orc.xnorm2(Xs, nthreads=threads)
+        xs = orc.gemm_xc(Cs, Xs, mode=1, nthreads=threads)
+        cid_o, Bs_o, _ = orc.beam_search_large_root(Xs, nx2, C0, norm0, xs, Gs, G0S, h, w.H_beam, root_mode=1,
+                                                    nthreads=threads)
+        t_cpu = time.perf_counter() - tc
+        log(f"cpu oracle: {ns} vectors in {t_cpu:.1f}s on {threads} threads")
+        out["cpu_baseline"] = {
+            "value": ns / t_cpu, "unit": "vectors/s", "cores": threads, "kind": "port",
+            "sample": f"first {ns} vectors of the stream; ||x||^2 + xC_small + nearest-root scan over 65,536 roots "
+                      f"+ 16-layer beam 32"}
+        same = (cid_o == first_codes["cid"][:ns]) & np.all(Bs_o == first_codes["Bs"][:ns], axis=1)
+        out["parity"] = {"sample": ns, "codes_identical_frac": float(np.mean(same))}
     ctx.close()
     print(json.dumps(out), flush=True)
 

@@ -20,6 +20,9 @@ CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIBDIR = os.path.join(HERE, "lib")
 LIB = os.path.join(LIBDIR, "libstlq_mi355.so")
+# test driver of the C++ host mirror (stlq_amd/host/stlq_mi355.hpp), linked against LIB
+HOSTCHECK_SRC = os.path.join(ROOT, "tests", "host_mirror_check.cpp")
+HOSTCHECK = os.path.join(LIBDIR, "libstlq_mi355_hostcheck.so")
 SOURCES = ["k_precomp.hip", "k_gemm.hip", "k_beam.hip", "k_ls.hip", "capi.hip"]
 ARCH = "gfx950"
 
@@ -67,9 +70,23 @@ def build(verbose: bool = False) -> str:
     if res.returncode != 0:
         raise RuntimeError(f"link failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
     os.replace(tmp, LIB)
+    build_hostcheck()
     if verbose:
         print(f"built {LIB}")
     return LIB
+
+
+def build_hostcheck() -> str:
+    """g++ build of the host-mirror test driver; only the C ABI header is needed."""
+    tmp = HOSTCHECK + ".tmp"
+    cmd = [os.environ.get("CXX", "g++"), "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall",
+           f"-I{os.path.join(ROOT, 'include')}", HOSTCHECK_SRC, "-o", tmp,
+           f"-L{LIBDIR}", "-lstlq_mi355", "-Wl,-rpath,$ORIGIN"]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"host mirror build failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, HOSTCHECK)
+    return HOSTCHECK
 
 
 if __name__ == "__main__":

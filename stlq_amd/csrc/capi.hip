@@ -777,6 +777,7 @@ int stlq_mi355_last_timings(stlq_mi355_ctx* c, stlq_mi355_timings* out) {
 
 namespace {
 int CheckLargeRoot(stlq_mi355_ctx* c, int H_beam, int root_mode);
+int64_t LargeRootTileVectors(stlq_mi355_ctx* c, int64_t n, int Hb, bool forced);
 int LargeRootTile(stlq_mi355_ctx* c, const float* dX, int64_t nt, int Hb, int root_mode, const uint32_t* d_forced,
                   const float* dxC_given, uint32_t* d_cluster, uint8_t* d_codes, float* d_best, hipStream_t s,
                   TileEvents* te);
@@ -917,13 +918,22 @@ int stlq_mi355_encode_stream(stlq_mi355_ctx* c, int64_t n_total, int64_t chunk, 
             if (!hip_ok(LaunchU8ToF32(sl.din.as<uint8_t>(), sl.dX.as<float>(), cnt * d, c->stream), "U8ToF32")) break;
             dX = sl.dX.as<float>();
         }
-        if (lr) {
-            rc = LargeRootTile(c, dX, sl.count, Hb, sp->root_mode, nullptr, nullptr, sl.dcluster.as<uint32_t>(),
-                               sl.dcodes.as<uint8_t>(), sl.dbest.as<float>(), c->stream, nullptr);
-        } else {
-            EncodeOut o{sl.dcodes.as<uint8_t>(), want ? sl.da.as<float>() : nullptr, want ? sl.dcost.as<float>() : nullptr,
-                        nullptr};
-            rc = EncodeTile(c, dX, sl.count, sp->encode, o, c->stream, false);
+        // Encode the chunk in workspace-bounded tiles (sequential on the context stream).
+        const int64_t tile = lr ? LargeRootTileVectors(c, sl.count, Hb, false)
+                                : TileVectors(sl.count, c->d, c->m, c->H, Hb);
+        for (int64_t t0 = 0; t0 < sl.count && rc == STLQ_MI355_OK; t0 += tile) {
+            const int64_t nt = std::min(tile, sl.count - t0);
+            if (lr) {
+                TileEvents te;
+                rc = LargeRootTile(c, dX + t0 * d, nt, Hb, sp->root_mode, nullptr, nullptr,
+                                   sl.dcluster.as<uint32_t>() + t0, sl.dcodes.as<uint8_t>() + t0 * code_b,
+                                   sl.dbest.as<float>() + t0, c->stream, &te);
+                if (rc == STLQ_MI355_OK) c->tiles.push_back(te);
+            } else {
+                EncodeOut o{sl.dcodes.as<uint8_t>() + t0 * m, want ? sl.da.as<float>() + t0 * m : nullptr,
+                            want ? sl.dcost.as<float>() + t0 : nullptr, nullptr};
+                rc = EncodeTile(c, dX + t0 * d, nt, sp->encode, o, c->stream, true);
+            }
         }
         if (rc != STLQ_MI355_OK) break;
         if (!hip_ok(hipMemcpyAsync(sl.hcodes, sl.dcodes.p, cnt * code_b, hipMemcpyDeviceToHost, c->stream), "hipMemcpyAsync"))

@@ -1,0 +1,413 @@
+// C++ host mirror of STLQ's encoder interface on top of the libstlq_mi355 C ABI.
+//
+// The types and free functions below carry the reference's names, argument order and meaning
+// (include/stlq/common/types.h, include/stlq/quantizer/{encoder,beam_search,icm,least_squares,
+// cost_utils,precomp_large_root}.h) so that an EncodeBase-style caller can switch to the MI355X
+// encoder by changing a namespace. They live in stlq_mi355::stlq to avoid clashing with the
+// reference's own definitions when both are linked into one program.
+//
+// Device state: one context per host thread (thread_local, device 0 unless SetDevice is called
+// first). The codebook precomp is uploaded once per Precomp::build_tag, the way the reference's
+// CUDA sessions cache device copies (beam_search_cuda_api.inc:34, :244-245).
+//
+// Errors: the reference's CPU functions return void/bool and its CUDA paths throw
+// std::runtime_error (beam_search_cuda_kernels.inc:5-14); here every failure of the C ABI throws
+// std::runtime_error with the library's message.
+#pragma once
+
+#include <algorithm>
+#include <cstdint>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "stlq_mi355.h"
+
+namespace stlq_mi355 {
+namespace stlq {
+
+using Code = std::uint8_t;
+using FullCode = Code;
+
+template <typename T>
+struct ColMajorMatrix {  // include/stlq/common/types.h:35-51
+    int rows = 0;
+    int cols = 0;
+    std::vector<T> data;
+    ColMajorMatrix() = default;
+    ColMajorMatrix(int r, int c) : rows(r), cols(c), data(static_cast<std::size_t>(r) * c) {}
+    T* Col(int j) { return data.data() + static_cast<std::size_t>(j) * rows; }
+    const T* Col(int j) const { return data.data() + static_cast<std::size_t>(j) * rows; }
+    T& operator()(int i, int j) { return data[static_cast<std::size_t>(j) * rows + i]; }
+    const T& operator()(int i, int j) const { return data[static_cast<std::size_t>(j) * rows + i]; }
+};
+
+struct CodebookPack {  // types.h:53-60
+    int d = 0;
+    std::vector<int> h_vec;
+    std::vector<ColMajorMatrix<float>> books;
+    std::uint64_t build_tag = 0;
+};
+
+struct Precomp {  // types.h:62-75
+    ColMajorMatrix<float> C_all;
+    ColMajorMatrix<float> G;
+    std::vector<int> offsets;
+    std::vector<int> flat_layer;
+    std::vector<int> h_vec;
+    std::vector<float> invnorm_flat;
+    int H = 0;
+    int d = 0;
+    int m = 0;
+    std::uint64_t build_tag = 0;
+};
+
+struct BaseEncoding {  // types.h:77-80
+    ColMajorMatrix<FullCode> B;
+    ColMajorMatrix<float> a;
+};
+
+struct EncodeOptions {  // base.encode.* (config.h:473-482)
+    bool use_abs = true;
+    int H_beam = 2;
+    int ils_iters = 0;
+    int icm_iters = 4;
+    int perturb_k = 3;
+    int seed = 38251450;
+};
+
+namespace detail {
+
+inline void Check(int rc) {
+    if (rc != STLQ_MI355_OK) throw std::runtime_error(std::string("stlq_mi355: ") + stlq_mi355_last_error());
+}
+
+struct Session {
+    stlq_mi355_ctx* ctx = nullptr;
+    const void* owner = nullptr;     // Precomp bound to ctx
+    std::uint64_t tag = 0;
+    int d = 0;
+    const void* lr_owner = nullptr;  // PrecompLargeRoot bound to ctx
+    std::uint64_t lr_tag = 0;
+    ~Session() {
+        if (ctx) stlq_mi355_ctx_destroy(ctx);
+    }
+};
+
+inline int& DeviceOrdinal() {
+    static thread_local int dev = 0;
+    return dev;
+}
+
+inline Session& ThreadSession() {
+    static thread_local Session s;
+    if (!s.ctx) Check(stlq_mi355_ctx_create(DeviceOrdinal(), &s.ctx));
+    return s;
+}
+
+inline std::uint64_t NextBuildTag() {
+    static std::uint64_t tag = 0;
+    return ++tag;
+}
+
+// Uploads the precomp unless this thread's context already holds the one with this build tag.
+inline stlq_mi355_ctx* Bind(const Precomp& pre) {
+    Session& s = ThreadSession();
+    if (s.owner != &pre || s.tag != pre.build_tag || pre.build_tag == 0) {
+        Check(stlq_mi355_set_precomp(s.ctx, pre.d, pre.m, pre.h_vec.data(), pre.C_all.data.data(),
+                                     pre.G.data.data(), pre.invnorm_flat.data()));
+        s.owner = &pre;
+        s.tag = pre.build_tag;
+        s.d = pre.d;
+    }
+    return s.ctx;
+}
+
+}  // namespace detail
+
+// Selects the HIP device of the calling thread's context (before its first use).
+inline void SetDevice(int device) { detail::DeviceOrdinal() = device; }
+
+// BuildPrecomp (src/quantizer/encoder_precomp.inc:1-53): C_all, offsets, invnorm and
+// G = C_all^T C_all, computed on the device and copied back.
+inline bool BuildPrecomp(const CodebookPack& codebooks, Precomp* precomp) {
+    if (!precomp || codebooks.books.empty()) return false;
+    const int m = static_cast<int>(codebooks.books.size());
+    const int d = codebooks.books.front().rows;
+    Precomp& p = *precomp;
+    p.m = m;
+    p.d = d;
+    p.h_vec.clear();
+    p.offsets.assign(m, 0);
+    int H = 0;
+    for (int l = 0; l < m; ++l) {
+        p.offsets[l] = H;
+        p.h_vec.push_back(codebooks.books[l].cols);
+        H += codebooks.books[l].cols;
+    }
+    p.H = H;
+    p.C_all = ColMajorMatrix<float>(d, H);
+    p.flat_layer.assign(H, 0);
+    for (int l = 0; l < m; ++l) {
+        const auto& b = codebooks.books[l];
+        std::copy(b.data.begin(), b.data.end(), p.C_all.Col(p.offsets[l]));
+        for (int c = 0; c < b.cols; ++c) p.flat_layer[p.offsets[l] + c] = l;
+    }
+    p.G = ColMajorMatrix<float>(H, H);
+    p.invnorm_flat.assign(H, 0.0f);
+    detail::Session& s = detail::ThreadSession();
+    detail::Check(stlq_mi355_set_codebooks(s.ctx, d, m, p.h_vec.data(), p.C_all.data.data()));
+    detail::Check(stlq_mi355_get_precomp(s.ctx, p.G.data.data(), p.invnorm_flat.data()));
+    p.build_tag = detail::NextBuildTag();
+    s.owner = &p;
+    s.tag = p.build_tag;
+    s.d = d;
+    return true;
+}
+
+// ComputeXNorm2 (src/quantizer/cost_utils.cpp:88-110, cost_utils.h:12). The reference's
+// signature carries no precomp; the device routine runs on this thread's context, which must
+// already hold a Precomp (BuildPrecomp or any call that takes one) of dimension X.rows.
+inline void ComputeXNorm2(const ColMajorMatrix<float>& X, std::vector<float>* X_norm2) {
+    detail::Session& s = detail::ThreadSession();
+    if (!s.owner || s.d != X.rows)
+        throw std::runtime_error("stlq_mi355: ComputeXNorm2 needs a bound Precomp with d == X.rows");
+    X_norm2->resize(static_cast<std::size_t>(X.cols));
+    detail::Check(stlq_mi355_xnorm2(s.ctx, X.data.data(), X.cols, X_norm2->data()));
+}
+
+// xC = C_all^T X (StreamKernelProvider::Gemm call site, encoder_encode_base.inc:86-90).
+inline void ComputeXc(const Precomp& pre, const ColMajorMatrix<float>& X, ColMajorMatrix<float>* xC) {
+    *xC = ColMajorMatrix<float>(pre.H, X.cols);
+    detail::Check(stlq_mi355_gemm_xc(detail::Bind(pre), X.data.data(), X.cols, xC->data.data()));
+}
+
+// BeamSearchPrefixLS (src/quantizer/beam_search.cpp:196-422).
+inline void BeamSearchPrefixLS(const ColMajorMatrix<float>& X, const Precomp& precomp,
+                               const ColMajorMatrix<float>& xC, int H_beam, ColMajorMatrix<FullCode>* B) {
+    *B = ColMajorMatrix<FullCode>(precomp.m, X.cols);
+    detail::Check(stlq_mi355_beam_search(detail::Bind(precomp), X.data.data(), nullptr, xC.data.data(), X.cols,
+                                         std::max(1, H_beam), B->data.data(), nullptr));
+}
+
+// SolveLeastSquaresAll (src/quantizer/least_squares.cpp:406-565).
+inline void SolveLeastSquaresAll(const Precomp& precomp, const ColMajorMatrix<float>& xC,
+                                 const ColMajorMatrix<FullCode>& B, ColMajorMatrix<float>* a) {
+    *a = ColMajorMatrix<float>(precomp.m, B.cols);
+    int64_t fails = 0;
+    detail::Check(stlq_mi355_solve_ls_all(detail::Bind(precomp), xC.data.data(), B.data.data(), B.cols,
+                                          a->data.data(), &fails));
+}
+
+// ComputeCosts (src/quantizer/cost_utils.cpp:139-158).
+inline void ComputeCosts(const Precomp& precomp, const ColMajorMatrix<float>& xC, const ColMajorMatrix<FullCode>& B,
+                         const ColMajorMatrix<float>& a, const std::vector<float>& X_norm2,
+                         std::vector<float>* out_cost) {
+    out_cost->resize(static_cast<std::size_t>(B.cols));
+    detail::Check(stlq_mi355_compute_costs(detail::Bind(precomp), xC.data.data(), B.data.data(), a.data.data(),
+                                           X_norm2.data(), B.cols, out_cost->data()));
+}
+
+namespace detail {
+inline void DynamicIcm(const ColMajorMatrix<float>& X, const Precomp& precomp, const ColMajorMatrix<float>& xC,
+                       int icm_iters, int ils_iters, int perturb_k, std::uint32_t seed, bool use_abs,
+                       ColMajorMatrix<FullCode>* B, ColMajorMatrix<float>* a, std::vector<float>* X_norm2,
+                       std::vector<float>* cost) {
+    if (ils_iters > 0 && perturb_k > 0 && precomp.m > 1)
+        throw std::runtime_error("stlq_mi355: ILS (ils_iters > 0) is not part of this build");
+    stlq_mi355_ctx* ctx = Bind(precomp);
+    if (X_norm2 && X_norm2->empty()) ComputeXNorm2(X, X_norm2);
+    std::vector<float> cost_local;
+    std::vector<float>* c = cost ? cost : &cost_local;
+    c->resize(static_cast<std::size_t>(B->cols));
+    *a = ColMajorMatrix<float>(precomp.m, B->cols);
+    Check(stlq_mi355_icm(ctx, X.data.data(), X_norm2 ? X_norm2->data() : nullptr, xC.data.data(), B->cols,
+                         icm_iters, use_abs ? 1 : 0, seed, B->data.data(), a->data.data(), c->data()));
+}
+}  // namespace detail
+
+// DynamicIcmWithIlsAbsNoNormal / ...NoAbsNoNormal (src/quantizer/icm.cpp:1132-1170), ils_iters = 0.
+inline void DynamicIcmWithIlsAbsNoNormal(const ColMajorMatrix<float>& X, const Precomp& precomp,
+                                         const ColMajorMatrix<float>& xC, int icm_iters, int ils_iters, int perturb_k,
+                                         std::uint32_t seed, ColMajorMatrix<FullCode>* B, ColMajorMatrix<float>* a,
+                                         std::vector<float>* X_norm2, std::vector<float>* cost,
+                                         bool print_progress = true, std::uint64_t sample_id_offset = 0) {
+    (void)print_progress;
+    (void)sample_id_offset;  // only seeds ILS perturbations (icm.cpp:953-956)
+    detail::DynamicIcm(X, precomp, xC, icm_iters, ils_iters, perturb_k, seed, true, B, a, X_norm2, cost);
+}
+
+inline void DynamicIcmWithIlsNoAbsNoNormal(const ColMajorMatrix<float>& X, const Precomp& precomp,
+                                           const ColMajorMatrix<float>& xC, int icm_iters, int ils_iters,
+                                           int perturb_k, std::uint32_t seed, ColMajorMatrix<FullCode>* B,
+                                           ColMajorMatrix<float>* a, std::vector<float>* X_norm2,
+                                           std::vector<float>* cost, bool print_progress = true,
+                                           std::uint64_t sample_id_offset = 0) {
+    (void)print_progress;
+    (void)sample_id_offset;
+    detail::DynamicIcm(X, precomp, xC, icm_iters, ils_iters, perturb_k, seed, false, B, a, X_norm2, cost);
+}
+
+// EncodeBase (src/quantizer/encoder_encode_base.inc:1-106) without the ILS outer loop; the
+// whole pipeline (xC GEMM, beam, LS, ICM, costs) runs on the device.
+inline bool EncodeBase(const EncodeOptions& opt, const ColMajorMatrix<float>& Xb, const CodebookPack& codebooks,
+                       const Precomp& precomp, BaseEncoding* base, float* out_beam_mse, float* out_final_mse,
+                       std::string* error) {
+    if (!base) {
+        if (error) *error = "BaseEncoding output is null.";
+        return false;
+    }
+    if (Xb.rows <= 0 || Xb.cols <= 0) {
+        if (error) *error = "Empty base dataset.";
+        return false;
+    }
+    if (precomp.d != Xb.rows || precomp.m != static_cast<int>(codebooks.books.size())) {
+        if (error) *error = "Precomp dimensions do not match codebooks or dataset.";
+        return false;
+    }
+    if (opt.ils_iters > 0 && opt.perturb_k > 0 && precomp.m > 1) {
+        if (error) *error = "ILS (ils_iters > 0) is not part of this build.";
+        return false;
+    }
+    stlq_mi355_encode_params p{std::max(1, opt.H_beam), opt.icm_iters, 0, opt.perturb_k, opt.use_abs ? 1 : 0,
+                               static_cast<std::uint32_t>(opt.seed), 1};
+    base->B = ColMajorMatrix<FullCode>(precomp.m, Xb.cols);
+    base->a = ColMajorMatrix<float>(precomp.m, Xb.cols);
+    double bm = 0.0, fm = 0.0;
+    const int rc = stlq_mi355_encode(detail::Bind(precomp), Xb.data.data(), Xb.cols, &p, base->B.data.data(),
+                                     base->a.data.data(), nullptr, &bm, &fm);
+    if (rc != STLQ_MI355_OK) {
+        if (error) *error = stlq_mi355_last_error();
+        return false;
+    }
+    if (out_beam_mse) *out_beam_mse = static_cast<float>(bm);
+    if (out_final_mse) *out_final_mse = static_cast<float>(fm);
+    return true;
+}
+
+class StreamKernelProvider;  // the reference's GEMM provider; unused here (the device runs the GEMMs)
+
+struct PrecompLargeRootBuildOptions {  // precomp_large_root.h:40-47 (CPU-only options)
+    bool build_g0s_transpose = false;
+    int g0s_transpose_max_mb = 0;
+};
+
+// PrecompLargeRoot (precomp_large_root.h:12-39). norm0, G_small, invnorm_small_flat and G0S are
+// computed on the device and stay there; the host copies of those members remain empty.
+struct PrecompLargeRoot {
+    int d = 0;
+    int m = 0;
+    std::vector<int> h_vec;
+    std::vector<int> offsets;
+    std::uint64_t build_tag = 0;
+    ColMajorMatrix<float> C0;
+    std::vector<float> norm0;
+    int H_small = 0;
+    std::vector<int> small_offsets;
+    ColMajorMatrix<float> C_small;
+    ColMajorMatrix<float> G_small;
+    std::vector<float> invnorm_small_flat;
+    ColMajorMatrix<float> G0S;
+    ColMajorMatrix<float> G0S_T;
+    bool ready = false;
+};
+
+struct BeamSearchLargeRootTiming {  // beam_search.h:11-16
+    double norm_x2 = 0.0;
+    double root_gemm = 0.0;
+    double root_update = 0.0;
+    double expand = 0.0;
+};
+
+namespace detail {
+inline stlq_mi355_ctx* BindLargeRoot(const PrecompLargeRoot& pre) {
+    if (!pre.ready) throw std::runtime_error("stlq_mi355: PrecompLargeRoot is not built");
+    Session& s = ThreadSession();
+    if (s.lr_owner != &pre || s.lr_tag != pre.build_tag || pre.build_tag == 0) {
+        Check(stlq_mi355_set_large_root(s.ctx, pre.d, pre.m, pre.h_vec.data(), pre.C0.data.data(),
+                                        pre.C_small.data.data()));
+        s.lr_owner = &pre;
+        s.lr_tag = pre.build_tag;
+    }
+    return s.ctx;
+}
+}  // namespace detail
+
+// BuildPrecompLargeRoot (src/quantizer/precomp_large_root.cpp:27-157): layer 0 of C_root is
+// the large root codebook, layers 1..m-1 the small ones (at most 256 codewords each).
+inline bool BuildPrecompLargeRoot(const CodebookPack& C_root, StreamKernelProvider* kernels,
+                                  const PrecompLargeRootBuildOptions& opts, PrecompLargeRoot* out,
+                                  std::string* err) {
+    (void)kernels;
+    (void)opts;
+    if (!out || C_root.books.size() < 2) {
+        if (err) *err = "large-root precomp needs a root and at least one small codebook";
+        return false;
+    }
+    PrecompLargeRoot& p = *out;
+    p = PrecompLargeRoot();
+    p.m = static_cast<int>(C_root.books.size());
+    p.d = C_root.books.front().rows;
+    int H = 0;
+    for (int l = 0; l < p.m; ++l) {
+        p.offsets.push_back(H);
+        p.h_vec.push_back(C_root.books[l].cols);
+        H += C_root.books[l].cols;
+    }
+    p.C0 = C_root.books[0];
+    p.small_offsets.assign(p.m, 0);
+    for (int l = 1; l < p.m; ++l) {
+        p.small_offsets[l] = p.H_small;
+        p.H_small += p.h_vec[l];
+    }
+    p.C_small = ColMajorMatrix<float>(p.d, p.H_small);
+    for (int l = 1; l < p.m; ++l) {
+        const auto& b = C_root.books[l];
+        std::copy(b.data.begin(), b.data.end(), p.C_small.Col(p.small_offsets[l]));
+    }
+    p.ready = true;
+    p.build_tag = detail::NextBuildTag();
+    try {
+        detail::Session& s = detail::ThreadSession();
+        const int rc = stlq_mi355_set_large_root(s.ctx, p.d, p.m, p.h_vec.data(), p.C0.data.data(),
+                                                 p.C_small.data.data());
+        if (rc != STLQ_MI355_OK) {
+            if (err) *err = stlq_mi355_last_error();
+            p.ready = false;
+            return false;
+        }
+        s.lr_owner = &p;
+        s.lr_tag = p.build_tag;
+    } catch (const std::exception& e) {
+        if (err) *err = e.what();
+        p.ready = false;
+        return false;
+    }
+    return true;
+}
+
+// BeamSearchPrefixLSLargeRoot (src/quantizer/beam_search.cpp:579-726, beam_search.h:26-32).
+// An empty xC_small (rows == 0) has the device compute C_small^T X itself.
+inline void BeamSearchPrefixLSLargeRoot(const ColMajorMatrix<float>& X, const PrecompLargeRoot& pre,
+                                        const ColMajorMatrix<float>& xC_small, int H_beam,
+                                        std::vector<std::uint32_t>* cluster_id, ColMajorMatrix<Code>* B_small,
+                                        BeamSearchLargeRootTiming* timing = nullptr) {
+    stlq_mi355_ctx* ctx = detail::BindLargeRoot(pre);
+    cluster_id->assign(static_cast<std::size_t>(X.cols), 0u);
+    *B_small = ColMajorMatrix<Code>(pre.m - 1, X.cols);
+    const float* xcs = xC_small.rows > 0 ? xC_small.data.data() : nullptr;
+    detail::Check(stlq_mi355_beam_search_large_root(ctx, X.data.data(), xcs, X.cols, std::max(1, H_beam), nullptr, 0,
+                                                    cluster_id->data(), B_small->data.data(), nullptr));
+    if (timing) {
+        stlq_mi355_timings t{};
+        detail::Check(stlq_mi355_last_timings(ctx, &t));
+        timing->norm_x2 = 0.0;
+        timing->root_gemm = t.gemm_ms * 1e-3;
+        timing->root_update = 0.0;
+        timing->expand = t.beam_ms * 1e-3;
+    }
+}
+
+}  // namespace stlq
+}  // namespace stlq_mi355

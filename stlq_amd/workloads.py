@@ -150,17 +150,15 @@ def make_large_root(w: Workload, h0: int, n_small: int, X_train: np.ndarray | No
     """Root codebook (h0 codewords = distinct training samples) and n_small residual codebooks
     trained on the residual to the nearest root."""
     mix = Mixture(w.kind, w.d, w.n_comp, w.seed)
-    rng = np.random.default_rng(w.seed + 9)
     C0 = mix.sample(20_000_000, h0)
     if X_train is None:
         X_train = mix.sample(10_000_000, w.train_n)
     # nearest root by ||x - c||^2 for the residual codebooks
     lab = np.empty(X_train.shape[0], np.int64)
-    c2 = np.sum(C0.astype(np.float64) ** 2, axis=1)
+    c2 = np.sum(C0.astype(np.float64) ** 2, axis=1).astype(np.float32)
     for b0 in range(0, X_train.shape[0], 2048):
-        xb = X_train[b0:b0 + 2048].astype(np.float64)
-        lab[b0:b0 + 2048] = np.argmax(2.0 * xb @ C0.T.astype(np.float64) - c2[None, :], axis=1)
+        xb = X_train[b0:b0 + 2048]
+        lab[b0:b0 + 2048] = np.argmax(2.0 * (xb @ C0.T) - c2[None, :], axis=1)
     R = (X_train - C0[lab]).astype(np.float32)
     Cs = residual_codebooks(R, n_small, w.K, w.kmeans_iters, w.seed + 77)
-    del rng
     return C0, Cs

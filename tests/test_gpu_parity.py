@@ -422,3 +422,26 @@ def test_stream_large_root_u8_matches_in_memory(ctx, chunk):
     assert np.array_equal(got["cluster_id"], cid)
     assert np.array_equal(got["B_small"], Bs)
     assert np.array_equal(_bits(got["best_err"]), _bits(err))
+
+
+def test_stream_chunk_larger_than_workspace(ctx, monkeypatch):
+    """A streamed chunk bigger than the workspace budget is encoded in tiles, with identical results."""
+    from stlq_amd import workloads
+
+    mix = workloads.Mixture("desc", 32, 64, 91)
+    X = mix.sample(0, 6000)
+    C = workloads.residual_codebooks(mix.sample(1_000_000, 2000), 4, 64, 3, 4)
+    ctx.set_codebooks(C, [64] * 4)
+    cfg = EncodeConfig(H_beam=4, icm_iters=1, want_coeffs=True)
+    codes, a, cost, _ = ctx.encode(X, cfg)
+    monkeypatch.setenv("STLQ_MI355_WORKSPACE_GB", "0.0005")
+    got = np.zeros_like(codes)
+
+    def fill(first, count, out):
+        out[:] = X[first:first + count]
+
+    def sink(first, count, res):
+        got[first:first + count] = res["codes"]
+
+    ctx.encode_stream(6000, 6000, cfg, fill, sink)
+    assert np.array_equal(codes, got)

@@ -1,0 +1,111 @@
+"""The C++ host mirror of the reference's encoder interface (stlq_amd/host/stlq_mi355.hpp).
+
+tests/host_mirror_check.cpp drives the reference-named functions (BuildPrecomp, BeamSearchPrefixLS,
+ComputeXNorm2, DynamicIcmWithIls*NoNormal, EncodeBase, BuildPrecompLargeRoot,
+BeamSearchPrefixLSLargeRoot) on arrays handed over from here; the GPU tests compare what they
+return with the oracle, bit for bit, so a transposed operand or a misplaced argument in the
+mirror's plumbing fails them.
+"""
+import ctypes
+import os
+
+import numpy as np
+import pytest
+
+from tests.helpers import rvq_problem
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HOSTCHECK = os.path.join(ROOT, "stlq_amd", "lib", "libstlq_mi355_hostcheck.so")
+
+_f32p = ctypes.POINTER(ctypes.c_float)
+_u8p = ctypes.POINTER(ctypes.c_uint8)
+_u32p = ctypes.POINTER(ctypes.c_uint32)
+_i32p = ctypes.POINTER(ctypes.c_int32)
+
+
+def _lib():
+    if not os.path.exists(HOSTCHECK):
+        pytest.fail(f"{HOSTCHECK} is not built (python -c 'import __graft_entry__ as g; g.build()')")
+    lib = ctypes.CDLL(HOSTCHECK)
+    lib.mirror_encode.restype = ctypes.c_int
+    lib.mirror_encode.argtypes = [ctypes.c_int, ctypes.c_int, _i32p, _f32p, _f32p, ctypes.c_int, ctypes.c_int,
+                                  ctypes.c_int, ctypes.c_int, ctypes.c_uint32, _f32p, _u8p, _u8p, _f32p, _f32p,
+                                  _f32p, ctypes.c_char_p, ctypes.c_int]
+    lib.mirror_large_root.restype = ctypes.c_int
+    lib.mirror_large_root.argtypes = [ctypes.c_int, ctypes.c_int, _i32p, _f32p, _f32p, _f32p, ctypes.c_int,
+                                      ctypes.c_int, _u32p, _u8p, ctypes.c_char_p, ctypes.c_int]
+    return lib
+
+
+def _p(a, t):
+    return a.ctypes.data_as(t)
+
+
+def _bits(a):
+    return np.ascontiguousarray(a).view(np.uint32)
+
+
+def test_hostcheck_library_loads():
+    lib = _lib()
+    assert lib.mirror_encode is not None and lib.mirror_large_root is not None
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("icm_iters,use_abs", [(0, 1), (2, 1), (2, 0)])
+def test_mirror_encode_matches_oracle(orc, icm_iters, use_abs):
+    n, d, m, K, Hb, seed = 3000, 48, 5, 64, 6, 38251450
+    X, C = rvq_problem(71 + icm_iters + use_abs, n, d, m, K)
+    h = np.full(m, K, np.int32)
+    G = np.empty((C.shape[0], C.shape[0]), np.float32)
+    cb = np.empty((n, m), np.uint8)
+    cf = np.empty((n, m), np.uint8)
+    a = np.empty((n, m), np.float32)
+    cost = np.empty(n, np.float32)
+    mse = np.empty(2, np.float32)
+    err = ctypes.create_string_buffer(512)
+    C = np.ascontiguousarray(C, np.float32)
+    X = np.ascontiguousarray(X, np.float32)
+    print(f"mirror_encode n={n} d={d} m={m} K={K} beam={Hb} icm={icm_iters} abs={use_abs}", flush=True)
+    rc = _lib().mirror_encode(d, m, _p(h, _i32p), _p(C, _f32p), _p(X, _f32p), n, Hb, icm_iters, use_abs, seed,
+                              _p(G, _f32p), _p(cb, _u8p), _p(cf, _u8p), _p(a, _f32p), _p(cost, _f32p),
+                              _p(mse, _f32p), err, 512)
+    assert rc == 0, err.value.decode()
+    G_o, inv_o = orc.build_precomp(C, h)
+    assert np.array_equal(_bits(G_o), _bits(G))
+    nx2 = orc.xnorm2(X)
+    xC = orc.gemm_xc(C, X, mode=1)
+    codes_o, _ = orc.beam_search(nx2, xC, G_o, h, Hb)
+    assert np.array_equal(codes_o, cb)
+    codes_f, a_o, cost_o, _ = orc.icm(xC, G_o, inv_o, h, nx2, codes_o, icm_iters, use_abs, seed)
+    assert np.array_equal(codes_f, cf)
+    assert np.array_equal(_bits(a_o), _bits(a))
+    assert np.array_equal(_bits(cost_o), _bits(cost))
+    want = np.float32(np.mean(np.maximum(cost_o.astype(np.float64), 0.0)))
+    assert abs(mse[1] - want) <= 1e-6 * abs(want)
+
+
+@pytest.mark.gpu
+def test_mirror_large_root_matches_oracle(orc):
+    from stlq_amd import workloads
+
+    n, d, h0, K, m, Hb, seed = 2000, 32, 1500, 64, 4, 8, 93
+    mix = workloads.Mixture("desc", d, 256, seed)
+    rng = np.random.default_rng(seed)
+    C0 = mix.sample(5_000_000, h0)
+    Xtr = mix.sample(1_000_000, 3000)
+    Cs = workloads.residual_codebooks(Xtr - C0[rng.integers(0, h0, 3000)], m - 1, K, 3, seed + 1)
+    X = mix.sample(0, n)
+    h = np.array([h0] + [K] * (m - 1), np.int32)
+    cid = np.empty(n, np.uint32)
+    Bs = np.empty((n, m - 1), np.uint8)
+    err = ctypes.create_string_buffer(512)
+    print(f"mirror_large_root n={n} d={d} h0={h0} K={K} m={m} beam={Hb}", flush=True)
+    rc = _lib().mirror_large_root(d, m, _p(h, _i32p), _p(C0, _f32p), _p(Cs, _f32p), _p(X, _f32p), n, Hb,
+                                  _p(cid, _u32p), _p(Bs, _u8p), err, 512)
+    assert rc == 0, err.value.decode()
+    norm0, Gs, G0S = orc.build_precomp_large_root(C0, Cs)
+    nx2 = orc.xnorm2(X)
+    xs = orc.gemm_xc(Cs, X, mode=1)
+    cid_o, Bs_o, _ = orc.beam_search_large_root(X, nx2, C0, norm0, xs, Gs, G0S, list(h), Hb)
+    assert np.array_equal(cid_o, cid)
+    assert np.array_equal(Bs_o, Bs)
