@@ -62,6 +62,8 @@ def lib():
         L.orc_beam_search_large_root.argtypes = [_f32p, _int, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p,
                                                  _int, _int, _int, _i32p, _int, _i64, _u32p, _int,
                                                  _u32p, _u8p, _f32p, _int]
+        L.orc_large_root_candidates.argtypes = [_f32p, _int, _f32p, _f32p, _f32p, _int, _int, _i64, _u32p, _int,
+                                                _f32p, _i32p, _f32p, _f32p, _int]
         _lib = L
     return _lib
 
@@ -228,3 +230,22 @@ def beam_search_large_root(X, nx2, C0, norm0, xC_small, G_small, G0S, h_vec, H_b
                                      _p(hv, _i32p), H_beam, n, _p(fr, _u32p), root_mode, _p(cid, _u32p),
                                      _p(Bs, _u8p), _p(err, _f32p), nthreads)
     return cid, Bs, err
+
+
+def large_root_candidates(X, nx2, C0, norm0, H_beam, forced_root=None, root_mode=0, nthreads=0):
+    """Root stage of the large-root beam: [n, H_beam] arrays (errs, codes, a0, r00) in the
+    layout of ExpandFromRootCandidates; unused slots have error +inf."""
+    X = _c(X, np.float32)
+    nx2 = _c(nx2, np.float32)
+    C0 = _c(C0, np.float32)
+    norm0 = _c(norm0, np.float32)
+    n, d = X.shape
+    fr = _c(forced_root, np.uint32) if forced_root is not None else None
+    errs = np.empty((n, H_beam), np.float32)
+    codes = np.empty((n, H_beam), np.int32)
+    a0 = np.empty((n, H_beam), np.float32)
+    r00 = np.empty((n, H_beam), np.float32)
+    lib().orc_large_root_candidates(_p(X, _f32p), d, _p(nx2, _f32p), _p(C0, _f32p), _p(norm0, _f32p), C0.shape[0],
+                                    H_beam, n, _p(fr, _u32p), root_mode, _p(errs, _f32p), _p(codes, _i32p),
+                                    _p(a0, _f32p), _p(r00, _f32p), nthreads)
+    return errs, codes, a0, r00

@@ -1,0 +1,123 @@
+"""ctypes access to the reference's own CPU encoder functions, compiled from the reference
+sources in place by `make -C oracle ref` into oracle/_ref/libstlq_ref.so (see ref_driver.cpp).
+
+TEST INFRASTRUCTURE ONLY: tests use it to check the oracle restatement against the reference;
+the product never loads it. Where the reference sources are absent the library cannot be built
+and available() is False.
+
+Array conventions follow the oracle's: numpy row-major (n, d) == the reference's column-major
+d x n, (n, H) == H x n, codes (n, m) == m x n.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "_ref", "libstlq_ref.so")
+REF_ROOT = os.environ.get("STLQ_REFERENCE_ROOT", "/root/reference")
+_lib = None
+
+_f32p = ctypes.POINTER(ctypes.c_float)
+_i32p = ctypes.POINTER(ctypes.c_int32)
+_u8p = ctypes.POINTER(ctypes.c_uint8)
+_u32p = ctypes.POINTER(ctypes.c_uint32)
+_int = ctypes.c_int
+
+
+def sources_present() -> bool:
+    return os.path.exists(os.path.join(REF_ROOT, "src", "quantizer", "beam_search.cpp"))
+
+
+def build() -> str:
+    """make -C oracle ref (g++ on the reference's own translation units)."""
+    subprocess.run(["make", "-s", "-C", _HERE, "ref", f"REF={REF_ROOT}"], check=True)
+    return _LIB_PATH
+
+
+def available() -> bool:
+    return os.path.exists(_LIB_PATH)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        # Lazy binding: GemmRaw/BlasSetThreads (blas.cpp, not buildable here) stay unresolved and
+        # are never reached by the driver's entry points.
+        L = ctypes.CDLL(_LIB_PATH, mode=os.RTLD_LAZY)
+        L.ref_xnorm2.argtypes = [_f32p, _int, _int, _f32p]
+        L.ref_beam_search.argtypes = [_f32p, _int, _int, _f32p, _f32p, _int, _i32p, _int, _int, _u8p]
+        L.ref_compute_costs.argtypes = [_f32p, _f32p, _int, _i32p, _int, _u8p, _f32p, _f32p, _int, _f32p]
+        L.ref_expand_large_root.argtypes = [_f32p, _int, _f32p, _int, _i32p, _int, _f32p, _int, _int, _f32p,
+                                            _i32p, _f32p, _f32p, _u32p, _u8p]
+        for f in (L.ref_xnorm2, L.ref_beam_search, L.ref_compute_costs, L.ref_expand_large_root):
+            f.restype = None
+        _lib = L
+    return _lib
+
+
+def _c(a, dt):
+    return np.ascontiguousarray(a, dtype=dt)
+
+
+def _p(a, t):
+    return a.ctypes.data_as(t)
+
+
+def xnorm2(X):
+    X = _c(X, np.float32)
+    n, d = X.shape
+    out = np.empty(n, np.float32)
+    lib().ref_xnorm2(_p(X, _f32p), d, n, _p(out, _f32p))
+    return out
+
+
+def beam_search(X, xC, G, h_vec, H_beam):
+    """stlq::BeamSearchPrefixLS; ||x||^2 is formed inside from X."""
+    X = _c(X, np.float32)
+    xC = _c(xC, np.float32)
+    G = _c(G, np.float32)
+    hv = _c(h_vec, np.int32)
+    n, d = X.shape
+    H = G.shape[0]
+    m = len(hv)
+    codes = np.empty((n, m), np.uint8)
+    lib().ref_beam_search(_p(X, _f32p), d, n, _p(xC, _f32p), _p(G, _f32p), H, _p(hv, _i32p), m, H_beam,
+                          _p(codes, _u8p))
+    return codes
+
+
+def compute_costs(xC, G, h_vec, codes, a, nx2):
+    xC = _c(xC, np.float32)
+    G = _c(G, np.float32)
+    hv = _c(h_vec, np.int32)
+    codes = _c(codes, np.uint8)
+    a = _c(a, np.float32)
+    nx2 = _c(nx2, np.float32)
+    n, H = xC.shape
+    cost = np.empty(n, np.float32)
+    lib().ref_compute_costs(_p(xC, _f32p), _p(G, _f32p), H, _p(hv, _i32p), len(hv), _p(codes, _u8p), _p(a, _f32p),
+                            _p(nx2, _f32p), n, _p(cost, _f32p))
+    return cost
+
+
+def expand_large_root(G_small, G0S, h_vec, xC_small, H_beam, root_errs, root_codes, root_a0, root_r00):
+    """stlq::BeamSearchPrefixLSLargeRootExpandFromRootCandidates over all vectors.
+    G0S as the oracle returns it: numpy (Hs, h0) == the reference's h0 x Hs column-major."""
+    G_small = _c(G_small, np.float32)
+    G0S = _c(G0S, np.float32)
+    hv = _c(h_vec, np.int32)
+    xs = _c(xC_small, np.float32)
+    n, Hs = xs.shape
+    h0 = G0S.shape[1]
+    m = len(hv)
+    cid = np.empty(n, np.uint32)
+    Bs = np.empty((n, m - 1), np.uint8)
+    lib().ref_expand_large_root(_p(G_small, _f32p), Hs, _p(G0S, _f32p), h0, _p(hv, _i32p), m, _p(xs, _f32p), n,
+                                H_beam, _p(_c(root_errs, np.float32), _f32p), _p(_c(root_codes, np.int32), _i32p),
+                                _p(_c(root_a0, np.float32), _f32p), _p(_c(root_r00, np.float32), _f32p),
+                                _p(cid, _u32p), _p(Bs, _u8p))
+    return cid, Bs

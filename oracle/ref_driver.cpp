@@ -1,0 +1,118 @@
+// Test infrastructure: a C-ABI driver around the reference's own CPU encoder functions, compiled
+// from the reference sources where they lie (oracle/Makefile, target `ref`) into
+// oracle/_ref/libstlq_ref.so. Tests use it to check the oracle restatement against the real
+// reference; nothing in the product links or loads it.
+//
+// Compiled with the reference's translation units
+//   src/quantizer/beam_search.cpp, linear_algebra.cpp, cost_utils.cpp, src/common/timer.cpp
+// blas.cpp is not buildable here (it includes cblas.h, which the image lacks), so GemmRaw and
+// BlasSetThreads stay unresolved. They are only reached from the root-score GEMM of
+// BeamSearchPrefixLSLargeRoot (beam_search.cpp:623-690), which this driver never calls; the
+// library is loaded with lazy binding.
+//
+// Array conventions (all column-major as in the reference's ColMajorMatrix):
+//   X d x n, xC H x n, G H x H, codes m x n (uint8), a m x n.
+#include <cstdint>
+#include <cstring>
+#include <vector>
+
+#include "stlq/common/types.h"
+#include "stlq/quantizer/beam_search.h"
+#include "stlq/quantizer/cost_utils.h"
+#include "stlq/quantizer/precomp_large_root.h"
+
+namespace {
+
+stlq::Precomp MakePrecomp(const float* G, int H, const int* h_vec, int m, int d) {
+    stlq::Precomp p;
+    p.m = m;
+    p.d = d;
+    p.H = H;
+    p.h_vec.assign(h_vec, h_vec + m);
+    int off = 0;
+    for (int l = 0; l < m; ++l) {
+        p.offsets.push_back(off);
+        for (int k = 0; k < h_vec[l]; ++k) p.flat_layer.push_back(l);
+        off += h_vec[l];
+    }
+    p.G = stlq::ColMajorMatrix<float>(H, H);
+    std::memcpy(p.G.data.data(), G, sizeof(float) * static_cast<std::size_t>(H) * H);
+    return p;
+}
+
+template <typename T>
+stlq::ColMajorMatrix<T> Wrap(const T* src, int rows, int cols) {
+    stlq::ColMajorMatrix<T> M(rows, cols);
+    if (src) std::memcpy(M.data.data(), src, sizeof(T) * M.data.size());
+    return M;
+}
+
+}  // namespace
+
+extern "C" {
+
+// stlq::ComputeXNorm2 (cost_utils.cpp:88-110).
+void ref_xnorm2(const float* X, int d, int n, float* out) {
+    const auto Xm = Wrap(X, d, n);
+    std::vector<float> v;
+    stlq::ComputeXNorm2(Xm, &v);
+    std::memcpy(out, v.data(), sizeof(float) * static_cast<std::size_t>(n));
+}
+
+// stlq::BeamSearchPrefixLS (beam_search.cpp:196-422); ||x||^2 is computed inside from X.
+void ref_beam_search(const float* X, int d, int n, const float* xC, const float* G, int H, const int* h_vec, int m,
+                     int H_beam, uint8_t* codes) {
+    const auto pre = MakePrecomp(G, H, h_vec, m, d);
+    const auto Xm = Wrap(X, d, n);
+    const auto xCm = Wrap(xC, H, n);
+    stlq::ColMajorMatrix<stlq::FullCode> B;
+    stlq::BeamSearchPrefixLS(Xm, pre, xCm, H_beam, &B);
+    std::memcpy(codes, B.data.data(), B.data.size());
+}
+
+// stlq::ComputeCosts (cost_utils.cpp:139-158).
+void ref_compute_costs(const float* xC, const float* G, int H, const int* h_vec, int m, const uint8_t* codes,
+                       const float* a, const float* nx2, int n, float* cost) {
+    const auto pre = MakePrecomp(G, H, h_vec, m, 0);
+    const auto xCm = Wrap(xC, H, n);
+    const auto B = Wrap(codes, m, n);
+    const auto am = Wrap(a, m, n);
+    const std::vector<float> xn(nx2, nx2 + n);
+    std::vector<float> out;
+    stlq::ComputeCosts(pre, xCm, B, am, xn, &out);
+    std::memcpy(cost, out.data(), sizeof(float) * static_cast<std::size_t>(n));
+}
+
+// stlq::BeamSearchPrefixLSLargeRootExpandFromRootCandidates (beam_search.cpp:728-992) for all
+// n vectors. G_small Hs x Hs, G0S h0 x Hs, xC_small Hs x n; root_* are [n, H_beam] row-major.
+void ref_expand_large_root(const float* G_small, int Hs, const float* G0S, int h0, const int* h_vec, int m,
+                           const float* xC_small, int n, int H_beam, const float* root_errs, const int* root_codes,
+                           const float* root_a0, const float* root_r00, uint32_t* cluster_id, uint8_t* B_small) {
+    stlq::PrecompLargeRoot pre;
+    pre.m = m;
+    pre.h_vec.assign(h_vec, h_vec + m);
+    int off = 0;
+    for (int l = 0; l < m; ++l) {
+        pre.offsets.push_back(off);
+        off += h_vec[l];
+    }
+    pre.H_small = Hs;
+    pre.small_offsets.assign(m, 0);
+    int so = 0;
+    for (int l = 1; l < m; ++l) {
+        pre.small_offsets[l] = so;
+        so += h_vec[l];
+    }
+    pre.G_small = Wrap(G_small, Hs, Hs);
+    pre.G0S = Wrap(G0S, h0, Hs);
+    pre.ready = true;
+    const auto xs = Wrap(xC_small, Hs, n);
+    std::vector<std::uint32_t> cid(static_cast<std::size_t>(n), 0u);  // the callee writes, not resizes
+    stlq::ColMajorMatrix<stlq::Code> Bs(m - 1, n);
+    stlq::BeamSearchPrefixLSLargeRootExpandFromRootCandidates(pre, xs, 0, n, H_beam, root_errs, root_codes, root_a0,
+                                                             root_r00, &cid, &Bs);
+    std::memcpy(cluster_id, cid.data(), sizeof(uint32_t) * static_cast<std::size_t>(n));
+    std::memcpy(B_small, Bs.data.data(), Bs.data.size());
+}
+
+}  // extern "C"

@@ -13,8 +13,13 @@
 //    (src/core/blas.cpp:33-54, un-vendored BLAS), whose summation order is unpinned. Here G is
 //    a sequential mul+add dot product (exactly symmetric), and xC is either sequential mul+add
 //    (mode 0) or a fused k-ordered accumulation (mode 1), the order of the device GEMM.
-//  * ||x||^2 uses an `omp simd` reduction of unspecified order in the reference
-//    (beam_search.cpp:218-223, cost_utils.cpp:88-110); here it is a sequential sum.
+//  * ||x||^2 and the large-root ||c0||^2 are `omp simd` reductions in the reference
+//    (beam_search.cpp:218-223, :629-633, cost_utils.cpp:99-109, precomp_large_root.cpp:14-23).
+//    OpenMP leaves their order open; the reference's own Release build (GCC, -O3 -fopenmp, no
+//    -march, so SSE2 with 4 float lanes) sums element t into lane t mod 4 over the first
+//    floor(d/4)*4 elements, adds the remaining elements to lane 0, and then adds the lanes in
+//    order to the initial 0. SimdLane4SumSq restates that order; it was checked bit for bit
+//    against that build for d = 1..131 (tests/test_ref_cpu.py).
 //  * SolveLeastSquaresAll for m not in {5,10} calls LAPACK spotrf/spotrs
 //    (least_squares.cpp:512-564); here every m uses the hand-written Cholesky of
 //    least_squares.cpp:44-84, with LAPACK's failure test (pivot <= 0 or NaN) for m not in
@@ -357,6 +362,25 @@ inline float SampleCost(const float* xCi, const float* G, int H, int m, const in
 // This is the accumulation order of the device GEMM (v_mfma_f32_16x16x4_f32 issued over
 // ascending k: each product is fused into the running fp32 sum), so xC and root scores computed
 // here match the device bit for bit. The reference's own order is BLAS's (unpinned).
+// Sum of squares in the reference build's OpenMP-simd order (see the file comment).
+inline float SimdLane4SumSq(const float* x, int d) {
+    float p0 = 0.0f, p1 = 0.0f, p2 = 0.0f, p3 = 0.0f;
+    const int d4 = d & ~3;
+    for (int t = 0; t < d4; t += 4) {
+        p0 += x[t] * x[t];
+        p1 += x[t + 1] * x[t + 1];
+        p2 += x[t + 2] * x[t + 2];
+        p3 += x[t + 3] * x[t + 3];
+    }
+    for (int t = d4; t < d; ++t) p0 += x[t] * x[t];
+    float s = 0.0f;
+    s += p0;
+    s += p1;
+    s += p2;
+    s += p3;
+    return s;
+}
+
 __attribute__((target("fma"))) inline float FusedDot(const float* c, const float* x, int d) {
     float s = 0.0f;
     for (int r = 0; r < d; ++r) s = std::fma(c[r], x[r], s);
@@ -365,6 +389,47 @@ __attribute__((target("fma"))) inline float FusedDot(const float* c, const float
 
 __attribute__((target("fma"))) void FusedDots(const float* C, int d, int H, const float* x, float* out) {
     for (int f = 0; f < H; ++f) out[f] = FusedDot(C + static_cast<std::size_t>(f) * d, x, d);
+}
+
+// Root candidates of one vector (beam_search.cpp:639-709): streaming top-`slots` over the root
+// codes in ascending order, or the one given root (a forced root is a single finite slot).
+// Root scores <c0_code, x> come from GemmRaw in the reference (beam_search.cpp:665); here they
+// are the fused k-ordered dot of the device's root GEMM.
+void RootCandidates(const float* x, int d, float nx2, const float* C0, const float* norm0, int h0, int slots,
+                    const uint32_t* forced, float* rerr, int* rcode, float* ra0, float* rr00) {
+    std::fill(rerr, rerr + slots, kInf);
+    std::fill(rcode, rcode + slots, 0);
+    std::fill(ra0, ra0 + slots, 0.0f);
+    std::fill(rr00, rr00 + slots, 0.0f);
+    auto root_score = [&](int code) { return FusedDot(C0 + static_cast<std::size_t>(code) * d, x, d); };
+    if (forced) {
+        const int code = static_cast<int>(*forced);
+        const float alpha = norm0[code];
+        if (alpha != 0.0f) {
+            const float gamma = root_score(code);
+            const float a1 = gamma / alpha;
+            rerr[0] = nx2 - gamma * a1;
+            rcode[0] = code;
+            ra0[0] = a1;
+            rr00[0] = std::sqrt(alpha);
+        }
+        return;
+    }
+    float worst;
+    int wi = FirstMaxSlot(rerr, slots, &worst);
+    for (int code = 0; code < h0; ++code) {
+        const float alpha = norm0[code];
+        if (alpha == 0.0f) continue;
+        const float gamma = root_score(code);
+        const float a1 = gamma / alpha;
+        const float e1 = nx2 - gamma * a1;
+        if (e1 >= worst) continue;
+        rerr[wi] = e1;
+        rcode[wi] = code;
+        ra0[wi] = a1;
+        rr00[wi] = std::sqrt(alpha);
+        wi = FirstMaxSlot(rerr, slots, &worst);
+    }
 }
 
 }  // namespace
@@ -403,10 +468,7 @@ void orc_xnorm2(const float* X, int d, int64_t n, float* out, int nthreads) {
     SetThreads(nthreads);
     #pragma omp parallel for schedule(static)
     for (int64_t i = 0; i < n; ++i) {
-        const float* x = X + static_cast<std::size_t>(i) * d;
-        float s = 0.0f;
-        for (int t = 0; t < d; ++t) s += x[t] * x[t];
-        out[i] = s;
+        out[i] = SimdLane4SumSq(X + static_cast<std::size_t>(i) * d, d);
     }
 }
 
@@ -705,13 +767,8 @@ void orc_mse_fp64_refit(const float* X, int d, const float* C_all, int H, int m,
 int orc_build_precomp_large_root(int d, int h0, int Hs, const float* C0, const float* C_small,
                                  float* norm0, float* G_small, float* G0S, int nthreads) {
     SetThreads(nthreads);
-    // precomp_large_root.cpp:94-101: norm0 = ||c0||^2 (sequential here).
-    for (int c = 0; c < h0; ++c) {
-        const float* v = C0 + static_cast<std::size_t>(c) * d;
-        float s = 0.0f;
-        for (int r = 0; r < d; ++r) s += v[r] * v[r];
-        norm0[c] = s;
-    }
+    // precomp_large_root.cpp:82-90: norm0 = Norm2(c0) (the OpenMP-simd order of :14-23).
+    for (int c = 0; c < h0; ++c) norm0[c] = SimdLane4SumSq(C0 + static_cast<std::size_t>(c) * d, d);
     // precomp_large_root.cpp:126-130: G_small = C_small^T C_small, G0S = C0^T C_small.
     #pragma omp parallel for schedule(dynamic, 16)
     for (int j = 0; j < Hs; ++j) {
@@ -761,42 +818,8 @@ int orc_beam_search_large_root(const float* X, int d, const float* nx2, const fl
         for (int64_t i = 0; i < n; ++i) {
             const float* x = X + static_cast<std::size_t>(i) * d;
             const float* xCi = xC_small + static_cast<std::size_t>(i) * Hs;
-            // Root candidates (beam_search.cpp:639-709): streaming top-H by ascending code.
-            std::fill(rerr.begin(), rerr.end(), kInf);
-            std::fill(rcode.begin(), rcode.end(), 0);
-            std::fill(ra0.begin(), ra0.end(), 0.0f);
-            std::fill(rr00.begin(), rr00.end(), 0.0f);
-            // Root scores <c0_code, x>: GemmRaw in the reference (beam_search.cpp:665); here the
-            // fused k-ordered dot of the device's root GEMM.
-            auto root_score = [&](int code) { return FusedDot(C0 + static_cast<std::size_t>(code) * d, x, d); };
-            if (forced_root) {
-                const int code = static_cast<int>(forced_root[i]);
-                const float alpha = norm0[code];
-                if (alpha != 0.0f) {
-                    const float gamma = root_score(code);
-                    const float a1 = gamma / alpha;
-                    rerr[0] = nx2[i] - gamma * a1;
-                    rcode[0] = code;
-                    ra0[0] = a1;
-                    rr00[0] = std::sqrt(alpha);
-                }
-            } else {
-                float worst;
-                int wi = FirstMaxSlot(rerr.data(), root_slots, &worst);
-                for (int code = 0; code < h0; ++code) {
-                    const float alpha = norm0[code];
-                    if (alpha == 0.0f) continue;
-                    const float gamma = root_score(code);
-                    const float a1 = gamma / alpha;
-                    const float e1 = nx2[i] - gamma * a1;
-                    if (e1 >= worst) continue;
-                    rerr[wi] = e1;
-                    rcode[wi] = code;
-                    ra0[wi] = a1;
-                    rr00[wi] = std::sqrt(alpha);
-                    wi = FirstMaxSlot(rerr.data(), root_slots, &worst);
-                }
-            }
+            RootCandidates(x, d, nx2[i], C0, norm0, h0, root_slots, forced_root ? &forced_root[i] : nullptr,
+                           rerr.data(), rcode.data(), ra0.data(), rr00.data());
             // ExpandFromRootCandidates seeding (beam_search.cpp:760-793).
             W.Reset();
             int cur = 0, nxt = 1;
@@ -830,6 +853,26 @@ int orc_beam_search_large_root(const float* X, int d, const float* nx2, const fl
                 B_small[static_cast<std::size_t>(i) * (m - 1) + (L - 1)] = W.Code(cur, best, L);
             if (best_err) best_err[i] = W.err[cur][best];
         }
+    }
+    return 0;
+}
+
+int orc_large_root_candidates(const float* X, int d, const float* nx2, const float* C0, const float* norm0, int h0,
+                              int H_beam, int64_t n, const uint32_t* forced_root, int root_mode, float* root_errs,
+                              int* root_codes, float* root_a0, float* root_r00, int nthreads) {
+    if (h0 <= 0 || H_beam <= 0) return -1;
+    SetThreads(nthreads);
+    const int slots = (forced_root != nullptr || root_mode == 1) ? 1 : H_beam;
+    #pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; ++i) {
+        const std::size_t o = static_cast<std::size_t>(i) * H_beam;
+        std::fill(root_errs + o, root_errs + o + H_beam, kInf);
+        std::fill(root_codes + o, root_codes + o + H_beam, 0);
+        std::fill(root_a0 + o, root_a0 + o + H_beam, 0.0f);
+        std::fill(root_r00 + o, root_r00 + o + H_beam, 0.0f);
+        RootCandidates(X + static_cast<std::size_t>(i) * d, d, nx2[i], C0, norm0, h0, slots,
+                       forced_root ? &forced_root[i] : nullptr, root_errs + o, root_codes + o, root_a0 + o,
+                       root_r00 + o);
     }
     return 0;
 }

@@ -26,7 +26,8 @@ extern "C" {
 int orc_build_precomp(int d, int m, const int* h_vec, const float* C_all,
                       float* G, float* invnorm, int nthreads);
 
-/* cost_utils.cpp:88-110 (||x||^2, fixed sequential order). */
+/* cost_utils.cpp:88-110 (||x||^2 in the reference Release build's OpenMP-simd order: four
+ * interleaved partial sums, tail into lane 0, lanes added in order). */
 void orc_xnorm2(const float* X, int d, int64_t n, float* out, int nthreads);
 
 /* blas.cpp:33-54 call site encoder_encode_base.inc:33-37 (xC = C_all^T X).
@@ -93,6 +94,14 @@ int orc_beam_search_large_root(const float* X, int d, const float* nx2, const fl
                                const uint32_t* forced_root, int root_mode,
                                uint32_t* cluster_id, uint8_t* B_small, float* best_err,
                                int nthreads);
+
+/* The root stage of the above alone (beam_search.cpp:639-709): per vector, H_beam slots
+ * [n, H_beam] of (error, code, a0, r00) in the layout ExpandFromRootCandidates takes
+ * (beam_search.h:36-47); unused slots hold error +inf. */
+int orc_large_root_candidates(const float* X, int d, const float* nx2, const float* C0,
+                              const float* norm0, int h0, int H_beam, int64_t n,
+                              const uint32_t* forced_root, int root_mode, float* root_errs,
+                              int* root_codes, float* root_a0, float* root_r00, int nthreads);
 
 #ifdef __cplusplus
 }

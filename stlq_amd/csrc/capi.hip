@@ -451,7 +451,7 @@ int stlq_mi355_set_codebooks(stlq_mi355_ctx* c, int d, int m, const int* h_vec, 
     c->G_cm.p = c->G_rm.p;
     c->G_cm.bytes = 0;  // alias, never freed through G_cm
     HIP_TRY(LaunchGram(c->C_all.as<float>(), d, c->H, c->G_rm.as<float>(), c->stream));
-    HIP_TRY(LaunchNorms(c->C_all.as<float>(), d, c->H, nullptr, c->invnorm.as<float>(), c->stream));
+    HIP_TRY(LaunchNorms(c->C_all.as<float>(), d, c->H, false, nullptr, c->invnorm.as<float>(), c->stream));
     HIP_TRY(LaunchDiag(c->G_rm.as<float>(), c->H, c->gdiag.as<float>(), c->stream));
     HIP_TRY(hipStreamSynchronize(c->stream));
     c->has_pre = true;
@@ -1116,7 +1116,7 @@ int stlq_mi355_set_large_root(stlq_mi355_ctx* c, int d, int m, const int* h_vec,
     HIP_TRY(c->G0S.Ensure(h0 * Hs * 4));
     HIP_TRY(c->gdiag_small.Ensure(Hs * 4));
     HIP_TRY(hipMemcpyAsync(c->C0.p, C0, h0 * d * 4, hipMemcpyHostToDevice, c->stream));
-    HIP_TRY(LaunchNorms(c->C0.as<float>(), d, c->h0, c->norm0.as<float>(), nullptr, c->stream));
+    HIP_TRY(LaunchNorms(c->C0.as<float>(), d, c->h0, true, c->norm0.as<float>(), nullptr, c->stream));
     if (c->Hs > 0) {
         HIP_TRY(hipMemcpyAsync(c->Cs.p, C_small, static_cast<size_t>(c->Hs) * d * 4, hipMemcpyHostToDevice, c->stream));
         HIP_TRY(LaunchGram(c->Cs.as<float>(), d, c->Hs, c->G_small.as<float>(), c->stream));

@@ -73,7 +73,7 @@ struct RootArgs {
 // ---- launchers (each defined in the .hip file that holds the kernel) ----
 hipError_t LaunchGram(const float* C, int d, int H, float* G_rm, hipStream_t s);
 hipError_t LaunchCross(const float* C0, int h0, const float* Cs, int Hs, int d, float* G0S_rm, hipStream_t s);
-hipError_t LaunchNorms(const float* C, int d, int H, float* norm2, float* invnorm, hipStream_t s);
+hipError_t LaunchNorms(const float* C, int d, int H, bool lane4, float* norm2, float* invnorm, hipStream_t s);
 hipError_t LaunchDiag(const float* G_rm, int H, float* diag, hipStream_t s);
 hipError_t LaunchTranspose(const float* in, int rows, int cols, float* out, hipStream_t s);
 hipError_t LaunchXNorm2(const float* X, int d, int64_t n, float* out, hipStream_t s);

@@ -66,14 +66,36 @@ __global__ __launch_bounds__(256) void SeqDotKernel(const float* __restrict__ A,
     }
 }
 
-// encoder_precomp.inc:31-39 / precomp_large_root.cpp:14-23: ||c||^2 and 1/sqrt(||c||^2).
-__global__ void NormsKernel(const float* __restrict__ C, int d, int H, float* __restrict__ norm2,
+// Sum of squares in the order the reference's Release build gives its `omp simd` reductions
+// (GCC, -O3 -fopenmp, baseline x86-64 = 4 float lanes): element t goes to lane t mod 4 over the
+// first floor(d/4)*4 elements, the rest to lane 0, then the lanes are added in order to 0.
+__device__ __forceinline__ float SimdLane4SumSq(const float* __restrict__ x, int d) {
+    float p0 = 0.0f, p1 = 0.0f, p2 = 0.0f, p3 = 0.0f;
+    const int d4 = d & ~3;
+    for (int t = 0; t < d4; t += 4) {
+        p0 = p0 + x[t] * x[t];
+        p1 = p1 + x[t + 1] * x[t + 1];
+        p2 = p2 + x[t + 2] * x[t + 2];
+        p3 = p3 + x[t + 3] * x[t + 3];
+    }
+    for (int t = d4; t < d; ++t) p0 = p0 + x[t] * x[t];
+    return (((0.0f + p0) + p1) + p2) + p3;
+}
+
+// ||c||^2 and 1/sqrt(||c||^2) per codeword. lane4 = false: the sequential loop of
+// encoder_precomp.inc:31-39 (invnorm_flat); lane4 = true: Norm2 of precomp_large_root.cpp:14-23
+// (norm0, invnorm_small_flat), an `omp simd` reduction.
+__global__ void NormsKernel(const float* __restrict__ C, int d, int H, bool lane4, float* __restrict__ norm2,
                             float* __restrict__ invnorm) {
     const int f = blockIdx.x * blockDim.x + threadIdx.x;
     if (f >= H) return;
     const float* c = C + static_cast<int64_t>(f) * d;
     float s = 0.0f;
-    for (int r = 0; r < d; ++r) s = s + c[r] * c[r];
+    if (lane4) {
+        s = SimdLane4SumSq(c, d);
+    } else {
+        for (int r = 0; r < d; ++r) s = s + c[r] * c[r];
+    }
     if (norm2) norm2[f] = s;
     if (invnorm) invnorm[f] = s > 0.0f ? 1.0f / sqrtf(s) : 0.0f;
 }
@@ -98,9 +120,10 @@ __global__ void TransposeKernel(const float* __restrict__ in, int rows, int cols
     }
 }
 
-// ||x||^2 per vector, t ascending (cost_utils.cpp:99-109 with a fixed order).
-// A wave stages 64 vectors' rows through LDS in chunks so the global reads are coalesced,
-// while each lane still accumulates its own vector sequentially.
+// ||x||^2 per vector (cost_utils.cpp:99-109, beam_search.cpp:218-223) in the reference build's
+// OpenMP-simd order (SimdLane4SumSq above). A wave stages 64 vectors' rows through LDS in chunks
+// so the global reads are coalesced; each lane keeps its vector's four partial sums. The chunk
+// length is a multiple of 4, so lane t mod 4 is the same within and across chunks.
 constexpr int kNormChunk = 32;
 __global__ __launch_bounds__(256) void XNorm2Kernel(const float* __restrict__ X, int d, int64_t n,
                                                     float* __restrict__ out) {
@@ -108,7 +131,8 @@ __global__ __launch_bounds__(256) void XNorm2Kernel(const float* __restrict__ X,
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int64_t v0 = (static_cast<int64_t>(blockIdx.x) * 4 + wave) * kWave;
     const int nv = v0 < n ? static_cast<int>(min<int64_t>(kWave, n - v0)) : 0;
-    float s = 0.0f;
+    const int d4 = d & ~3;
+    float p0 = 0.0f, p1 = 0.0f, p2 = 0.0f, p3 = 0.0f;
     for (int t0 = 0; t0 < d; t0 += kNormChunk) {
         const int tl = min(kNormChunk, d - t0);
         for (int r = 0; r < nv; ++r) {
@@ -116,14 +140,19 @@ __global__ __launch_bounds__(256) void XNorm2Kernel(const float* __restrict__ X,
         }
         __syncthreads();
         if (lane < nv) {
-            for (int t = 0; t < tl; ++t) {
-                const float v = tile[wave][lane][t];
-                s = s + v * v;
+            const float* row = tile[wave][lane];
+            const int main = max(0, min(tl, d4 - t0));  // multiple of 4
+            for (int t = 0; t < main; t += 4) {
+                p0 = p0 + row[t] * row[t];
+                p1 = p1 + row[t + 1] * row[t + 1];
+                p2 = p2 + row[t + 2] * row[t + 2];
+                p3 = p3 + row[t + 3] * row[t + 3];
             }
+            for (int t = main; t < tl; ++t) p0 = p0 + row[t] * row[t];
         }
         __syncthreads();
     }
-    if (lane < nv) out[v0 + lane] = s;
+    if (lane < nv) out[v0 + lane] = (((0.0f + p0) + p1) + p2) + p3;
 }
 
 __global__ void Fill8Kernel(uint8_t* p, uint8_t v, int64_t n) {
@@ -183,9 +212,9 @@ hipError_t LaunchCross(const float* C0, int h0, const float* Cs, int Hs, int d, 
     return hipGetLastError();
 }
 
-hipError_t LaunchNorms(const float* C, int d, int H, float* norm2, float* invnorm, hipStream_t s) {
+hipError_t LaunchNorms(const float* C, int d, int H, bool lane4, float* norm2, float* invnorm, hipStream_t s) {
     if (H <= 0) return hipSuccess;
-    hipLaunchKernelGGL(NormsKernel, dim3((H + 255) / 256), dim3(256), 0, s, C, d, H, norm2, invnorm);
+    hipLaunchKernelGGL(NormsKernel, dim3((H + 255) / 256), dim3(256), 0, s, C, d, H, lane4, norm2, invnorm);
     return hipGetLastError();
 }
 

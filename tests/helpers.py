@@ -65,3 +65,62 @@ def parity(orc, X, C, h_vec, codes_ref, codes_test, max_frac=1e-3, tie_rel=1e-5,
         rep["max_rel_mse"] = float(rel.max())
         rep["ok"] = rep["frac_diff"] <= max_frac and rep["max_rel_mse"] <= max(tie_rel, mse_rel)
     return rep
+
+
+BEAM_CASES = [
+    # name, seed, n, d, h_vec, H_beam, kind
+    ("m2_K16_b4", 10, 800, 12, [16, 16], 4, "gauss"),
+    ("m4_K32_b1", 11, 800, 24, [32] * 4, 1, "gauss"),
+    ("m4_K256_b4_c1", 12, 600, 128, [256] * 4, 4, "gauss"),
+    ("m8_K256_b16_c2", 13, 500, 128, [256] * 8, 16, "desc"),
+    ("m8_K256_b16_sphere", 14, 400, 96, [256] * 8, 16, "sphere"),
+    ("m5_K100_b64", 15, 300, 20, [100, 90, 80, 70, 60], 64, "gauss"),
+    ("m3_K7_b40", 16, 500, 6, [7, 9, 5], 40, "gauss"),
+    ("m10_K64_b8", 17, 300, 40, [64] * 10, 8, "gauss"),
+    ("m16_K256_b8_decay", 18, 120, 64, [256] * 16, 8, "decay"),
+    ("m1_K200_b3", 19, 500, 16, [200], 3, "gauss"),
+    ("m6_K65_b33", 20, 300, 30, [65, 130, 200, 3, 256, 64], 33, "gauss"),
+]
+
+
+def beam_case(seed, n, d, h, kind):
+    if kind == "gauss" and max(h) < 100:
+        return random_problem(seed, n, d, h, x_scale=2.0)
+    if len(set(h)) == 1:
+        return rvq_problem(seed, n, d, len(h), h[0], kind=kind, train_n=max(2000, 4 * h[0]), iters=4)
+    return random_problem(seed, n, d, h, x_scale=2.0)
+
+
+DEGENERATE = ["dup_within_layer", "dup_across_layers", "zero_codeword", "zero_layer", "zero_root_layer",
+              "tiny_codebook", "scaled_copies"]
+
+
+def degenerate_problem(case):
+    """Exact ties, zero codewords/layers, tiny codebooks: (X, C, h_vec) for one named case."""
+    rng = np.random.default_rng(100 + DEGENERATE.index(case))
+    d, h = 10, [12, 12, 12, 12]
+    C = rng.standard_normal((48, d)).astype(np.float32)
+    X = (rng.standard_normal((400, d)) * 2).astype(np.float32)
+    if case == "dup_within_layer":
+        C[3] = C[7]
+        C[12 + 5] = C[12 + 1]
+        C[24 + 0] = C[24 + 11]
+    elif case == "dup_across_layers":
+        C[12 + 4] = C[2]
+        C[24 + 4] = C[2]
+        C[36 + 9] = C[12 + 4]
+    elif case == "zero_codeword":
+        C[5] = 0
+        C[12 + 0] = 0
+        C[36 + 11] = 0
+    elif case == "zero_layer":
+        C[24:36] = 0
+    elif case == "zero_root_layer":
+        C[0:12] = 0
+    elif case == "tiny_codebook":
+        h = [2, 1, 3, 2]
+        C = C[:8]
+    elif case == "scaled_copies":
+        C[12 + 3] = 2.0 * C[1]
+        C[24 + 6] = -0.5 * C[12 + 8]
+    return X, C, h

@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 
 from stlq_amd.encoder import EncodeConfig
-from tests.helpers import parity, random_problem, rvq_problem
+from tests.helpers import BEAM_CASES, DEGENERATE, beam_case, degenerate_problem, parity, random_problem, rvq_problem
 
 pytestmark = pytest.mark.gpu
 
@@ -33,8 +33,10 @@ def test_precomp_bit_exact(ctx, orc):
     assert np.array_equal(_bits(inv), _bits(invo))
 
 
-def test_xnorm_bit_exact(ctx, orc):
-    X, C = random_problem(2, 3001, 130, [8, 8], x_scale=50.0)
+@pytest.mark.parametrize("d", [1, 3, 13, 37, 96, 128, 130, 960])
+def test_xnorm_bit_exact(ctx, orc, d):
+    """||x||^2 in the reference build's OpenMP-simd order, aligned and ragged d."""
+    X, C = random_problem(2 + d, 3001, d, [8, 8], x_scale=50.0)
     ctx.set_codebooks(C, [8, 8])
     assert np.array_equal(_bits(ctx.xnorm2(X)), _bits(orc.xnorm2(X)))
 
@@ -51,33 +53,9 @@ def test_gemm_xc_close(ctx, orc, n, d, H):
     assert np.max(np.abs(xg - x64) / scale) < 4 * d * 2.0 ** -24
 
 
-BEAM_CASES = [
-    # name, seed, n, d, h_vec, H_beam, kind
-    ("m2_K16_b4", 10, 800, 12, [16, 16], 4, "gauss"),
-    ("m4_K32_b1", 11, 800, 24, [32] * 4, 1, "gauss"),
-    ("m4_K256_b4_c1", 12, 600, 128, [256] * 4, 4, "gauss"),
-    ("m8_K256_b16_c2", 13, 500, 128, [256] * 8, 16, "desc"),
-    ("m8_K256_b16_sphere", 14, 400, 96, [256] * 8, 16, "sphere"),
-    ("m5_K100_b64", 15, 300, 20, [100, 90, 80, 70, 60], 64, "gauss"),
-    ("m3_K7_b40", 16, 500, 6, [7, 9, 5], 40, "gauss"),
-    ("m10_K64_b8", 17, 300, 40, [64] * 10, 8, "gauss"),
-    ("m16_K256_b8_decay", 18, 120, 64, [256] * 16, 8, "decay"),
-    ("m1_K200_b3", 19, 500, 16, [200], 3, "gauss"),
-    ("m6_K65_b33", 20, 300, 30, [65, 130, 200, 3, 256, 64], 33, "gauss"),
-]
-
-
-def _beam_case(seed, n, d, h, kind):
-    if kind == "gauss" and max(h) < 100:
-        return random_problem(seed, n, d, h, x_scale=2.0)
-    if len(set(h)) == 1:
-        return rvq_problem(seed, n, d, len(h), h[0], kind=kind, train_n=max(2000, 4 * h[0]), iters=4)
-    return random_problem(seed, n, d, h, x_scale=2.0)
-
-
 @pytest.mark.parametrize("name,seed,n,d,h,Hb,kind", BEAM_CASES, ids=[c[0] for c in BEAM_CASES])
 def test_beam_bit_exact_given_same_inputs(ctx, orc, name, seed, n, d, h, Hb, kind):
-    X, C = _beam_case(seed, n, d, h, kind)
+    X, C = beam_case(seed, n, d, h, kind)
     G, inv = _set(ctx, C, h)
     nx2 = orc.xnorm2(X)
     xC = orc.gemm_xc(C, X)
@@ -100,40 +78,11 @@ def test_beam_from_gpu_xc_bit_exact(ctx, orc):
     assert np.array_equal(codes_g, codes_o)
 
 
-DEGENERATE = ["dup_within_layer", "dup_across_layers", "zero_codeword", "zero_layer", "zero_root_layer",
-              "tiny_codebook", "scaled_copies"]
-
-
 @pytest.mark.parametrize("case", DEGENERATE)
 def test_beam_degenerate_bit_exact(ctx, orc, case):
     """Exact ties, skipped candidates (alpha == 0, denom == 0), non-finite beam errors and the
     all-skipped fallback follow the reference's slot rules bit for bit."""
-    rng = np.random.default_rng(100 + DEGENERATE.index(case))
-    d, h = 10, [12, 12, 12, 12]
-    C = rng.standard_normal((48, d)).astype(np.float32)
-    X = (rng.standard_normal((400, d)) * 2).astype(np.float32)
-    if case == "dup_within_layer":
-        C[3] = C[7]
-        C[12 + 5] = C[12 + 1]
-        C[24 + 0] = C[24 + 11]
-    elif case == "dup_across_layers":
-        C[12 + 4] = C[2]
-        C[24 + 4] = C[2]
-        C[36 + 9] = C[12 + 4]
-    elif case == "zero_codeword":
-        C[5] = 0
-        C[12 + 0] = 0
-        C[36 + 11] = 0
-    elif case == "zero_layer":
-        C[24:36] = 0
-    elif case == "zero_root_layer":
-        C[0:12] = 0
-    elif case == "tiny_codebook":
-        h = [2, 1, 3, 2]
-        C = C[:8]
-    elif case == "scaled_copies":
-        C[12 + 3] = 2.0 * C[1]
-        C[24 + 6] = -0.5 * C[12 + 8]
+    X, C, h = degenerate_problem(case)
     G, inv = _set(ctx, C, h)
     nx2 = orc.xnorm2(X)
     xC = orc.gemm_xc(C, X)

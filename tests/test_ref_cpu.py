@@ -1,0 +1,104 @@
+"""The oracle restatement against the reference's own CPU encoder, compiled from its sources
+(oracle/Makefile target `ref`, oracle/ref_driver.cpp).
+
+Pinned here, bit for bit, on the same inputs:
+  * ||x||^2 (ComputeXNorm2, cost_utils.cpp:88-110) for ragged and aligned d;
+  * BeamSearchPrefixLS codes (beam_search.cpp:196-422) on every beam case of the GPU parity
+    suite plus the degenerate ones (ties, zero codewords and layers, tiny codebooks), with
+    G, xC from the oracle fed to both (the reference's BLAS G/xC order is not buildable here);
+  * ComputeCosts (cost_utils.cpp:139-158) for m = 1..16;
+  * the large-root expansion BeamSearchPrefixLSLargeRootExpandFromRootCandidates
+    (beam_search.cpp:728-992) from the oracle's root candidates, for top-H, nearest and forced
+    roots.
+These run only where the reference library is built (this container); elsewhere they skip.
+"""
+import numpy as np
+import pytest
+
+from oracle import ref
+from tests.helpers import BEAM_CASES, DEGENERATE, beam_case, degenerate_problem, random_problem, rvq_problem
+
+pytestmark = pytest.mark.skipif(not ref.available(), reason="reference CPU encoder not built (make -C oracle ref)")
+
+
+def _bits(a):
+    return np.ascontiguousarray(a).view(np.uint32)
+
+
+@pytest.mark.parametrize("d", [1, 2, 3, 4, 5, 7, 8, 13, 31, 33, 64, 96, 127, 128, 130, 960])
+def test_xnorm2_matches_reference(orc, d):
+    rng = np.random.default_rng(d)
+    X = (rng.standard_normal((500, d)) * rng.uniform(0.1, 30.0, (500, 1))).astype(np.float32)
+    assert np.array_equal(_bits(ref.xnorm2(X)), _bits(orc.xnorm2(X)))
+
+
+@pytest.mark.parametrize("name,seed,n,d,h,Hb,kind", BEAM_CASES, ids=[c[0] for c in BEAM_CASES])
+def test_beam_matches_reference(orc, name, seed, n, d, h, Hb, kind):
+    X, C = beam_case(seed, n, d, h, kind)
+    G, _ = orc.build_precomp(C, h)
+    xC = orc.gemm_xc(C, X)
+    codes_r = ref.beam_search(X, xC, G, h, Hb)
+    codes_o, _ = orc.beam_search(orc.xnorm2(X), xC, G, h, Hb)
+    bad = np.nonzero(np.any(codes_r != codes_o, axis=1))[0]
+    assert bad.size == 0, (name, bad[:10])
+
+
+@pytest.mark.parametrize("case", DEGENERATE)
+def test_beam_degenerate_matches_reference(orc, case):
+    X, C, h = degenerate_problem(case)
+    G, _ = orc.build_precomp(C, h)
+    xC = orc.gemm_xc(C, X)
+    nx2 = orc.xnorm2(X)
+    for Hb in (1, 2, 5, 16):
+        codes_r = ref.beam_search(X, xC, G, h, Hb)
+        codes_o, _ = orc.beam_search(nx2, xC, G, h, Hb)
+        bad = np.nonzero(np.any(codes_r != codes_o, axis=1))[0]
+        assert bad.size == 0, (case, Hb, bad[:10], codes_r[bad[:3]], codes_o[bad[:3]])
+
+
+def test_beam_c2_shape_matches_reference(orc):
+    """Descriptor-like 128-d vectors, 8 x 256 codebooks, beam 16 (the headline shape)."""
+    X, C = rvq_problem(5, 3000, 128, 8, 256, kind="desc", train_n=3000, iters=4)
+    h = [256] * 8
+    G, _ = orc.build_precomp(C, h)
+    xC = orc.gemm_xc(C, X, mode=1)
+    assert np.array_equal(ref.beam_search(X, xC, G, h, 16), orc.beam_search(orc.xnorm2(X), xC, G, h, 16)[0])
+
+
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8, 10, 16])
+def test_costs_match_reference(orc, m):
+    h = [32] * m
+    X, C = random_problem(40 + m, 600, 24, h, x_scale=2.0)
+    G, _ = orc.build_precomp(C, h)
+    xC = orc.gemm_xc(C, X)
+    nx2 = orc.xnorm2(X)
+    codes, _ = orc.beam_search(nx2, xC, G, h, 4)
+    a, _ = orc.solve_ls_all(xC, G, h, codes)
+    assert np.array_equal(_bits(ref.compute_costs(xC, G, h, codes, a, nx2)),
+                          _bits(orc.compute_costs(xC, G, h, codes, a, nx2)))
+
+
+@pytest.mark.parametrize("mode", ["topH", "nearest", "forced"])
+@pytest.mark.parametrize("Hb", [1, 4, 32])
+def test_large_root_expansion_matches_reference(orc, mode, Hb):
+    from stlq_amd import workloads
+
+    n, d, h0, K, m, seed = 600, 32, 700, 64, 5, 61 + Hb
+    mix = workloads.Mixture("gauss", d, 128, seed)
+    rng = np.random.default_rng(seed)
+    C0 = mix.sample(5_000_000, h0)
+    Xtr = mix.sample(1_000_000, 2000)
+    Cs = workloads.residual_codebooks(Xtr - C0[rng.integers(0, h0, 2000)], m - 1, K, 3, seed + 1)
+    X = mix.sample(0, n)
+    h = [h0] + [K] * (m - 1)
+    norm0, Gs, G0S = orc.build_precomp_large_root(C0, Cs)
+    nx2 = orc.xnorm2(X)
+    xs = orc.gemm_xc(Cs, X, mode=1)
+    forced = rng.integers(0, h0, n).astype(np.uint32) if mode == "forced" else None
+    root_mode = 1 if mode == "nearest" else 0
+    errs, codes, a0, r00 = orc.large_root_candidates(X, nx2, C0, norm0, Hb, forced_root=forced, root_mode=root_mode)
+    cid_r, Bs_r = ref.expand_large_root(Gs, G0S, h, xs, Hb, errs, codes, a0, r00)
+    cid_o, Bs_o, _ = orc.beam_search_large_root(X, nx2, C0, norm0, xs, Gs, G0S, h, Hb, forced_root=forced,
+                                                root_mode=root_mode)
+    assert np.array_equal(cid_r, cid_o)
+    assert np.array_equal(Bs_r, Bs_o)
