@@ -36,6 +36,17 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return ""
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -190,47 +201,51 @@ def main():
 
     if args.cpu_sample > 0:
         from oracle import oracle as orc
+        from oracle import ref
 
         ns = min(args.cpu_sample, n)
         threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
+        use_ref = ref.available()
         Xs = X[:ns]
         G, inv = orc.build_precomp(C, h, nthreads=threads)
         tc = time.perf_counter()
-        nx2 = orc.xnorm2(Xs, nthreads=threads)
+        nx2 = ref.xnorm2(Xs) if use_ref else orc.xnorm2(Xs, nthreads=threads)
         xC = orc.gemm_xc(C, Xs, mode=1, nthreads=threads)
         t_gemm = time.perf_counter() - tc
-        codes_o, _ = orc.beam_search(nx2, xC, G, h, B, nthreads=threads)
+        if use_ref:
+            codes_o = ref.beam_search(Xs, xC, G, h, B)
+        else:
+            codes_o, _ = orc.beam_search(nx2, xC, G, h, B, nthreads=threads)
         t_beam = time.perf_counter() - tc - t_gemm
         if w.icm_iters:
             codes_o, a_o, cost_o, _ = orc.icm(xC, G, inv, h, nx2, codes_o, w.icm_iters, True, cfg.seed,
                                               nthreads=threads)
         else:
             a_o, _ = orc.solve_ls_all(xC, G, h, codes_o, nthreads=threads)
-            cost_o = orc.compute_costs(xC, G, h, codes_o, a_o, nx2, nthreads=threads)
+            cost_o = ref.compute_costs(xC, G, h, codes_o, a_o, nx2) if use_ref else \
+                orc.compute_costs(xC, G, h, codes_o, a_o, nx2, nthreads=threads)
         t_cpu = time.perf_counter() - tc
-        log(f"cpu oracle: {ns} vectors in {t_cpu:.1f}s on {threads} threads")
-        cpu_model = ""
-        try:
-            with open("/proc/cpuinfo") as f:
-                for line in f:
-                    if line.startswith("model name"):
-                        cpu_model = line.split(":", 1)[1].strip()
-                        break
-        except OSError:
-            pass
+        log(f"cpu {'reference' if use_ref else 'oracle'}: {ns} vectors in {t_cpu:.1f}s on {threads} threads")
+        cpu_model = _cpu_model()
+        if use_ref:
+            what = (f"reference ComputeXNorm2 + BeamSearchPrefixLS{' + ComputeCosts' if not w.icm_iters else ''} "
+                    f"(its own sources, g++ -O3 -fopenmp); xC by the oracle's fused-order dot (the reference's "
+                    f"BLAS is not in the image); {'ICM and ' if w.icm_iters else ''}LS refit by the oracle")
+        else:
+            what = (f"oracle port: ||x||^2 + xC + beam + {'ICM ' if w.icm_iters else ''}LS refit + cost")
         out["cpu_baseline"] = {
             "value": ns / t_cpu,
             "unit": "vectors/s",
             "cores": threads,
-            "kind": "port",
-            "sample": f"first {ns} vectors of the same workload; ||x||^2 + xC + beam + "
-                      f"{'ICM ' if w.icm_iters else ''}LS refit + cost; "
-                      f"stages s: xC {t_gemm:.2f}, beam {t_beam:.2f}, rest {t_cpu - t_gemm - t_beam:.2f}; "
+            "kind": "reference" if use_ref else "port",
+            "sample": f"first {ns} vectors of the same workload; {what}; "
+                      f"stages s: ||x||^2+xC {t_gemm:.2f}, beam {t_beam:.2f}, rest {t_cpu - t_gemm - t_beam:.2f}; "
                       f"cpu: {cpu_model}",
         }
         same = np.all(codes[:ns] == codes_o, axis=1)
         out["parity"] = {
             "sample": ns,
+            "against": "reference" if use_ref else "oracle",
             "codes_identical_frac": float(np.mean(same)),
             "cost_bit_identical_frac": float(np.mean(cost[:ns].view(np.uint32) == cost_o.view(np.uint32))),
         }
@@ -344,24 +359,41 @@ def bench_stream_large_root(args, w):
     }
     if args.cpu_sample > 0:
         from oracle import oracle as orc
+        from oracle import ref
 
         ns = min(args.cpu_sample, keep)
         threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
+        use_ref = ref.available()
         Xs = pool[:ns].astype(np.float32)
         norm0, Gs, G0S = orc.build_precomp_large_root(C0, Cs, nthreads=threads)
         tc = time.perf_counter()
-        nx2 = orc.xnorm2(Xs, nthreads=threads)
+        nx2 = ref.xnorm2(Xs) if use_ref else orc.xnorm2(Xs, nthreads=threads)
         xs = orc.gemm_xc(Cs, Xs, mode=1, nthreads=threads)
-        cid_o, Bs_o, _ = orc.beam_search_large_root(Xs, nx2, C0, norm0, xs, Gs, G0S, h, w.H_beam, root_mode=1,
-                                                    nthreads=threads)
+        if use_ref:
+            errs, rcodes, a0, r00 = orc.large_root_candidates(Xs, nx2, C0, norm0, w.H_beam, root_mode=1,
+                                                              nthreads=threads)
+            t_root = time.perf_counter() - tc
+            cid_o, Bs_o = ref.expand_large_root(Gs, G0S, h, xs, w.H_beam, errs, rcodes, a0, r00)
+        else:
+            cid_o, Bs_o, _ = orc.beam_search_large_root(Xs, nx2, C0, norm0, xs, Gs, G0S, h, w.H_beam, root_mode=1,
+                                                        nthreads=threads)
+            t_root = 0.0
         t_cpu = time.perf_counter() - tc
-        log(f"cpu oracle: {ns} vectors in {t_cpu:.1f}s on {threads} threads")
+        log(f"cpu {'reference' if use_ref else 'oracle'}: {ns} vectors in {t_cpu:.1f}s on {threads} threads")
+        if use_ref:
+            what = (f"reference ComputeXNorm2 + BeamSearchPrefixLSLargeRootExpandFromRootCandidates (its own sources, "
+                    f"g++ -O3 -fopenmp) for the 16-layer beam 32; xC_small and the nearest-root scan over 65,536 "
+                    f"roots by the oracle (the reference's root GEMM needs BLAS); stages s: xnorm+xC+root "
+                    f"{t_root:.2f}, expansion {t_cpu - t_root:.2f}")
+        else:
+            what = "oracle port: ||x||^2 + xC_small + nearest-root scan over 65,536 roots + 16-layer beam 32"
         out["cpu_baseline"] = {
-            "value": ns / t_cpu, "unit": "vectors/s", "cores": threads, "kind": "port",
-            "sample": f"first {ns} vectors of the stream; ||x||^2 + xC_small + nearest-root scan over 65,536 roots "
-                      f"+ 16-layer beam 32"}
+            "value": ns / t_cpu, "unit": "vectors/s", "cores": threads,
+            "kind": "reference" if use_ref else "port",
+            "sample": f"first {ns} vectors of the stream; {what}; cpu: {_cpu_model()}"}
         same = (cid_o == first_codes["cid"][:ns]) & np.all(Bs_o == first_codes["Bs"][:ns], axis=1)
-        out["parity"] = {"sample": ns, "codes_identical_frac": float(np.mean(same))}
+        out["parity"] = {"sample": ns, "against": "reference" if use_ref else "oracle",
+                         "codes_identical_frac": float(np.mean(same))}
     ctx.close()
     print(json.dumps(out), flush=True)
 

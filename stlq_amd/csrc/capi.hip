@@ -586,7 +586,7 @@ static int LsCommon(stlq_mi355_ctx* c, const float* xC, const uint8_t* codes, co
     HIP_TRY(c->cost.Ensure(static_cast<size_t>(n) * 4));
     HIP_TRY(hipMemcpyAsync(c->xC.p, xC, static_cast<size_t>(n) * c->H * 4, hipMemcpyHostToDevice, c->stream));
     HIP_TRY(hipMemcpyAsync(c->codes.p, codes, static_cast<size_t>(n) * m, hipMemcpyHostToDevice, c->stream));
-    HIP_TRY(hipMemsetAsync(c->fails.p, 0, 4, c->stream));
+    HIP_TRY(LaunchFill8(c->fails.as<uint8_t>(), 0, 4, c->stream));  // a kernel, not a memset node, if captured
     LsArgs ls = MakeLs(c, c->xC.as<float>(), c->H, c->codes.as<uint8_t>(), c->a.as<float>(), c->nx2.as<float>(),
                        c->cost.as<float>(), n);
     if (a_out) {
@@ -642,7 +642,7 @@ int stlq_mi355_icm(stlq_mi355_ctx* c, const float* X, const float* nx2, const fl
         HIP_TRY(hipMemcpyAsync(c->X.p, X, static_cast<size_t>(n) * c->d * 4, hipMemcpyHostToDevice, c->stream));
         HIP_TRY(LaunchXNorm2(c->X.as<float>(), c->d, n, c->nx2.as<float>(), c->stream));
     }
-    HIP_TRY(hipMemsetAsync(c->fails.p, 0, 4, c->stream));
+    HIP_TRY(LaunchFill8(c->fails.as<uint8_t>(), 0, 4, c->stream));  // a kernel, not a memset node, if captured
     TileEvents te;
     te.n = n;
     te.e[0] = te.e[1] = te.e[2] = te.e[3] = te.e[4] = c->NextEvent();
@@ -676,7 +676,7 @@ int stlq_mi355_encode(stlq_mi355_ctx* c, const float* X, int64_t n, const stlq_m
     HIP_TRY(c->codes.Ensure(static_cast<size_t>(tile) * m));
     HIP_TRY(c->a.Ensure(static_cast<size_t>(tile) * m * 4));
     HIP_TRY(c->cost.Ensure(static_cast<size_t>(tile) * 4));
-    HIP_TRY(hipMemsetAsync(c->fails.p, 0, 4, c->stream));
+    HIP_TRY(LaunchFill8(c->fails.as<uint8_t>(), 0, 4, c->stream));  // a kernel, not a memset node, if captured
     std::vector<float> beam_cost, fin_cost;
     double beam_sum = 0.0, fin_sum = 0.0;
     for (int64_t t0 = 0; t0 < n; t0 += tile) {
@@ -733,7 +733,7 @@ int stlq_mi355_encode_device(stlq_mi355_ctx* c, const float* dX, int64_t n, cons
     const int Hb = std::max(1, params->H_beam);
     const int64_t tile = TileVectors(n, c->d, c->m, c->H, Hb);
     const size_t m = static_cast<size_t>(c->m);
-    HIP_TRY(hipMemsetAsync(c->fails.p, 0, 4, s));
+    HIP_TRY(LaunchFill8(c->fails.as<uint8_t>(), 0, 4, s));  // a kernel, not a memset node, if captured
     for (int64_t t0 = 0; t0 < n; t0 += tile) {
         const int64_t nt = std::min(tile, n - t0);
         EncodeOut o{dcodes + t0 * m, da ? da + t0 * m : nullptr, dcost ? dcost + t0 : nullptr, nullptr};
