@@ -217,22 +217,28 @@ def main():
         else:
             codes_o, _ = orc.beam_search(nx2, xC, G, h, B, nthreads=threads)
         t_beam = time.perf_counter() - tc - t_gemm
-        if w.icm_iters:
+        if use_ref:
+            if w.icm_iters:
+                codes_o, a_o, cost_o = ref.icm(Xs, xC, G, inv, h, codes_o, w.icm_iters, True, cfg.seed)
+            else:
+                a_o = ref.solve_ls_all(xC, G, h, codes_o)
+                cost_o = ref.compute_costs(xC, G, h, codes_o, a_o, nx2)
+        elif w.icm_iters:
             codes_o, a_o, cost_o, _ = orc.icm(xC, G, inv, h, nx2, codes_o, w.icm_iters, True, cfg.seed,
                                               nthreads=threads)
         else:
             a_o, _ = orc.solve_ls_all(xC, G, h, codes_o, nthreads=threads)
-            cost_o = ref.compute_costs(xC, G, h, codes_o, a_o, nx2) if use_ref else \
-                orc.compute_costs(xC, G, h, codes_o, a_o, nx2, nthreads=threads)
+            cost_o = orc.compute_costs(xC, G, h, codes_o, a_o, nx2, nthreads=threads)
         t_cpu = time.perf_counter() - tc
         log(f"cpu {'reference' if use_ref else 'oracle'}: {ns} vectors in {t_cpu:.1f}s on {threads} threads")
         cpu_model = _cpu_model()
         if use_ref:
-            what = (f"reference ComputeXNorm2 + BeamSearchPrefixLS{' + ComputeCosts' if not w.icm_iters else ''} "
-                    f"(its own sources, g++ -O3 -fopenmp); xC by the oracle's fused-order dot (the reference's "
-                    f"BLAS is not in the image); {'ICM and ' if w.icm_iters else ''}LS refit by the oracle")
+            tail = "DynamicIcmWithIlsAbsNoNormal (ICM)" if w.icm_iters else "SolveLeastSquaresAll + ComputeCosts"
+            what = (f"reference ComputeXNorm2 + BeamSearchPrefixLS + {tail}, compiled from its own sources "
+                    f"(g++ -O3 -fopenmp; LAPACK from the image's MKL, sequential layer); xC by the oracle's "
+                    f"fused-order dot (the reference's BLAS is not in the image)")
         else:
-            what = (f"oracle port: ||x||^2 + xC + beam + {'ICM ' if w.icm_iters else ''}LS refit + cost")
+            what = f"oracle port: ||x||^2 + xC + beam + {'ICM ' if w.icm_iters else ''}LS refit + cost"
         out["cpu_baseline"] = {
             "value": ns / t_cpu,
             "unit": "vectors/s",
@@ -243,11 +249,22 @@ def main():
                       f"cpu: {cpu_model}",
         }
         same = np.all(codes[:ns] == codes_o, axis=1)
+        diff_idx = np.nonzero(~same)[0]
+        max_rel_mse = 0.0
+        if diff_idx.size:
+            ma = orc.mse_fp64_refit(Xs[diff_idx], C, h, codes_o[diff_idx], nthreads=threads)
+            mb = orc.mse_fp64_refit(Xs[diff_idx], C, h, codes[:ns][diff_idx], nthreads=threads)
+            max_rel_mse = float(np.max(np.abs(ma - mb) / np.maximum(np.abs(ma), 1e-30)))
+        cg = cost[:ns].astype(np.float64)
+        co = cost_o.astype(np.float64)
         out["parity"] = {
             "sample": ns,
             "against": "reference" if use_ref else "oracle",
             "codes_identical_frac": float(np.mean(same)),
+            "differing_max_rel_mse_fp64": max_rel_mse,
             "cost_bit_identical_frac": float(np.mean(cost[:ns].view(np.uint32) == cost_o.view(np.uint32))),
+            # the fp32 cost ||x||^2 - 2 a.xC + a'Ga cancels, so its rounding scales with ||x||^2
+            "cost_max_diff_over_xnorm2": float(np.max(np.abs(cg - co) / np.maximum(nx2.astype(np.float64), 1e-30))),
         }
 
     for p in (dX, dcodes, da, dcost):

@@ -39,12 +39,23 @@ def build() -> str:
 
 
 def available() -> bool:
-    return os.path.exists(_LIB_PATH)
+    """True when the reference library is built and loads (its MKL dependency included)."""
+    if not os.path.exists(_LIB_PATH):
+        return False
+    try:
+        lib()
+    except OSError:
+        return False
+    return True
 
 
 def lib():
     global _lib
     if _lib is None:
+        # MKL's sequential layer for the LAPACK calls (read by mkl_rt when it first initialises):
+        # its threaded layer inside the reference's OpenMP loops left results depending on
+        # earlier calls in the process.
+        os.environ.setdefault("MKL_THREADING_LAYER", "SEQUENTIAL")
         # Lazy binding: GemmRaw/BlasSetThreads (blas.cpp, not buildable here) stay unresolved and
         # are never reached by the driver's entry points.
         L = ctypes.CDLL(_LIB_PATH, mode=os.RTLD_LAZY)
@@ -53,7 +64,11 @@ def lib():
         L.ref_compute_costs.argtypes = [_f32p, _f32p, _int, _i32p, _int, _u8p, _f32p, _f32p, _int, _f32p]
         L.ref_expand_large_root.argtypes = [_f32p, _int, _f32p, _int, _i32p, _int, _f32p, _int, _int, _f32p,
                                             _i32p, _f32p, _f32p, _u32p, _u8p]
-        for f in (L.ref_xnorm2, L.ref_beam_search, L.ref_compute_costs, L.ref_expand_large_root):
+        L.ref_solve_ls_all.argtypes = [_f32p, _f32p, _int, _i32p, _int, _u8p, _int, _f32p]
+        L.ref_icm.argtypes = [_f32p, _int, _int, _f32p, _f32p, _f32p, _int, _i32p, _int, _int, _int, ctypes.c_uint32,
+                              _u8p, _f32p, _f32p]
+        for f in (L.ref_xnorm2, L.ref_beam_search, L.ref_compute_costs, L.ref_expand_large_root, L.ref_solve_ls_all,
+                  L.ref_icm):
             f.restype = None
         _lib = L
     return _lib
@@ -102,6 +117,36 @@ def compute_costs(xC, G, h_vec, codes, a, nx2):
     lib().ref_compute_costs(_p(xC, _f32p), _p(G, _f32p), H, _p(hv, _i32p), len(hv), _p(codes, _u8p), _p(a, _f32p),
                             _p(nx2, _f32p), n, _p(cost, _f32p))
     return cost
+
+
+def solve_ls_all(xC, G, h_vec, codes):
+    """stlq::SolveLeastSquaresAll (hand Cholesky for m in {5, 10}, LAPACK spotrf/spotrs otherwise)."""
+    xC = _c(xC, np.float32)
+    G = _c(G, np.float32)
+    hv = _c(h_vec, np.int32)
+    codes = _c(codes, np.uint8)
+    n, H = xC.shape
+    a = np.empty((n, len(hv)), np.float32)
+    lib().ref_solve_ls_all(_p(xC, _f32p), _p(G, _f32p), H, _p(hv, _i32p), len(hv), _p(codes, _u8p), n, _p(a, _f32p))
+    return a
+
+
+def icm(X, xC, G, invnorm, h_vec, codes, icm_iters, use_abs, seed):
+    """stlq::DynamicIcmWithIls{Abs,NoAbs}NoNormal with ils_iters = 0; returns (codes, a, cost)."""
+    X = _c(X, np.float32)
+    xC = _c(xC, np.float32)
+    G = _c(G, np.float32)
+    inv = _c(invnorm, np.float32)
+    hv = _c(h_vec, np.int32)
+    codes = np.array(codes, dtype=np.uint8, copy=True, order="C")
+    n, d = X.shape
+    H = G.shape[0]
+    m = len(hv)
+    a = np.empty((n, m), np.float32)
+    cost = np.empty(n, np.float32)
+    lib().ref_icm(_p(X, _f32p), d, n, _p(xC, _f32p), _p(G, _f32p), _p(inv, _f32p), H, _p(hv, _i32p), m, icm_iters,
+                  int(bool(use_abs)), seed & 0xFFFFFFFF, _p(codes, _u8p), _p(a, _f32p), _p(cost, _f32p))
+    return codes, a, cost
 
 
 def expand_large_root(G_small, G0S, h_vec, xC_small, H_beam, root_errs, root_codes, root_a0, root_r00):

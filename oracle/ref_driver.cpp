@@ -4,11 +4,13 @@
 // reference; nothing in the product links or loads it.
 //
 // Compiled with the reference's translation units
-//   src/quantizer/beam_search.cpp, linear_algebra.cpp, cost_utils.cpp, src/common/timer.cpp
+//   src/quantizer/beam_search.cpp, linear_algebra.cpp, cost_utils.cpp, least_squares.cpp,
+//   icm.cpp, src/common/timer.cpp, logger.cpp
+// and linked against the image's MKL runtime for LAPACK spotrf_/spotrs_ (least_squares.cpp).
 // blas.cpp is not buildable here (it includes cblas.h, which the image lacks), so GemmRaw and
 // BlasSetThreads stay unresolved. They are only reached from the root-score GEMM of
-// BeamSearchPrefixLSLargeRoot (beam_search.cpp:623-690), which this driver never calls; the
-// library is loaded with lazy binding.
+// BeamSearchPrefixLSLargeRoot (beam_search.cpp:623-690) and from ILS/large-root paths this
+// driver never calls; the library is loaded with lazy binding.
 //
 // Array conventions (all column-major as in the reference's ColMajorMatrix):
 //   X d x n, xC H x n, G H x H, codes m x n (uint8), a m x n.
@@ -19,6 +21,8 @@
 #include "stlq/common/types.h"
 #include "stlq/quantizer/beam_search.h"
 #include "stlq/quantizer/cost_utils.h"
+#include "stlq/quantizer/icm.h"
+#include "stlq/quantizer/least_squares.h"
 #include "stlq/quantizer/precomp_large_root.h"
 
 namespace {
@@ -81,6 +85,39 @@ void ref_compute_costs(const float* xC, const float* G, int H, const int* h_vec,
     std::vector<float> out;
     stlq::ComputeCosts(pre, xCm, B, am, xn, &out);
     std::memcpy(cost, out.data(), sizeof(float) * static_cast<std::size_t>(n));
+}
+
+// stlq::SolveLeastSquaresAll (least_squares.cpp:406-565; LAPACK for m not in {5, 10}).
+void ref_solve_ls_all(const float* xC, const float* G, int H, const int* h_vec, int m, const uint8_t* codes, int n,
+                      float* a) {
+    const auto pre = MakePrecomp(G, H, h_vec, m, 0);
+    const auto xCm = Wrap(xC, H, n);
+    const auto B = Wrap(codes, m, n);
+    stlq::ColMajorMatrix<float> am;
+    stlq::SolveLeastSquaresAll(pre, xCm, B, &am);
+    std::memcpy(a, am.data.data(), sizeof(float) * am.data.size());
+}
+
+// stlq::DynamicIcmWithIls{Abs,NoAbs}NoNormal (icm.cpp:1132-1170) with ils_iters = 0: LS refit,
+// costs, then icm_iters RunIcm sweeps. codes (m x n) are updated in place. invnorm (H) is the
+// precomp's invnorm_flat.
+void ref_icm(const float* X, int d, int n, const float* xC, const float* G, const float* invnorm, int H,
+             const int* h_vec, int m, int icm_iters, int use_abs, uint32_t seed, uint8_t* codes, float* a,
+             float* cost) {
+    auto pre = MakePrecomp(G, H, h_vec, m, d);
+    pre.invnorm_flat.assign(invnorm, invnorm + H);
+    const auto Xm = Wrap(X, d, n);
+    const auto xCm = Wrap(xC, H, n);
+    auto B = Wrap(codes, m, n);
+    stlq::ColMajorMatrix<float> am;
+    std::vector<float> xn2, cst;
+    if (use_abs)
+        stlq::DynamicIcmWithIlsAbsNoNormal(Xm, pre, xCm, icm_iters, 0, 3, seed, &B, &am, &xn2, &cst, false, 0);
+    else
+        stlq::DynamicIcmWithIlsNoAbsNoNormal(Xm, pre, xCm, icm_iters, 0, 3, seed, &B, &am, &xn2, &cst, false, 0);
+    std::memcpy(codes, B.data.data(), B.data.size());
+    std::memcpy(a, am.data.data(), sizeof(float) * am.data.size());
+    std::memcpy(cost, cst.data(), sizeof(float) * cst.size());
 }
 
 // stlq::BeamSearchPrefixLSLargeRootExpandFromRootCandidates (beam_search.cpp:728-992) for all

@@ -7,16 +7,24 @@ Pinned here, bit for bit, on the same inputs:
     suite plus the degenerate ones (ties, zero codewords and layers, tiny codebooks), with
     G, xC from the oracle fed to both (the reference's BLAS G/xC order is not buildable here);
   * ComputeCosts (cost_utils.cpp:139-158) for m = 1..16;
+  * SolveLeastSquaresAll (least_squares.cpp:406-565) and ICM (DynamicIcmWithIls*NoNormal with
+    ils_iters = 0, icm.cpp:89-344, :872-899) for m in {1, 5, 10}, where the reference runs its
+    own Cholesky;
   * the large-root expansion BeamSearchPrefixLSLargeRootExpandFromRootCandidates
     (beam_search.cpp:728-992) from the oracle's root candidates, for top-H, nearest and forced
     roots.
+For m not in {5, 10} the reference solves the LS systems with LAPACK spotrf/spotrs (here the
+image's MKL, whose kernels are chosen per CPU), so their bits are not fixed by the reference.
+There the tests bound the deviation instead: equal-quality LS solutions (fp64 objective within
+1e-9 relative), and after ICM every differing code tuple ties the reference's within 1e-5
+relative fp64 MSE.
 These run only where the reference library is built (this container); elsewhere they skip.
 """
 import numpy as np
 import pytest
 
 from oracle import ref
-from tests.helpers import BEAM_CASES, DEGENERATE, beam_case, degenerate_problem, random_problem, rvq_problem
+from tests.helpers import BEAM_CASES, DEGENERATE, beam_case, degenerate_problem, parity, random_problem, rvq_problem
 
 pytestmark = pytest.mark.skipif(not ref.available(), reason="reference CPU encoder not built (make -C oracle ref)")
 
@@ -102,3 +110,53 @@ def test_large_root_expansion_matches_reference(orc, mode, Hb):
                                                 root_mode=root_mode)
     assert np.array_equal(cid_r, cid_o)
     assert np.array_equal(Bs_r, Bs_o)
+
+
+def _ls_problem(orc, m, seed=90):
+    h = [64] * m
+    X, C = rvq_problem(seed + m, 2000, 32, m, 64, kind="gauss", train_n=2000, iters=3)
+    G, inv = orc.build_precomp(C, h)
+    xC = orc.gemm_xc(C, X)
+    nx2 = orc.xnorm2(X)
+    codes, _ = orc.beam_search(nx2, xC, G, h, 4)
+    return X, C, h, G, inv, xC, nx2, codes
+
+
+@pytest.mark.parametrize("m", [1, 5, 10])
+def test_ls_matches_reference_own_cholesky(orc, m):
+    X, C, h, G, inv, xC, nx2, codes = _ls_problem(orc, m)
+    a_o, _ = orc.solve_ls_all(xC, G, h, codes)
+    assert np.array_equal(_bits(ref.solve_ls_all(xC, G, h, codes)), _bits(a_o))
+
+
+@pytest.mark.parametrize("use_abs", [True, False])
+@pytest.mark.parametrize("m", [1, 5, 10])
+def test_icm_matches_reference(orc, m, use_abs):
+    X, C, h, G, inv, xC, nx2, codes = _ls_problem(orc, m)
+    k_o, a_o, c_o, _ = orc.icm(xC, G, inv, h, nx2, codes, 3, use_abs, 38251450)
+    k_r, a_r, c_r = ref.icm(X, xC, G, inv, h, codes, 3, use_abs, 38251450)
+    assert np.array_equal(k_o, k_r)
+    assert np.array_equal(_bits(a_o), _bits(a_r))
+    assert np.array_equal(_bits(c_o), _bits(c_r))
+
+
+@pytest.mark.parametrize("m", [2, 3, 4, 8, 16])
+def test_ls_lapack_path_same_solution_quality(orc, m):
+    """Reference LS through LAPACK vs the oracle's Cholesky: rounding-level differences only."""
+    X, C, h, G, inv, xC, nx2, codes = _ls_problem(orc, m)
+    a_o, _ = orc.solve_ls_all(xC, G, h, codes)
+    a_r = ref.solve_ls_all(xC, G, h, codes)
+    mse_o = orc.mse_from_precomp(X, xC, G, h, codes, a_o)
+    mse_r = orc.mse_from_precomp(X, xC, G, h, codes, a_r)
+    assert np.max(np.abs(mse_o - mse_r) / np.maximum(np.abs(mse_r), 1e-30)) <= 1e-9
+
+
+@pytest.mark.parametrize("m", [3, 8, 16])
+def test_icm_lapack_path_differs_only_on_ties(orc, m):
+    """ICM whose LS goes through LAPACK in the reference: the accepted moves can flip where two
+    tuples' costs are equal up to the LS rounding; every such vector ties within 1e-5."""
+    X, C, h, G, inv, xC, nx2, codes = _ls_problem(orc, m)
+    k_o, _, _, _ = orc.icm(xC, G, inv, h, nx2, codes, 2, True, 38251450)
+    k_r, _, _ = ref.icm(X, xC, G, inv, h, codes, 2, True, 38251450)
+    rep = parity(orc, X, C, h, k_r, k_o, max_frac=0.03)
+    assert rep["ok"], rep
