@@ -85,22 +85,79 @@ __device__ __forceinline__ void RecomputeWorst(float s_err, int Hb, int rows, in
     worst = mx;
 }
 
+// Lane i receives lane i+1's value across the whole wave (DPP wave_shl:1); lane 63 keeps its own.
+__device__ __forceinline__ float WaveShl1(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x130, 0xF, 0xF, false));
+}
+__device__ __forceinline__ int WaveShl1(int v) { return __builtin_amdgcn_update_dpp(v, v, 0x130, 0xF, 0xF, false); }
+
+// Selection state of one vector's streaming top-H (beam_search.cpp:301-333).
+//  s_err/s_cand: slot h in lane h (the reference's errs/candidate of slot h).
+//  sv/ss: the same Hb (error, slot) pairs kept sorted in lanes 0..Hb-1 by the order in which
+//    RecomputeWorst (beam_search.cpp:101-113) picks the worst: larger error first, and among
+//    equal errors the lower slot. Lane 0 is then the worst slot, so an insertion needs no
+//    reduction: the new pair moves to its rank and the pairs above it shift down one lane.
+//  The order is only defined without NaN. The first NaN candidate that would enter switches
+//  the vector to `slow` for the rest of the layer, which recomputes the worst by a first-max
+//  scan with the reference's NaN comparisons.
+struct TopH {
+    float s_err = __builtin_huge_valf();
+    int s_cand = -1;
+    float worst = __builtin_huge_valf();
+    int widx = 0;
+    float sv = __builtin_huge_valf();
+    int ss = 0;
+    bool slow = false;
+    __device__ explicit TopH(int lane) : ss(lane) {}
+};
+
+// Lane mask of a predicate (the raw wave ballot: no bool-to-int round trip through a VGPR).
+__device__ __forceinline__ uint64_t Ballot(bool b) { return __builtin_amdgcn_ballot_w64(b); }
+
 // Replays the streaming top-H over one chunk of 64 candidates in lane (= scan) order.
 // Candidate `lane` is eligible when ok; it is inserted when !(e >= worst)
-// (beam_search.cpp:320: `if (e >= worst_err) continue;`).
-__device__ __forceinline__ void ReplayChunk(bool ok, float e, int cand_base, int Hb, int rows, int lane,
-                                            float& s_err, int& s_cand, float& worst, int& widx) {
-    uint64_t mask = __ballot(ok && !(e >= worst));
+// (beam_search.cpp:320: `if (e >= worst_err) continue;`), into the worst slot.
+__device__ __forceinline__ void ReplayChunk(bool ok, float e, int cand_base, int Hb, int rows, int lane, TopH& t) {
+    const uint64_t okm = Ballot(ok);
+    uint64_t mask = okm & Ballot(!(e >= t.worst));
+    if (!mask) return;
+    if (!t.slow && (Ballot(__builtin_isnan(e)) & mask) != 0ull) t.slow = true;
+    if (t.slow) {
+        while (mask) {
+            const int l = static_cast<int>(__builtin_ctzll(mask));
+            const float ev = ReadLane(e, l);
+            if (lane == t.widx) {
+                t.s_err = ev;
+                t.s_cand = cand_base + l;
+            }
+            RecomputeWorst(t.s_err, Hb, rows, lane, t.worst, t.widx);
+            const uint64_t later = (l >= 63) ? 0ull : (~0ull << (l + 1));
+            mask = okm & Ballot(!(e >= t.worst)) & later;
+        }
+        return;
+    }
+    // lanes 1..Hb-1 of the sorted list: the pairs that stay when lane 0 (the worst) is evicted
+    const uint64_t keep = (Hb >= 64 ? ~0ull : ((1ull << Hb) - 1ull)) & ~1ull;
     while (mask) {
         const int l = static_cast<int>(__builtin_ctzll(mask));
         const float ev = ReadLane(e, l);
-        if (lane == widx) {
-            s_err = ev;
-            s_cand = cand_base + l;
-        }
-        RecomputeWorst(s_err, Hb, rows, lane, worst, widx);
+        const int w = t.widx;
+        const bool at_w = lane == w;
+        t.s_err = at_w ? ev : t.s_err;
+        t.s_cand = at_w ? cand_base + l : t.s_cand;
+        // rank of the new pair: remaining pairs ordered before it (larger error, or equal error
+        // and lower slot), evaluated without branches
+        const uint64_t before = (Ballot(t.sv > ev) | (Ballot(t.sv == ev) & Ballot(t.ss < w))) & keep;
+        const int r = __popcll(before);
+        const float shv = WaveShl1(t.sv);
+        const int shs = WaveShl1(t.ss);
+        const bool lt = lane < r, eq = lane == r;
+        t.sv = lt ? shv : (eq ? ev : t.sv);
+        t.ss = lt ? shs : (eq ? w : t.ss);
+        t.worst = ReadLane(t.sv, 0);
+        t.widx = __builtin_amdgcn_readlane(t.ss, 0);
         const uint64_t later = (l >= 63) ? 0ull : (~0ull << (l + 1));
-        mask = __ballot(ok && !(e >= worst)) & later;
+        mask = okm & Ballot(!(e >= t.worst)) & later;
     }
 }
 
@@ -199,10 +256,7 @@ __global__ __launch_bounds__(256) void Layer0Kernel(LayerArgs p) {
     const float nx2 = p.nx2[i];
     const float* xCi = p.xC + i * p.ldx;
 
-    float s_err = kInfF;
-    int s_cand = -1;
-    float worst = kInfF;
-    int widx = 0;
+    TopH top(lane);
     const int nch = (K + kWave - 1) / kWave;
     for (int j = 0; j < nch; ++j) {
         const int k = lane + kWave * j;
@@ -212,8 +266,10 @@ __global__ __launch_bounds__(256) void Layer0Kernel(LayerArgs p) {
         const float gamma = act ? xCi[off0 + k] : 0.0f;
         const float a1 = gamma / alpha;
         const float e1 = nx2 - gamma * a1;
-        ReplayChunk(ok, e1, kWave * j, Hb, rows, lane, s_err, s_cand, worst, widx);
+        ReplayChunk(ok, e1, kWave * j, Hb, rows, lane, top);
     }
+    const float s_err = top.s_err;
+    const int s_cand = top.s_cand;
 
     const int curH = __popcll(__ballot(lane < Hb && s_err < kInfF));  // CountFinite, no max(1,.)
     // Insertion-time write-back of the surviving slot contents (beam_search.cpp:253-258).
@@ -271,29 +327,53 @@ __global__ __launch_bounds__(256) void LayerKernel(LayerArgs p) {
         alp[j] = act ? p.gdiag[offL + k] : 0.0f;
     }
 
-    float s_err = kInfF;
-    int s_cand = -1;
-    float worst = kInfF;
-    int widx = 0;
+    TopH top(lane);
     const int curH = p.in.curH[i];
 
-    for (int h = 0; h < curH; ++h) {
+    // Beam slot h's codes (and root) sit in lane h, read with one vector load per word for all
+    // slots at once, so a slot's G rows can be addressed without waiting for its record.
+    constexpr int kCodeWords = (L + 3) / 4;
+    uint32_t cw[kCodeWords];
+    uint32_t rootw = 0;
+    {
+        const uint32_t* rl = reinterpret_cast<const uint32_t*>(recs_in + (lane < curH ? lane : 0) * rc.stride);
+#pragma unroll
+        for (int w = 0; w < kCodeWords; ++w) cw[w] = rl[rc.code + w];
+        if (LR) rootw = rl[rc.root];
+    }
+    // G rows of slot h: A[j][t] = G(prefix_t, offL + lane + 64 j) (the large root's prefix 0 reads
+    // G0S(root, .)).
+    auto load_rows = [&](int h, float (&A)[kMaxChunks][L]) {
+        const float* rowp[L];
+#pragma unroll
+        for (int t = 0; t < L; ++t) {
+            if (LR && t == 0) {
+                const uint32_t root = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(rootw), h));
+                rowp[t] = p.gram.G0S + static_cast<int64_t>(root) * ld + offL + lane;
+            } else {
+                const uint32_t word = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(cw[t >> 2]), h));
+                const uint32_t code = (word >> (8 * (t & 3))) & 0xFFu;
+                rowp[t] = G + static_cast<uint32_t>(p.gram.off[t] + static_cast<int>(code)) * static_cast<uint32_t>(ld);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < kMaxChunks; ++j) {
+#pragma unroll
+            for (int t = 0; t < L; ++t) {
+                const bool act = FULL || (j < nch && lane + kWave * j < K);
+                A[j][t] = act ? rowp[t][kWave * j] : 0.0f;
+            }
+        }
+    };
+    // Evaluates slot h's candidates and replays them into the top-H (scan order: slot, then code).
+    auto process = [&](int h, const float (&A)[kMaxChunks][L]) {
         const float* rec = recs_in + h * rc.stride;
         const float E_old = rec[0];
         float aold[L];
         float Rv[L][L];
         float Ri[L];
-        const float* rowp[L];
 #pragma unroll
-        for (int t = 0; t < L; ++t) {
-            aold[t] = rec[rc.coef + t];
-            if (LR && t == 0) {
-                const uint32_t root = reinterpret_cast<const uint32_t*>(rec)[rc.root];
-                rowp[t] = p.gram.G0S + static_cast<int64_t>(root) * ld + offL + lane;
-            } else {
-                rowp[t] = G + static_cast<uint32_t>(p.gram.off[t] + CodeAt(rec, rc.code, t)) * static_cast<uint32_t>(ld);
-            }
-        }
+        for (int t = 0; t < L; ++t) aold[t] = rec[rc.coef + t];
         bool diag_fast = !LR;
 #pragma unroll
         for (int r = 0; r < L; ++r) {
@@ -303,16 +383,6 @@ __global__ __launch_bounds__(256) void LayerKernel(LayerArgs p) {
             diag_fast = diag_fast && DiagFastOk(Rv[r][r]);
         }
         auto Rf = [&](int r, int c) { return Rv[r][c]; };
-
-        float A[kMaxChunks][L];
-#pragma unroll
-        for (int j = 0; j < kMaxChunks; ++j) {
-#pragma unroll
-            for (int t = 0; t < L; ++t) {
-                const bool act = FULL || (j < nch && lane + kWave * j < K);
-                A[j][t] = act ? rowp[t][kWave * j] : 0.0f;
-            }
-        }
 
         float ech[kMaxChunks];
         bool okc[kMaxChunks];
@@ -349,9 +419,17 @@ __global__ __launch_bounds__(256) void LayerKernel(LayerArgs p) {
         }
 #pragma unroll
         for (int j = 0; j < kMaxChunks; ++j) {
-            if (FULL || j < nch) ReplayChunk(okc[j], ech[j], h * K + kWave * j, Hb, rows, lane, s_err, s_cand, worst, widx);
+            if (FULL || j < nch) ReplayChunk(okc[j], ech[j], h * K + kWave * j, Hb, rows, lane, top);
         }
+    };
+
+    for (int h = 0; h < curH; ++h) {
+        float A[kMaxChunks][L];
+        load_rows(h, A);
+        process(h, A);
     }
+    const float s_err = top.s_err;
+    const int s_cand = top.s_cand;
 
     // Deferred write-back (beam_search.cpp:337-383) or the all-skipped fallback (:385-400).
     const int newH = __popcll(__ballot(lane < Hb && s_err < kInfF));
@@ -508,8 +586,7 @@ __global__ __launch_bounds__(256) void RootSeedKernel(RootArgs p) {
             }
         }
     } else {
-        float worst = kInfF;
-        int widx = 0;
+        TopH top(lane);
         const float* sc = p.scores + i * p.ldx;
         for (int c0 = 0; c0 < p.h0; c0 += kWave) {
             const int code = c0 + lane;
@@ -519,8 +596,10 @@ __global__ __launch_bounds__(256) void RootSeedKernel(RootArgs p) {
             const float gamma = act ? sc[code] : 0.0f;
             const float a1 = gamma / alpha;
             const float e1 = nx2 - gamma * a1;
-            ReplayChunk(ok, e1, c0, rs, rows, lane, s_err, s_cand, worst, widx);
+            ReplayChunk(ok, e1, c0, rs, rows, lane, top);
         }
+        s_err = top.s_err;
+        s_cand = top.s_cand;
     }
     const bool seeded = lane < rs && !(s_err >= kInfF);
     const int curH = max(1, __popcll(__ballot(seeded)));
