@@ -196,7 +196,7 @@ int stlq_mi355_last_timings(stlq_mi355_ctx* ctx, stlq_mi355_timings* out);
 
 /* BuildPrecompLargeRoot (src/quantizer/precomp_large_root.cpp:27-157,
  * include/stlq/quantizer/precomp_large_root.h:52-56): layer 0 is a large root codebook
- * C0 (d x h0, any h0 >= 1), layers 1..m-1 are C_small (d x Hs, h_vec[l] <= 256). Computes
+ * C0 (d x h0, 1 <= h0 <= 2^26 - 2), layers 1..m-1 are C_small (d x Hs, h_vec[l] <= 256). Computes
  * norm0, G_small and G0S (h0 x Hs) on the device. */
 int stlq_mi355_set_large_root(stlq_mi355_ctx* ctx, int d, int m, const int* h_vec,
                               const float* C0, const float* C_small);

@@ -1094,7 +1094,8 @@ extern "C" {
 int stlq_mi355_set_large_root(stlq_mi355_ctx* c, int d, int m, const int* h_vec, const float* C0,
                               const float* C_small) {
     RC_TRY(CheckCtx(c));
-    RC_TRY(ValidateLayers(d, m, h_vec, 1 << 30));
+    // root ids travel in the 26-bit candidate field of the beam's selection keys
+    RC_TRY(ValidateLayers(d, m, h_vec, (1 << 26) - 2));
     if (!C0 || (m > 1 && !C_small)) return Fail(STLQ_MI355_ERR_INVALID, "null codebooks");
     c->has_lr = false;
     c->lr_d = d;

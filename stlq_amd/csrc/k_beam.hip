@@ -20,6 +20,8 @@
 // (Markstein's theorem) as long as nothing over- or underflows; the kernel takes it only when
 // R(i,i) lies in [2^-20, 2^20] and every numerator magnitude in [2^-100, 2^100], and otherwise
 // re-evaluates the chunk with IEEE division. tests/division_check.c verifies the identity.
+#include <type_traits>
+
 #include "internal.hpp"
 
 namespace stlq_mi355 {
@@ -85,44 +87,86 @@ __device__ __forceinline__ void RecomputeWorst(float s_err, int Hb, int rows, in
     worst = mx;
 }
 
-// Lane i receives lane i+1's value across the whole wave (DPP wave_shl:1); lane 63 keeps its own.
-__device__ __forceinline__ float WaveShl1(float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x130, 0xF, 0xF, false));
-}
-__device__ __forceinline__ int WaveShl1(int v) { return __builtin_amdgcn_update_dpp(v, v, 0x130, 0xF, 0xF, false); }
-
-// Selection state of one vector's streaming top-H (beam_search.cpp:301-333).
-//  s_err/s_cand: slot h in lane h (the reference's errs/candidate of slot h).
-//  sv/ss: the same Hb (error, slot) pairs kept sorted in lanes 0..Hb-1 by the order in which
-//    RecomputeWorst (beam_search.cpp:101-113) picks the worst: larger error first, and among
-//    equal errors the lower slot. Lane 0 is then the worst slot, so an insertion needs no
-//    reduction: the new pair moves to its rank and the pairs above it shift down one lane.
-//  The order is only defined without NaN. The first NaN candidate that would enter switches
-//  the vector to `slow` for the rest of the layer, which recomputes the worst by a first-max
-//  scan with the reference's NaN comparisons.
-struct TopH {
-    float s_err = __builtin_huge_valf();
-    int s_cand = -1;
-    float worst = __builtin_huge_valf();
-    int widx = 0;
-    float sv = __builtin_huge_valf();
-    int ss = 0;
-    bool slow = false;
-    __device__ explicit TopH(int lane) : ss(lane) {}
-};
-
 // Lane mask of a predicate (the raw wave ballot: no bool-to-int round trip through a VGPR).
 __device__ __forceinline__ uint64_t Ballot(bool b) { return __builtin_amdgcn_ballot_w64(b); }
+
+// Order-preserving unsigned image of a non-NaN float (negative values reversed below the
+// positive ones). -0 is kept out of the fast path, so equal errors have equal images.
+__device__ __forceinline__ uint32_t OrderBits(float v) {
+    const uint32_t b = __float_as_uint(v);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+__device__ __forceinline__ float FromOrderBits(uint32_t o) {
+    return __uint_as_float((o & 0x80000000u) ? (o & 0x7FFFFFFFu) : ~o);
+}
+
+// Selection state of one vector's streaming top-H (beam_search.cpp:301-333).
+//  Fast path: lane q (< Hb) holds one slot's 64-bit key [OrderBits(err) | 63-slot (6 bits) |
+//    candidate (26 bits)], kept in descending key order. A larger key is the slot RecomputeWorst
+//    (beam_search.cpp:101-113) would pick first: larger error, and among equal errors the lower
+//    slot. Lane 0 is therefore the worst slot, and an insertion is a rank (one 64-bit compare and
+//    a ballot), a one-lane shift of the keys above the rank, and a select.
+//  s_err/s_cand (slot h in lane h) are rebuilt from the keys when the fast path ends (ToSlots).
+//  A NaN or -0 candidate that would enter switches the vector to `slow` for the rest of the
+//  layer: slot arrays with a first-max scan that follows the reference's NaN comparisons.
+constexpr uint32_t kNoCand = (1u << 26) - 1u;
+
+struct TopH {
+    uint64_t key;
+    uint32_t whi, wlo;  // key of lane 0 (the worst slot) while on the fast path
+    float worst = __builtin_huge_valf();
+    int widx = 0;
+    bool slow = false;
+    float s_err = __builtin_huge_valf();
+    int s_cand = -1;
+    __device__ explicit TopH(int lane)
+        : key((static_cast<uint64_t>(OrderBits(__builtin_huge_valf())) << 32) |
+              (static_cast<uint64_t>(63 - lane) << 26) | kNoCand),
+          whi(OrderBits(__builtin_huge_valf())),
+          wlo((63u << 26) | kNoCand) {}
+};
+
+// Lane i receives lane i+1's value across the whole wave (DPP wave_shl:1); lane 63 keeps its own.
+// (bound_ctrl: lane 63 reads 0; callers never take lane 63's value.)
+__device__ __forceinline__ uint64_t WaveShl1(uint64_t v) {
+    const int lo = __builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x130, 0xF, 0xF, true);
+    const int hi = __builtin_amdgcn_update_dpp(0, static_cast<int>(v >> 32), 0x130, 0xF, 0xF, true);
+    return (static_cast<uint64_t>(static_cast<uint32_t>(hi)) << 32) | static_cast<uint32_t>(lo);
+}
+
+// Slot-indexed view of the sorted keys: lane h receives the error and candidate of slot h; the
+// worst slot as RecomputeWorst names it.
+__device__ __forceinline__ void ToSlots(TopH& t) {
+    t.worst = FromOrderBits(t.whi);
+    t.widx = 63 - static_cast<int>(t.wlo >> 26);
+    const uint32_t lo = static_cast<uint32_t>(t.key);
+    const int slot = 63 - static_cast<int>((lo >> 26) & 63u);
+    const uint32_t c = lo & kNoCand;
+    const float err = FromOrderBits(static_cast<uint32_t>(t.key >> 32));
+    t.s_err = __int_as_float(__builtin_amdgcn_ds_permute(slot << 2, __float_as_int(err)));
+    const int cand = __builtin_amdgcn_ds_permute(slot << 2, static_cast<int>(c));
+    t.s_cand = cand == static_cast<int>(kNoCand) ? -1 : cand;
+}
+
+// Ends the fast path of a layer (no-op after a switch to the slow path).
+__device__ __forceinline__ void Finish(TopH& t) {
+    if (!t.slow) ToSlots(t);
+}
 
 // Replays the streaming top-H over one chunk of 64 candidates in lane (= scan) order.
 // Candidate `lane` is eligible when ok; it is inserted when !(e >= worst)
 // (beam_search.cpp:320: `if (e >= worst_err) continue;`), into the worst slot.
+// cand_base + lane must stay below 2^26 - 1 (callers check).
 __device__ __forceinline__ void ReplayChunk(bool ok, float e, int cand_base, int Hb, int rows, int lane, TopH& t) {
     const uint64_t okm = Ballot(ok);
-    uint64_t mask = okm & Ballot(!(e >= t.worst));
-    if (!mask) return;
-    if (!t.slow && (Ballot(__builtin_isnan(e)) & mask) != 0ull) t.slow = true;
+    if (!okm) return;
+    // NaN (either kind) or -0 among the candidates: leave the key order (NaN always enters)
+    if (!t.slow && (Ballot(__builtin_amdgcn_class(e, 0x23)) & okm) != 0ull) {
+        ToSlots(t);
+        t.slow = true;
+    }
     if (t.slow) {
+        uint64_t mask = okm & Ballot(!(e >= t.worst));
         while (mask) {
             const int l = static_cast<int>(__builtin_ctzll(mask));
             const float ev = ReadLane(e, l);
@@ -131,33 +175,27 @@ __device__ __forceinline__ void ReplayChunk(bool ok, float e, int cand_base, int
                 t.s_cand = cand_base + l;
             }
             RecomputeWorst(t.s_err, Hb, rows, lane, t.worst, t.widx);
-            const uint64_t later = (l >= 63) ? 0ull : (~0ull << (l + 1));
-            mask = okm & Ballot(!(e >= t.worst)) & later;
+            mask = (mask & (mask - 1ull)) & Ballot(!(e >= t.worst));
         }
         return;
     }
-    // lanes 1..Hb-1 of the sorted list: the pairs that stay when lane 0 (the worst) is evicted
+    // Without NaN and -0, e < worst exactly when OrderBits(e) < OrderBits(worst).
+    const uint32_t oe = OrderBits(e);
+    uint64_t mask = okm & Ballot(oe < t.whi);
+    // lanes 1..Hb-1 of the sorted keys: the ones that stay when lane 0 (the worst) is evicted
     const uint64_t keep = (Hb >= 64 ? ~0ull : ((1ull << Hb) - 1ull)) & ~1ull;
     while (mask) {
         const int l = static_cast<int>(__builtin_ctzll(mask));
-        const float ev = ReadLane(e, l);
-        const int w = t.widx;
-        const bool at_w = lane == w;
-        t.s_err = at_w ? ev : t.s_err;
-        t.s_cand = at_w ? cand_base + l : t.s_cand;
-        // rank of the new pair: remaining pairs ordered before it (larger error, or equal error
-        // and lower slot), evaluated without branches
-        const uint64_t before = (Ballot(t.sv > ev) | (Ballot(t.sv == ev) & Ballot(t.ss < w))) & keep;
-        const int r = __popcll(before);
-        const float shv = WaveShl1(t.sv);
-        const int shs = WaveShl1(t.ss);
-        const bool lt = lane < r, eq = lane == r;
-        t.sv = lt ? shv : (eq ? ev : t.sv);
-        t.ss = lt ? shs : (eq ? w : t.ss);
-        t.worst = ReadLane(t.sv, 0);
-        t.widx = __builtin_amdgcn_readlane(t.ss, 0);
-        const uint64_t later = (l >= 63) ? 0ull : (~0ull << (l + 1));
-        mask = okm & Ballot(!(e >= t.worst)) & later;
+        // the new pair takes the evicted slot: the slot field of lane 0's key
+        const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(oe), l));
+        const uint32_t lo = (t.wlo & 0xFC000000u) | static_cast<uint32_t>(cand_base + l);
+        const uint64_t nk = (static_cast<uint64_t>(hi) << 32) | lo;
+        const int r = __popcll(Ballot(t.key > nk) & keep);
+        const uint64_t sh = WaveShl1(t.key);
+        t.key = lane < r ? sh : (lane == r ? nk : t.key);
+        t.whi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(t.key >> 32), 0));
+        t.wlo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(t.key), 0));
+        mask = (mask ^ (1ull << l)) & Ballot(oe < t.whi);
     }
 }
 
@@ -175,11 +213,12 @@ __device__ __forceinline__ int BestSlot(float err, int curH, int lane) {
 
 // Record layout of one beam slot (dword offsets); RecStride(m) dwords per slot.
 struct Rec {
-    int coef, R, code, root, stride;
+    int coef, R, rinv, code, root, stride;
     __host__ __device__ explicit Rec(int m) {
         coef = 1;
         R = 1 + m;
-        code = R + TriSize(m);
+        rinv = R + TriSize(m);  // RN(1/R(r,r)) of the diagonal, formed once when the slot is made
+        code = rinv + m;
         root = code + CodeStride(m) / 4;
         stride = (root + 1 + 3) & ~3;
     }
@@ -190,13 +229,17 @@ __device__ __forceinline__ int CodeAt(const float* rec, int code_off, int t) {
     return static_cast<int>((w >> (8 * (t & 3))) & 0xFFu);
 }
 
-// Quotient s/d given y = RN(1/d): exact when `safe` (see the file comment).
-__device__ __forceinline__ float QuotFast(float s, float d, float y, bool& safe) {
+// Quotient s/d given y = RN(1/d); exact when every numerator's magnitude lies in
+// [2^-100, 2^100] (see the file comment), which the caller checks from the running extremes
+// lo = min |s| and hi = max |s|. A NaN numerator leaves lo/hi untouched: its quotient and every
+// value that depends on it are NaN on either path.
+__device__ __forceinline__ float QuotFast(float s, float d, float y, float& lo, float& hi) {
     const float q0 = s * y;
     const float r = __builtin_fmaf(d, q0, -s);
     const float q = __builtin_fmaf(-r, y, q0);
     const float as = __builtin_fabsf(s);
-    safe = safe && (as >= 0x1p-100f) && (as <= 0x1p100f);
+    lo = __builtin_fminf(lo, as);
+    hi = __builtin_fmaxf(hi, as);
     return q;
 }
 
@@ -206,19 +249,21 @@ __device__ __forceinline__ bool DiagFastOk(float d) { return d >= 0x1p-20f && d 
 // (linear_algebra.cpp:57-77; the large-root expansion multiplies by 1/diag instead,
 // beam_search.cpp:544-547/569-572), delta = A.v, eta = A.a_old, then
 // a_last = (gamma - eta)/(alpha - delta), e = max(E_old - diff*a_last, 0).
-// MODE 0: IEEE division; 1: Markstein quotient with reciprocal table `rinv` (sets `safe`);
+// MODE 0: IEEE division; 1: Markstein quotient with reciprocal table `rinv` (clears `safe` when
+// a numerator leaves the exact range);
 // 2: reciprocal multiply (large-root semantics).
 template <int L, int MODE, typename RFn>
 __device__ __forceinline__ void EvalCand(RFn R, const float (&rinv)[L], const float (&A)[L], const float (&aold)[L],
                                          float E_old, float alpha, float gamma, float (&y)[L], float (&v)[L],
                                          float& e, float& denom, float& a_last, bool& ok, bool& safe) {
+    float lo = __builtin_huge_valf(), hi = 0.0f;
 #pragma unroll
     for (int r = 0; r < L; ++r) {
         float s = A[r];
 #pragma unroll
         for (int j = 0; j < r; ++j) s = s - R(j, r) * y[j];
         if (MODE == 0) y[r] = s / R(r, r);
-        else if (MODE == 1) y[r] = QuotFast(s, R(r, r), rinv[r], safe);
+        else if (MODE == 1) y[r] = QuotFast(s, R(r, r), rinv[r], lo, hi);
         else y[r] = s * rinv[r];
     }
 #pragma unroll
@@ -227,9 +272,10 @@ __device__ __forceinline__ void EvalCand(RFn R, const float (&rinv)[L], const fl
 #pragma unroll
         for (int j = r + 1; j < L; ++j) s = s - R(r, j) * v[j];
         if (MODE == 0) v[r] = s / R(r, r);
-        else if (MODE == 1) v[r] = QuotFast(s, R(r, r), rinv[r], safe);
+        else if (MODE == 1) v[r] = QuotFast(s, R(r, r), rinv[r], lo, hi);
         else v[r] = s * rinv[r];
     }
+    if (MODE == 1) safe = safe && (lo >= 0x1p-100f) && (hi <= 0x1p100f);
     float delta = 0.0f, eta = 0.0f;
 #pragma unroll
     for (int t = 0; t < L; ++t) {
@@ -268,6 +314,7 @@ __global__ __launch_bounds__(256) void Layer0Kernel(LayerArgs p) {
         const float e1 = nx2 - gamma * a1;
         ReplayChunk(ok, e1, kWave * j, Hb, rows, lane, top);
     }
+    Finish(top);
     const float s_err = top.s_err;
     const int s_cand = top.s_cand;
 
@@ -287,6 +334,7 @@ __global__ __launch_bounds__(256) void Layer0Kernel(LayerArgs p) {
         rec[0] = s_err;
         rec[rc.coef] = a0;
         rec[rc.R] = r00;
+        rec[rc.rinv] = 1.0f / r00;
         reinterpret_cast<uint32_t*>(rec + rc.code)[0] = c0;
         reinterpret_cast<uint32_t*>(rec)[rc.root] = 0u;
     }
@@ -379,43 +427,39 @@ __global__ __launch_bounds__(256) void LayerKernel(LayerArgs p) {
         for (int r = 0; r < L; ++r) {
 #pragma unroll
             for (int c = r; c < L; ++c) Rv[r][c] = rec[rc.R + TriIdx(m, r, c)];
-            Ri[r] = 1.0f / Rv[r][r];
+            Ri[r] = rec[rc.rinv + r];
             diag_fast = diag_fast && DiagFastOk(Rv[r][r]);
         }
         auto Rf = [&](int r, int c) { return Rv[r][c]; };
 
         float ech[kMaxChunks];
         bool okc[kMaxChunks];
-        bool safe = true;
-#pragma unroll
-        for (int j = 0; j < kMaxChunks; ++j) {
-            ech[j] = kInfF;
-            okc[j] = false;
-            if (!FULL && j >= nch) continue;
-            float y[L], v[L], denom, a_last, e;
-            bool ok;
-            if (LR) {
-                EvalCand<L, 2>(Rf, Ri, A[j], aold, E_old, alp[j], gam[j], y, v, e, denom, a_last, ok, safe);
-            } else if (diag_fast) {
-                EvalCand<L, 1>(Rf, Ri, A[j], aold, E_old, alp[j], gam[j], y, v, e, denom, a_last, ok, safe);
-            } else {
-                EvalCand<L, 0>(Rf, Ri, A[j], aold, E_old, alp[j], gam[j], y, v, e, denom, a_last, ok, safe);
-            }
-            ech[j] = e;
-            okc[j] = ok && (FULL || (j < nch && lane + kWave * j < K));
-        }
-        if (!LR && diag_fast && __ballot(!safe) != 0ull) {
-            // A numerator left the range where the reciprocal-corrected quotient is exact:
-            // re-evaluate this beam's chunks with IEEE division (rare).
+        // All chunks of the slot with one arithmetic mode (the choice is per slot), so the chunk
+        // loop below is straight-line code.
+        auto eval_all = [&](auto mode_tag, bool& safe) {
+            constexpr int MODE = decltype(mode_tag)::value;
 #pragma unroll
             for (int j = 0; j < kMaxChunks; ++j) {
+                ech[j] = kInfF;
+                okc[j] = false;
                 if (!FULL && j >= nch) continue;
                 float y[L], v[L], denom, a_last, e;
-                bool ok, unused = true;
-                EvalCand<L, 0>(Rf, Ri, A[j], aold, E_old, alp[j], gam[j], y, v, e, denom, a_last, ok, unused);
+                bool ok;
+                EvalCand<L, MODE>(Rf, Ri, A[j], aold, E_old, alp[j], gam[j], y, v, e, denom, a_last, ok, safe);
                 ech[j] = e;
                 okc[j] = ok && (FULL || (j < nch && lane + kWave * j < K));
             }
+        };
+        bool safe = true;
+        if (LR) {
+            eval_all(std::integral_constant<int, 2>(), safe);
+        } else if (diag_fast) {
+            eval_all(std::integral_constant<int, 1>(), safe);
+            // A numerator left the range where the reciprocal-corrected quotient is exact:
+            // re-evaluate this slot's chunks with IEEE division (rare).
+            if (Ballot(!safe) != 0ull) eval_all(std::integral_constant<int, 0>(), safe);
+        } else {
+            eval_all(std::integral_constant<int, 0>(), safe);
         }
 #pragma unroll
         for (int j = 0; j < kMaxChunks; ++j) {
@@ -428,6 +472,7 @@ __global__ __launch_bounds__(256) void LayerKernel(LayerArgs p) {
         load_rows(h, A);
         process(h, A);
     }
+    Finish(top);
     const float s_err = top.s_err;
     const int s_cand = top.s_cand;
 
@@ -457,8 +502,10 @@ __global__ __launch_bounds__(256) void LayerKernel(LayerArgs p) {
 #pragma unroll
                 for (int c = r; c < L; ++c) ro[rc.R + TriIdx(m, r, c)] = ri[rc.R + TriIdx(m, r, c)];
                 ro[rc.R + TriIdx(m, r, L)] = 0.0f;
+                ro[rc.rinv + r] = ri[rc.rinv + r];
             }
             ro[rc.R + TriIdx(m, L, L)] = 0.0f;
+            ro[rc.rinv + L] = 1.0f / 0.0f;
             nroot = reinterpret_cast<const uint32_t*>(ri)[rc.root];
         } else if (nh == 0 && lane == 0) {
             // No beam at all (layer 0 had no finite candidate): the reference's next-buffer slot 0
@@ -467,9 +514,11 @@ __global__ __launch_bounds__(256) void LayerKernel(LayerArgs p) {
 #pragma unroll
             for (int t = 0; t <= L; ++t) ro[rc.coef + t] = 0.0f;
 #pragma unroll
-            for (int r = 0; r <= L; ++r)
+            for (int r = 0; r <= L; ++r) {
 #pragma unroll
                 for (int c = r; c <= L; ++c) ro[rc.R + TriIdx(m, r, c)] = 0.0f;
+                ro[rc.rinv + r] = 1.0f / 0.0f;
+            }
         }
     } else {
         outH = max(1, newH);
@@ -485,7 +534,7 @@ __global__ __launch_bounds__(256) void LayerKernel(LayerArgs p) {
             for (int r = 0; r < L; ++r) {
 #pragma unroll
                 for (int c = r; c < L; ++c) Rv[r][c] = ri[rc.R + TriIdx(m, r, c)];
-                Ri[r] = 1.0f / Rv[r][r];
+                Ri[r] = ri[rc.rinv + r];
             }
 #pragma unroll
             for (int t = 0; t < L; ++t) {
@@ -518,8 +567,11 @@ __global__ __launch_bounds__(256) void LayerKernel(LayerArgs p) {
 #pragma unroll
                 for (int c = r; c < L; ++c) ro[rc.R + TriIdx(m, r, c)] = Rv[r][c];
                 ro[rc.R + TriIdx(m, r, L)] = y[r];
+                ro[rc.rinv + r] = Ri[r];
             }
-            ro[rc.R + TriIdx(m, L, L)] = sqrtf(denom);
+            const float rLL = sqrtf(denom);
+            ro[rc.R + TriIdx(m, L, L)] = rLL;
+            ro[rc.rinv + L] = 1.0f / rLL;
         }
     }
     if (lane < Hb) {
@@ -598,6 +650,7 @@ __global__ __launch_bounds__(256) void RootSeedKernel(RootArgs p) {
             const float e1 = nx2 - gamma * a1;
             ReplayChunk(ok, e1, c0, rs, rows, lane, top);
         }
+        Finish(top);
         s_err = top.s_err;
         s_cand = top.s_cand;
     }
@@ -617,6 +670,7 @@ __global__ __launch_bounds__(256) void RootSeedKernel(RootArgs p) {
         rec[0] = seeded ? s_err : kInfF;
         rec[rc.coef] = a0;
         rec[rc.R] = r00;
+        rec[rc.rinv] = 1.0f / r00;
         reinterpret_cast<uint32_t*>(rec + rc.code)[0] = 0u;
         reinterpret_cast<uint32_t*>(rec)[rc.root] = root;
     }
