@@ -36,6 +36,36 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def _profiled_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 summary of this workload
+    (FETCH_SIZE/WRITE_SIZE calibrated against a plain copy kernel), or None when it has no row."""
+    path = os.path.join(ROOT, "profiles", "c2_encode_hbm_traffic.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                cells = [c.strip() for c in line.strip().strip("|").split("|")]
+                if len(cells) == 5 and cells[0] == kernel:
+                    return (float(cells[3]) + float(cells[4])) * 1e9, os.path.relpath(path, ROOT)
+    except (OSError, ValueError):
+        pass
+    return None, None
+
+
+def _profiled_valu(kernel: str):
+    """VALU and SALU wave instructions per launch of `kernel` from the committed rocprofv3 SQ
+    counter summary of this workload, or (None, None, None)."""
+    path = os.path.join(ROOT, "profiles", "c2_encode_sq_counters.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                cells = [c.strip() for c in line.strip().strip("|").split("|")]
+                if len(cells) == 8 and cells[0] == kernel:
+                    return float(cells[1]), float(cells[2]), os.path.relpath(path, ROOT)
+    except (OSError, ValueError):
+        pass
+    return None, None, None
+
+
 def _cpu_model() -> str:
     try:
         with open("/proc/cpuinfo") as f:
@@ -147,6 +177,10 @@ def main():
         "device_total_ms": total_ms / steps,
     }
 
+    traffic, traffic_src = (_profiled_traffic(f"LayerKernel<{last}, false, true>") if args.config == "C2"
+                            else (None, None))
+    valu, salu, valu_src = (_profiled_valu(f"LayerKernel<{last}, false, true>") if args.config == "C2"
+                            else (None, None, None))
     metric = ("vectors encoded/sec (d=128,M=8,K=256,B=16)" if args.config == "C2" else
               f"vectors encoded/sec (d={d},M={M},K={K},B={B}" + (f",ICM={w.icm_iters})" if w.icm_iters else ")"))
     workload = {
@@ -180,9 +214,17 @@ def main():
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
             "frac": beam_ach / PEAK_HBM_GBS,
-            "traffic": None,
+            "traffic": traffic,
+            "traffic_source": traffic_src,
             "algorithmic_bytes_per_launch": sel_bytes,
             "avg_launch_ms": avg_last_ms,
+            # What bounds this kernel instead: VALU issue (exact fp32 candidate arithmetic and the
+            # top-H replay); wave instructions per launch from the SQ counters, rate at this run's
+            # launch time.
+            "valu_wave_insts_per_launch": valu,
+            "salu_wave_insts_per_launch": salu,
+            "valu_wave_insts_per_s": (valu / (avg_last_ms * 1e-3)) if valu else None,
+            "valu_source": valu_src,
         },
         "roofline_distance": {
             "kernel": "xC GEMM (GemmXcKernel, fp32 MFMA, lookup form)",

@@ -67,6 +67,7 @@ struct DevBuf {
 // One tile's event set; resolved lazily when timings are read.
 struct TileEvents {
     hipEvent_t e[7] = {};  // start, xnorm, gemm, beam, ls, icm, end
+    hipEvent_t gemm_end = nullptr;  // set when the GEMM ran on the aux stream (then e[2] = beam start)
     hipEvent_t lay[kMaxM + 1] = {};  // before layer 0, after each beam layer
     int layers = 0;
     int64_t n = 0;
@@ -87,6 +88,7 @@ struct stlq_mi355_ctx {
     int device = 0;
     hipStream_t stream = nullptr;
     hipStream_t copy_stream = nullptr;
+    hipStream_t aux_stream = nullptr;  // xC GEMM of the next sub-tile while the current one's beam runs
 
     // Full precomp (BuildPrecomp).
     bool has_pre = false;
@@ -117,9 +119,11 @@ struct stlq_mi355_ctx {
         }
         return event_pool[event_next++];
     }
+    bool overlapped = false;  // tiles of the last call overlapped in time (total = envelope)
     void ResetTimings() {
         tiles.clear();
         event_next = 0;
+        overlapped = false;
     }
 };
 
@@ -307,8 +311,117 @@ struct EncodeOut {
 };
 
 // One tile of EncodeBase on device-resident X.
+// Beam, LS refit + costs and ICM of one tile whose ||x||^2 and xC are already on the device.
+int BeamAndRefit(stlq_mi355_ctx* c, const float* dxC, const float* dnx2, int64_t n, const stlq_mi355_encode_params& P,
+                 const EncodeOut& o, hipStream_t s, TileEvents* te) {
+    const int Hb = std::max(1, P.H_beam);
+    auto rec = [&](int k) -> hipError_t {
+        if (!te) return hipSuccess;
+        te->e[k] = c->NextEvent();
+        return hipEventRecord(te->e[k], s);
+    };
+    RC_TRY(RunBeam(c, dxC, c->H, dnx2, n, Hb, o.codes, o.best, s, te ? &te->beam_launches : nullptr, te));
+    HIP_TRY(rec(3));
+    const bool need_ls = P.want_coeffs || P.icm_iters > 0;
+    float* da = o.a;
+    float* dcost = o.cost;
+    if (need_ls) {
+        if (!da) {
+            HIP_TRY(c->a.Ensure(static_cast<size_t>(n) * c->m * 4));
+            da = c->a.as<float>();
+        }
+        if (!dcost) {
+            HIP_TRY(c->cost.Ensure(static_cast<size_t>(n) * 4));
+            dcost = c->cost.as<float>();
+        }
+        LsArgs ls = MakeLs(c, dxC, c->H, o.codes, da, dnx2, dcost, n);
+        HIP_TRY(LaunchLsAll(ls, s));
+        HIP_TRY(LaunchCosts(ls, s));
+    }
+    HIP_TRY(rec(4));
+    if (P.icm_iters > 0) {
+        RC_TRY(RunIcm(c, dxC, c->H, dnx2, n, P.icm_iters, P.use_abs, P.seed, o.codes, da, dcost, s));
+    }
+    HIP_TRY(rec(5));
+    HIP_TRY(rec(6));
+    return STLQ_MI355_OK;
+}
+
+// Sub-tiles of a large tile: the xC GEMM (MFMA-bound) of sub-tile i+1 runs on the aux stream while
+// the beam (VALU-bound) of sub-tile i runs on `s`, so the two share the CUs. Two xC/||x||^2
+// buffers alternate; GEMM i+2 waits until sub-tile i's beam, LS and ICM are done with its buffer.
+// Sub-tile length, from STLQ_MI355_PIPE_SUB; unset or 0 keeps one tile. Off by default: on the
+// 1M-vector, 8 x 256, beam-16 encode the overlap saved about 1% of the wall time while the beam
+// layers ran slower beside the GEMM, and the GEMM's own timing stops being measurable.
+int64_t PipeSub() {
+    const char* v = std::getenv("STLQ_MI355_PIPE_SUB");
+    if (!v) return 0;
+    const long long x = std::atoll(v);
+    return x > 0 ? static_cast<int64_t>(x) : 0;
+}
+
+int EncodeTilePipelined(stlq_mi355_ctx* c, const float* dX, int64_t n, const stlq_mi355_encode_params& P,
+                        const EncodeOut& o, hipStream_t s, bool record) {
+    const int64_t sub = PipeSub();
+    const int64_t nsub = (n + sub - 1) / sub;
+    const size_t H = static_cast<size_t>(c->H), m = static_cast<size_t>(c->m);
+    HIP_TRY(c->nx2.Ensure(2 * static_cast<size_t>(sub) * 4));
+    HIP_TRY(c->xC.Ensure(2 * static_cast<size_t>(sub) * H * 4));
+    float* xcb[2] = {c->xC.as<float>(), c->xC.as<float>() + static_cast<size_t>(sub) * H};
+    float* nxb[2] = {c->nx2.as<float>(), c->nx2.as<float>() + sub};
+    hipStream_t aux = c->aux_stream;
+    std::vector<TileEvents> tes(static_cast<size_t>(nsub));
+    std::vector<hipEvent_t> gemm_done(static_cast<size_t>(nsub)), tile_done(static_cast<size_t>(nsub));
+    auto ev = [&](hipStream_t st) -> hipEvent_t {
+        hipEvent_t e = c->NextEvent();
+        if (e) (void)hipEventRecord(e, st);
+        return e;
+    };
+    // the aux stream starts after everything already queued on s (input copies, earlier calls)
+    hipEvent_t entry = ev(s);
+    if (!entry) return Fail(STLQ_MI355_ERR_HIP, "event creation failed");
+    HIP_TRY(hipStreamWaitEvent(aux, entry, 0));
+    auto launch_front = [&](int64_t i) -> int {
+        const int b = static_cast<int>(i & 1);
+        const int64_t off = i * sub, ni = std::min(sub, n - off);
+        if (i >= 2) HIP_TRY(hipStreamWaitEvent(aux, tile_done[static_cast<size_t>(i - 2)], 0));
+        TileEvents& te = tes[static_cast<size_t>(i)];
+        te.n = ni;
+        te.e[0] = ev(aux);
+        HIP_TRY(LaunchXNorm2(dX + off * c->d, c->d, ni, nxb[b], aux));
+        te.e[1] = ev(aux);
+        HIP_TRY(LaunchGemmXc(dX + off * c->d, ni, c->d, c->C_all.as<float>(), c->H, xcb[b], c->H, aux));
+        te.gemm_launches = 1;
+        te.gemm_end = gemm_done[static_cast<size_t>(i)] = ev(aux);
+        if (!te.e[0] || !te.e[1] || !te.gemm_end) return Fail(STLQ_MI355_ERR_HIP, "event creation failed");
+        return STLQ_MI355_OK;
+    };
+    RC_TRY(launch_front(0));
+    for (int64_t i = 0; i < nsub; ++i) {
+        if (i + 1 < nsub) RC_TRY(launch_front(i + 1));  // queued ahead of beam i so the two overlap
+        const int b = static_cast<int>(i & 1);
+        const int64_t off = i * sub, ni = std::min(sub, n - off);
+        HIP_TRY(hipStreamWaitEvent(s, gemm_done[static_cast<size_t>(i)], 0));
+        TileEvents& te = tes[static_cast<size_t>(i)];
+        te.e[2] = ev(s);
+        EncodeOut oi{o.codes + off * m, o.a ? o.a + off * m : nullptr, o.cost ? o.cost + off : nullptr,
+                     o.best ? o.best + off : nullptr};
+        RC_TRY(BeamAndRefit(c, xcb[b], nxb[b], ni, P, oi, s, &te));
+        tile_done[static_cast<size_t>(i)] = te.e[6];
+        if (!te.e[6]) return Fail(STLQ_MI355_ERR_HIP, "event creation failed");
+    }
+    if (record) {
+        for (const TileEvents& te : tes) c->tiles.push_back(te);
+        c->overlapped = true;
+    }
+    return STLQ_MI355_OK;
+}
+
+// allow_overlap = false keeps the whole tile's xC and ||x||^2 in c->xC / c->nx2 afterwards.
 int EncodeTile(stlq_mi355_ctx* c, const float* dX, int64_t n, const stlq_mi355_encode_params& P,
-               const EncodeOut& o, hipStream_t s, bool record) {
+               const EncodeOut& o, hipStream_t s, bool record, bool allow_overlap = true) {
+    const int64_t pipe = PipeSub();
+    if (allow_overlap && pipe > 0 && n >= 2 * pipe) return EncodeTilePipelined(c, dX, n, P, o, s, record);
     const int Hb = std::max(1, P.H_beam);
     HIP_TRY(c->nx2.Ensure(static_cast<size_t>(n) * 4));
     HIP_TRY(c->xC.Ensure(static_cast<size_t>(n) * c->H * 4));
@@ -387,7 +500,8 @@ int stlq_mi355_ctx_create(int device, stlq_mi355_ctx** out) {
     auto* c = new stlq_mi355_ctx();
     c->device = device;
     if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess ||
-        hipStreamCreateWithFlags(&c->copy_stream, hipStreamNonBlocking) != hipSuccess) {
+        hipStreamCreateWithFlags(&c->copy_stream, hipStreamNonBlocking) != hipSuccess ||
+        hipStreamCreateWithFlags(&c->aux_stream, hipStreamNonBlocking) != hipSuccess) {
         delete c;
         return Fail(STLQ_MI355_ERR_HIP, "stream creation failed");
     }
@@ -404,6 +518,7 @@ int stlq_mi355_ctx_destroy(stlq_mi355_ctx* c) {
     (void)hipSetDevice(c->device);
     (void)hipStreamSynchronize(c->stream);
     (void)hipStreamSynchronize(c->copy_stream);
+    (void)hipStreamSynchronize(c->aux_stream);
     DevBuf* bufs[] = {&c->C_all, &c->G_rm, &c->G_cm, &c->gdiag, &c->invnorm, &c->C0, &c->Cs, &c->norm0,
                       &c->G_small, &c->G0S, &c->gdiag_small, &c->X, &c->nx2, &c->xC, &c->xC_in, &c->codes, &c->a,
                       &c->cost, &c->best, &c->fails, &c->active, &c->changed, &c->mse, &c->gam0, &c->roots,
@@ -417,6 +532,7 @@ int stlq_mi355_ctx_destroy(stlq_mi355_ctx* c) {
     for (hipEvent_t e : c->event_pool) (void)hipEventDestroy(e);
     (void)hipStreamDestroy(c->stream);
     (void)hipStreamDestroy(c->copy_stream);
+    (void)hipStreamDestroy(c->aux_stream);
     delete c;
     return STLQ_MI355_OK;
 }
@@ -689,7 +805,7 @@ int stlq_mi355_encode(stlq_mi355_ctx* c, const float* X, int64_t n, const stlq_m
         if (want_mse && P.icm_iters > 0) {
             // Beam MSE before ICM: run the beam + LS alone first, then ICM on the same codes.
             Pt.icm_iters = 0;
-            RC_TRY(EncodeTile(c, c->X.as<float>(), nt, Pt, o, c->stream, true));
+            RC_TRY(EncodeTile(c, c->X.as<float>(), nt, Pt, o, c->stream, true, /*allow_overlap=*/false));
             beam_cost.resize(static_cast<size_t>(nt));
             HIP_TRY(hipMemcpyAsync(beam_cost.data(), c->cost.p, static_cast<size_t>(nt) * 4, hipMemcpyDeviceToHost,
                                    c->stream));
@@ -753,6 +869,7 @@ int stlq_mi355_last_timings(stlq_mi355_ctx* c, stlq_mi355_timings* out) {
         for (int k = 0; k < 6; ++k) {
             if (te.e[k] && te.e[k + 1] && te.e[k] != te.e[k + 1]) HIP_TRY(hipEventElapsedTime(&ms[k], te.e[k], te.e[k + 1]));
         }
+        if (te.gemm_end) HIP_TRY(hipEventElapsedTime(&ms[1], te.e[1], te.gemm_end));
         float tot = 0.0f;
         HIP_TRY(hipEventElapsedTime(&tot, te.e[0], te.e[6]));
         out->xnorm_ms += ms[0];
@@ -769,6 +886,11 @@ int stlq_mi355_last_timings(stlq_mi355_ctx* c, stlq_mi355_timings* out) {
             HIP_TRY(hipEventElapsedTime(&lm, te.lay[l], te.lay[l + 1]));
             out->layer_ms[l] += lm;
         }
+    }
+    if (c->overlapped && !c->tiles.empty()) {
+        float env = 0.0f;
+        HIP_TRY(hipEventElapsedTime(&env, c->tiles.front().e[0], c->tiles.back().e[6]));
+        out->total_ms = env;
     }
     return STLQ_MI355_OK;
 }

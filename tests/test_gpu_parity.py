@@ -254,6 +254,30 @@ def test_tiled_encode_matches_single_tile(ctx, orc, monkeypatch):
     assert np.array_equal(_bits(cost1), _bits(cost2))
 
 
+@pytest.mark.parametrize("sub", [700, 2500])
+def test_overlapped_subtiles_match_single_tile(ctx, orc, monkeypatch, sub):
+    """Sub-tiles whose xC GEMM overlaps the previous sub-tile's beam (two streams, alternating
+    buffers) give the same codes, coefficients, costs and MSE as one tile, with and without ICM."""
+    X, C = rvq_problem(52, 6001, 32, 4, 64, train_n=2000, iters=3)
+    h = [64] * 4
+    ctx.set_codebooks(C, h)
+    for icm in (2, 0):
+        cfg = EncodeConfig(H_beam=4, icm_iters=icm, want_coeffs=True)
+        want_mse = icm == 0  # (beam MSE before ICM keeps the whole tile's xC: no overlap there)
+        monkeypatch.setenv("STLQ_MI355_PIPE_SUB", "0")
+        codes1, a1, cost1, mse1 = ctx.encode(X, cfg, want_mse=want_mse)
+        monkeypatch.setenv("STLQ_MI355_PIPE_SUB", str(sub))
+        codes2, a2, cost2, mse2 = ctx.encode(X, cfg, want_mse=want_mse)
+        t = ctx.last_timings()
+        assert t.n == X.shape[0] and t.gemm_launches == -(-X.shape[0] // sub)
+        assert np.array_equal(codes1, codes2), icm
+        assert np.array_equal(_bits(a1), _bits(a2))
+        assert np.array_equal(_bits(cost1), _bits(cost2))
+        assert mse1 == mse2
+        codes3, _, _, _ = ctx.encode(X, cfg)  # again, reusing the buffers and events
+        assert np.array_equal(codes1, codes3)
+
+
 @pytest.mark.parametrize("chunk", [1000, 1777, 5000])
 def test_stream_matches_in_memory(ctx, chunk):
     from stlq_amd import workloads
