@@ -45,15 +45,14 @@ extern "C" {
 
 typedef struct stlq_mi355_ctx stlq_mi355_ctx;
 
-/* Encoder knobs of base.encode.* (include/stlq/common/config.h:473-482). ils_iters must be 0:
- * ILS perturbation is not part of this build. */
+/* Encoder knobs of base.encode.* (include/stlq/common/config.h:473-482). */
 typedef struct stlq_mi355_encode_params {
     int H_beam;      /* beam width; values < 1 are treated as 1 (encoder_encode_base.inc:39) */
     int icm_iters;   /* ICM sweeps after the beam (0 = none) */
-    int ils_iters;   /* must be 0 */
-    int perturb_k;   /* unused while ils_iters == 0 */
+    int ils_iters;   /* ILS rounds after the ICM (0 = none; icm.cpp:944-1001) */
+    int perturb_k;   /* codes perturbed per vector and ILS round (min(perturb_k, m)) */
     int use_abs;     /* |score| in the ICM code pick (DynamicIcmWithIlsAbsNoNormal) */
-    uint32_t seed;   /* ICM layer-order seed (std::mt19937) */
+    uint32_t seed;   /* ICM layer-order seed (std::mt19937) and ILS perturbation seed */
     int want_coeffs; /* also produce LS coefficients a and per-vector cost */
 } stlq_mi355_encode_params;
 
@@ -63,7 +62,7 @@ typedef struct stlq_mi355_timings {
     double gemm_ms;   /* xC = C_all^T X (fp32 MFMA) */
     double beam_ms;   /* all beam layers */
     double ls_ms;     /* LS refit + costs */
-    double icm_ms;
+    double icm_ms;    /* ICM and ILS */
     double total_ms;
     int64_t n;
     int gemm_launches;
@@ -126,6 +125,16 @@ int stlq_mi355_compute_costs(stlq_mi355_ctx* ctx, const float* xC, const uint8_t
 int stlq_mi355_icm(stlq_mi355_ctx* ctx, const float* X, const float* nx2, const float* xC,
                    int64_t n, int icm_iters, int use_abs, uint32_t seed, uint8_t* codes,
                    float* a, float* cost);
+
+/* DynamicIcmWithIls{Abs,NoAbs}NoNormal with the ILS outer loop (src/quantizer/icm.cpp:872-1003;
+ * include/stlq/quantizer/icm.h:15-43, the sample_id_offset argument): the ICM above, then
+ * ils_iters rounds of perturbing min(perturb_k, m) codes of layers 1..m-1 per vector (SplitMix64
+ * stream keyed by seed, round and sample_id_offset + i), ICM on the perturbed codes and
+ * accept-if-better (cand + 1e-6 < cost). ils_iters = 0 or perturb_k = 0 or m = 1 is the ICM. */
+int stlq_mi355_icm_ils(stlq_mi355_ctx* ctx, const float* X, const float* nx2, const float* xC,
+                       int64_t n, int icm_iters, int ils_iters, int perturb_k, int use_abs,
+                       uint32_t seed, uint64_t sample_id_offset, uint8_t* codes, float* a,
+                       float* cost);
 
 /* EncodeBase (src/quantizer/encoder_encode_base.inc:1-106, include/stlq/quantizer/encoder.h:
  * 66-74) without the ILS outer loop: xC GEMM, beam, [ICM], [LS refit + costs], all on the

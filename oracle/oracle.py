@@ -55,6 +55,9 @@ def lib():
         L.orc_icm.argtypes = [_f32p, _f32p, _f32p, _int, _int, _i32p, _f32p, _i64, _int, _int,
                               ctypes.c_uint32, _u8p, _f32p, _f32p, _int]
         L.orc_icm.restype = _i64
+        L.orc_icm_ils.argtypes = [_f32p, _f32p, _f32p, _int, _int, _i32p, _f32p, _i64, _int, _int, _int, _int,
+                                  ctypes.c_uint32, ctypes.c_uint64, _u8p, _f32p, _f32p, _int]
+        L.orc_icm_ils.restype = _i64
         L.orc_icm_orders.argtypes = [_int, _int, ctypes.c_uint32, _i32p]
         L.orc_mse_from_precomp.argtypes = [_f32p, _int, _f32p, _f32p, _int, _int, _i32p, _u8p, _f32p, _i64, _f64p, _int]
         L.orc_mse_fp64_refit.argtypes = [_f32p, _int, _f32p, _int, _int, _i32p, _u8p, _i64, _f64p, _int]
@@ -159,6 +162,25 @@ def icm(xC, G, invnorm, h_vec, nx2, codes, icm_iters, use_abs, seed, nthreads=0)
     fails = lib().orc_icm(_p(xC, _f32p), _p(G, _f32p), _p(inv, _f32p), H, m, _p(hv, _i32p), _p(nx2, _f32p), n,
                           icm_iters, int(bool(use_abs)), seed & 0xFFFFFFFF, _p(codes, _u8p), _p(a, _f32p),
                           _p(cost, _f32p), nthreads)
+    return codes, a, cost, int(fails)
+
+
+def icm_ils(xC, G, invnorm, h_vec, nx2, codes, icm_iters, ils_iters, perturb_k, use_abs, seed,
+            sample_id_offset=0, nthreads=0):
+    """ICM with the ILS outer loop; returns (codes, a, cost, ls_fails)."""
+    xC = _c(xC, np.float32)
+    G = _c(G, np.float32)
+    inv = _c(invnorm, np.float32)
+    hv = _c(h_vec, np.int32)
+    nx2 = _c(nx2, np.float32)
+    codes = np.array(codes, dtype=np.uint8, copy=True, order="C")
+    n, H = xC.shape
+    m = len(hv)
+    a = np.empty((n, m), np.float32)
+    cost = np.empty(n, np.float32)
+    fails = lib().orc_icm_ils(_p(xC, _f32p), _p(G, _f32p), _p(inv, _f32p), H, m, _p(hv, _i32p), _p(nx2, _f32p), n,
+                              icm_iters, ils_iters, perturb_k, int(bool(use_abs)), seed & 0xFFFFFFFF,
+                              int(sample_id_offset), _p(codes, _u8p), _p(a, _f32p), _p(cost, _f32p), nthreads)
     return codes, a, cost, int(fails)
 
 

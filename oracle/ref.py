@@ -65,8 +65,8 @@ def lib():
         L.ref_expand_large_root.argtypes = [_f32p, _int, _f32p, _int, _i32p, _int, _f32p, _int, _int, _f32p,
                                             _i32p, _f32p, _f32p, _u32p, _u8p]
         L.ref_solve_ls_all.argtypes = [_f32p, _f32p, _int, _i32p, _int, _u8p, _int, _f32p]
-        L.ref_icm.argtypes = [_f32p, _int, _int, _f32p, _f32p, _f32p, _int, _i32p, _int, _int, _int, ctypes.c_uint32,
-                              _u8p, _f32p, _f32p]
+        L.ref_icm.argtypes = [_f32p, _int, _int, _f32p, _f32p, _f32p, _int, _i32p, _int, _int, _int, _int, _int,
+                              ctypes.c_uint32, ctypes.c_uint64, _u8p, _f32p, _f32p]
         for f in (L.ref_xnorm2, L.ref_beam_search, L.ref_compute_costs, L.ref_expand_large_root, L.ref_solve_ls_all,
                   L.ref_icm):
             f.restype = None
@@ -131,8 +131,8 @@ def solve_ls_all(xC, G, h_vec, codes):
     return a
 
 
-def icm(X, xC, G, invnorm, h_vec, codes, icm_iters, use_abs, seed):
-    """stlq::DynamicIcmWithIls{Abs,NoAbs}NoNormal with ils_iters = 0; returns (codes, a, cost)."""
+def icm(X, xC, G, invnorm, h_vec, codes, icm_iters, use_abs, seed, ils_iters=0, perturb_k=3, sample_id_offset=0):
+    """stlq::DynamicIcmWithIls{Abs,NoAbs}NoNormal; returns (codes, a, cost)."""
     X = _c(X, np.float32)
     xC = _c(xC, np.float32)
     G = _c(G, np.float32)
@@ -145,7 +145,8 @@ def icm(X, xC, G, invnorm, h_vec, codes, icm_iters, use_abs, seed):
     a = np.empty((n, m), np.float32)
     cost = np.empty(n, np.float32)
     lib().ref_icm(_p(X, _f32p), d, n, _p(xC, _f32p), _p(G, _f32p), _p(inv, _f32p), H, _p(hv, _i32p), m, icm_iters,
-                  int(bool(use_abs)), seed & 0xFFFFFFFF, _p(codes, _u8p), _p(a, _f32p), _p(cost, _f32p))
+                  ils_iters, perturb_k, int(bool(use_abs)), seed & 0xFFFFFFFF, int(sample_id_offset),
+                  _p(codes, _u8p), _p(a, _f32p), _p(cost, _f32p))
     return codes, a, cost
 
 

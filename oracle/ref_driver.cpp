@@ -98,12 +98,12 @@ void ref_solve_ls_all(const float* xC, const float* G, int H, const int* h_vec, 
     std::memcpy(a, am.data.data(), sizeof(float) * am.data.size());
 }
 
-// stlq::DynamicIcmWithIls{Abs,NoAbs}NoNormal (icm.cpp:1132-1170) with ils_iters = 0: LS refit,
-// costs, then icm_iters RunIcm sweeps. codes (m x n) are updated in place. invnorm (H) is the
-// precomp's invnorm_flat.
+// stlq::DynamicIcmWithIls{Abs,NoAbs}NoNormal (icm.cpp:1132-1170): LS refit, costs, icm_iters
+// RunIcm sweeps, then ils_iters perturb + RunIcm + accept rounds. codes (m x n) are updated in
+// place. invnorm (H) is the precomp's invnorm_flat.
 void ref_icm(const float* X, int d, int n, const float* xC, const float* G, const float* invnorm, int H,
-             const int* h_vec, int m, int icm_iters, int use_abs, uint32_t seed, uint8_t* codes, float* a,
-             float* cost) {
+             const int* h_vec, int m, int icm_iters, int ils_iters, int perturb_k, int use_abs, uint32_t seed,
+             uint64_t sample_id_offset, uint8_t* codes, float* a, float* cost) {
     auto pre = MakePrecomp(G, H, h_vec, m, d);
     pre.invnorm_flat.assign(invnorm, invnorm + H);
     const auto Xm = Wrap(X, d, n);
@@ -112,9 +112,11 @@ void ref_icm(const float* X, int d, int n, const float* xC, const float* G, cons
     stlq::ColMajorMatrix<float> am;
     std::vector<float> xn2, cst;
     if (use_abs)
-        stlq::DynamicIcmWithIlsAbsNoNormal(Xm, pre, xCm, icm_iters, 0, 3, seed, &B, &am, &xn2, &cst, false, 0);
+        stlq::DynamicIcmWithIlsAbsNoNormal(Xm, pre, xCm, icm_iters, ils_iters, perturb_k, seed, &B, &am, &xn2, &cst,
+                                           false, sample_id_offset);
     else
-        stlq::DynamicIcmWithIlsNoAbsNoNormal(Xm, pre, xCm, icm_iters, 0, 3, seed, &B, &am, &xn2, &cst, false, 0);
+        stlq::DynamicIcmWithIlsNoAbsNoNormal(Xm, pre, xCm, icm_iters, ils_iters, perturb_k, seed, &B, &am, &xn2,
+                                             &cst, false, sample_id_offset);
     std::memcpy(codes, B.data.data(), B.data.size());
     std::memcpy(a, am.data.data(), sizeof(float) * am.data.size());
     std::memcpy(cost, cst.data(), sizeof(float) * cst.size());

@@ -596,16 +596,19 @@ void orc_icm_orders(int m, int icm_iters, uint32_t seed, int* order_out) {
     }
 }
 
-int64_t orc_icm(const float* xC, const float* G, const float* invnorm, int H, int m,
-                const int* h_vec, const float* nx2, int64_t n, int icm_iters, int use_abs,
-                uint32_t seed, uint8_t* codes, float* a, float* cost, int nthreads) {
-    SetThreads(nthreads);
+}  // extern "C"
+
+namespace {
+
+// RunIcm (icm.cpp:89-344) on codes/a/cost in place, with the layer order of each sweep given:
+// LS refit and costs of the incoming codes, then icm_iters sweeps over the active vectors.
+int64_t RunIcmOrders(const float* xC, const float* G, const float* invnorm, int H, int m, const int* h_vec,
+                     const float* nx2, int64_t n, int icm_iters, int use_abs, const int* orders, uint8_t* codes,
+                     float* a, float* cost, int nthreads) {
     const std::vector<int> off = Offsets(m, h_vec);
     // icm.cpp:109-114: LS refit and costs of the incoming codes.
     int64_t ls_fail = orc_solve_ls_all(xC, G, H, m, h_vec, codes, n, a, nthreads);
     orc_compute_costs(xC, G, H, m, h_vec, codes, a, nx2, n, cost, nthreads);
-    std::vector<int> orders(static_cast<std::size_t>(m) * std::max(0, icm_iters));
-    orc_icm_orders(m, icm_iters, seed, orders.data());
     std::vector<u8> active(static_cast<std::size_t>(n), 1), changed(static_cast<std::size_t>(n), 0);
     int max_h = 0;
     for (int l = 0; l < m; ++l) max_h = std::max(max_h, h_vec[l]);
@@ -671,6 +674,95 @@ int64_t orc_icm(const float* xC, const float* G, const float* invnorm, int H, in
         }
     }
     return ls_fail;
+}
+
+// icm.cpp:136-137 with the order reset of :121-123: each RunIcm starts from the identity order
+// and shuffles it once per sweep with the caller's std::mt19937 stream.
+std::vector<int> NextOrders(std::mt19937& rng, int m, int icm_iters) {
+    std::vector<int> order(static_cast<std::size_t>(m)), out;
+    std::iota(order.begin(), order.end(), 0);
+    for (int it = 0; it < icm_iters; ++it) {
+        std::shuffle(order.begin(), order.end(), rng);
+        out.insert(out.end(), order.begin(), order.end());
+    }
+    return out;
+}
+
+// SplitMix64 and UniformBelow (icm.cpp:55-87): the ILS perturbation stream.
+struct SplitMix64 {
+    uint64_t state;
+    uint64_t Next() {
+        uint64_t z = (state += 0x9e3779b97f4a7c15ULL);
+        z = (z ^ (z >> 30U)) * 0xbf58476d1ce4e5b9ULL;
+        z = (z ^ (z >> 27U)) * 0x94d049bb133111ebULL;
+        return z ^ (z >> 31U);
+    }
+};
+inline uint32_t UniformBelow(SplitMix64& r, uint32_t bound) {
+    return static_cast<uint32_t>((static_cast<unsigned __int128>(r.Next()) * bound) >> 64);
+}
+
+}  // namespace
+
+extern "C" {
+
+int64_t orc_icm(const float* xC, const float* G, const float* invnorm, int H, int m,
+                const int* h_vec, const float* nx2, int64_t n, int icm_iters, int use_abs,
+                uint32_t seed, uint8_t* codes, float* a, float* cost, int nthreads) {
+    SetThreads(nthreads);
+    std::vector<int> orders(static_cast<std::size_t>(m) * std::max(0, icm_iters));
+    orc_icm_orders(m, icm_iters, seed, orders.data());
+    return RunIcmOrders(xC, G, invnorm, H, m, h_vec, nx2, n, icm_iters, use_abs, orders.data(), codes, a, cost,
+                        nthreads);
+}
+
+int64_t orc_icm_ils(const float* xC, const float* G, const float* invnorm, int H, int m, const int* h_vec,
+                    const float* nx2, int64_t n, int icm_iters, int ils_iters, int perturb_k, int use_abs,
+                    uint32_t seed, uint64_t sample_id_offset, uint8_t* codes, float* a, float* cost,
+                    int nthreads) {
+    SetThreads(nthreads);
+    // DynamicIcmWithIlsImpl (icm.cpp:872-1003)
+    std::mt19937 rng(static_cast<std::mt19937::result_type>(seed));
+    std::vector<int> ord = NextOrders(rng, m, std::max(0, icm_iters));
+    int64_t fails = RunIcmOrders(xC, G, invnorm, H, m, h_vec, nx2, n, icm_iters, use_abs, ord.data(), codes, a,
+                                 cost, nthreads);
+    if (ils_iters <= 0 || perturb_k <= 0 || m <= 1) return fails;
+    const int ksel = std::min(perturb_k, m);
+    const int layer_span = m - 1;
+    std::vector<uint8_t> Bc(static_cast<std::size_t>(n) * m);
+    std::vector<float> ac(static_cast<std::size_t>(n) * m), cc(static_cast<std::size_t>(n));
+    for (int outer = 0; outer < ils_iters; ++outer) {
+        std::memcpy(Bc.data(), codes, Bc.size());
+        #pragma omp parallel for schedule(static)
+        for (int64_t i = 0; i < n; ++i) {
+            const uint64_t ig = sample_id_offset + static_cast<uint64_t>(i);
+            SplitMix64 r{static_cast<uint64_t>(seed) ^ (static_cast<uint64_t>(outer + 1) * 0x9e3779b97f4a7c15ULL) ^
+                         ((ig + 1) * 0xbf58476d1ce4e5b9ULL)};
+            uint8_t* ci = Bc.data() + static_cast<std::size_t>(i) * m;
+            for (int k = 0; k < ksel; ++k) {
+                const int layer = 1 + static_cast<int>(UniformBelow(r, static_cast<uint32_t>(layer_span)));
+                const int h = h_vec[layer];
+                if (h <= 1) continue;
+                const int old = ci[layer];
+                const int raw = static_cast<int>(UniformBelow(r, static_cast<uint32_t>(h - 1)));
+                ci[layer] = static_cast<uint8_t>(raw >= old ? raw + 1 : raw);
+            }
+        }
+        ord = NextOrders(rng, m, std::max(0, icm_iters));
+        fails += RunIcmOrders(xC, G, invnorm, H, m, h_vec, nx2, n, icm_iters, use_abs, ord.data(), Bc.data(),
+                              ac.data(), cc.data(), nthreads);
+        // accept if better (icm.cpp:977-987)
+        #pragma omp parallel for schedule(static)
+        for (int64_t i = 0; i < n; ++i) {
+            if (cc[i] + kEps < cost[i]) {
+                std::memcpy(codes + static_cast<std::size_t>(i) * m, Bc.data() + static_cast<std::size_t>(i) * m, m);
+                std::memcpy(a + static_cast<std::size_t>(i) * m, ac.data() + static_cast<std::size_t>(i) * m,
+                            sizeof(float) * m);
+                cost[i] = cc[i];
+            }
+        }
+    }
+    return fails;
 }
 
 void orc_mse_from_precomp(const float* X, int d, const float* xC, const float* G, int H, int m,

@@ -58,6 +58,15 @@ int64_t orc_icm(const float* xC, const float* G, const float* invnorm, int H, in
                 const int* h_vec, const float* nx2, int64_t n, int icm_iters, int use_abs,
                 uint32_t seed, uint8_t* codes, float* a, float* cost, int nthreads);
 
+/* DynamicIcmWithIls{Abs,NoAbs}NoNormal (icm.cpp:872-1003) with ILS: RunIcm, then ils_iters rounds
+ * of a SplitMix64 perturbation of min(perturb_k, m) codes in layers 1..m-1 (keyed by seed, round
+ * and sample_id_offset + i), RunIcm on the perturbed codes, and accept-if-better
+ * (cand + 1e-6 < cost). One std::mt19937(seed) stream supplies every RunIcm's layer orders. */
+int64_t orc_icm_ils(const float* xC, const float* G, const float* invnorm, int H, int m, const int* h_vec,
+                    const float* nx2, int64_t n, int icm_iters, int ils_iters, int perturb_k, int use_abs,
+                    uint32_t seed, uint64_t sample_id_offset, uint8_t* codes, float* a, float* cost,
+                    int nthreads);
+
 /* The layer order RunIcm uses on iteration `it` (std::shuffle with std::mt19937(seed),
  * icm.cpp:137/242/890). order_out has m * icm_iters entries. */
 void orc_icm_orders(int m, int icm_iters, uint32_t seed, int* order_out);

@@ -101,6 +101,8 @@ SIGNATURES = {
     "stlq_mi355_solve_ls_all": ([_vp, _f32p, _u8p, _i64, _f32p, _i64p], _int),
     "stlq_mi355_compute_costs": ([_vp, _f32p, _u8p, _f32p, _f32p, _i64, _f32p], _int),
     "stlq_mi355_icm": ([_vp, _f32p, _f32p, _f32p, _i64, _int, _int, ctypes.c_uint32, _u8p, _f32p, _f32p], _int),
+    "stlq_mi355_icm_ils": ([_vp, _f32p, _f32p, _f32p, _i64, _int, _int, _int, _int, ctypes.c_uint32, ctypes.c_uint64,
+                            _u8p, _f32p, _f32p], _int),
     "stlq_mi355_encode": ([_vp, _f32p, _i64, ctypes.POINTER(EncodeParams), _u8p, _f32p, _f32p, _f64p, _f64p], _int),
     "stlq_mi355_encode_device": ([_vp, _vp, _i64, ctypes.POINTER(EncodeParams), _vp, _vp, _vp, _vp], _int),
     "stlq_mi355_encode_stream": ([_vp, _i64, _i64, ctypes.POINTER(StreamParams), FILL_FN, SINK_FN, _vp,

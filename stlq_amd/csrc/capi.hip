@@ -105,6 +105,7 @@ struct stlq_mi355_ctx {
 
     // Work buffers (grown on demand, reused across calls).
     DevBuf X, nx2, xC, xC_in, codes, a, cost, best, fails, active, changed, mse, gam0, roots, scores;
+    DevBuf ils_codes, ils_a, ils_cost;  // ILS candidate state
     DevBuf st_rec[2], st_curH[2];
 
     std::vector<TileEvents> tiles;
@@ -269,8 +270,10 @@ std::vector<int> IcmOrders(int m, int iters, uint32_t seed) {
 }
 
 // RunIcm (icm.cpp:89-344) on one tile: LS refit + costs, then icm_iters sweeps.
-int RunIcm(stlq_mi355_ctx* c, const float* dxC, int64_t ldx, const float* dnx2, int64_t n, int iters,
-           int use_abs, uint32_t seed, uint8_t* dcodes, float* da, float* dcost, hipStream_t s) {
+// RunIcm (icm.cpp:89-344) with the layer order of every sweep given (iters x m).
+int RunIcmOrders(stlq_mi355_ctx* c, const float* dxC, int64_t ldx, const float* dnx2, int64_t n, int iters,
+                 int use_abs, const std::vector<int>& orders, uint8_t* dcodes, float* da, float* dcost,
+                 hipStream_t s) {
     LsArgs ls = MakeLs(c, dxC, ldx, dcodes, da, dnx2, dcost, n);
     HIP_TRY(LaunchLsAll(ls, s));
     HIP_TRY(LaunchCosts(ls, s));
@@ -278,7 +281,6 @@ int RunIcm(stlq_mi355_ctx* c, const float* dxC, int64_t ldx, const float* dnx2, 
     HIP_TRY(c->active.Ensure(static_cast<size_t>(n)));
     HIP_TRY(c->changed.Ensure(static_cast<size_t>(n)));
     HIP_TRY(LaunchFill8(c->active.as<uint8_t>(), 1, n, s));
-    const std::vector<int> orders = IcmOrders(c->m, iters, seed);
     IcmArgs q;
     q.ls = ls;
     q.codes_rw = dcodes;
@@ -303,6 +305,48 @@ int RunIcm(stlq_mi355_ctx* c, const float* dxC, int64_t ldx, const float* dnx2, 
     return STLQ_MI355_OK;
 }
 
+int RunIcm(stlq_mi355_ctx* c, const float* dxC, int64_t ldx, const float* dnx2, int64_t n, int iters,
+           int use_abs, uint32_t seed, uint8_t* dcodes, float* da, float* dcost, hipStream_t s) {
+    return RunIcmOrders(c, dxC, ldx, dnx2, n, iters, use_abs, IcmOrders(c->m, iters, seed), dcodes, da, dcost, s);
+}
+
+// DynamicIcmWithIls{Abs,NoAbs}NoNormal (icm.cpp:872-1003): RunIcm, then ils_iters rounds of
+// perturb (PerturbKernel) -> RunIcm on the candidate codes -> accept-if-better. One
+// std::mt19937(seed) stream supplies every RunIcm's layer orders, each RunIcm starting from the
+// identity order (icm.cpp:121-137). id0 is the global id of vector 0 (the reference's
+// sample_id_offset), so a tile of a larger set perturbs exactly as the whole set would.
+int RunIcmIls(stlq_mi355_ctx* c, const float* dxC, int64_t ldx, const float* dnx2, int64_t n, int icm_iters,
+              int ils_iters, int perturb_k, int use_abs, uint32_t seed, uint64_t id0, uint8_t* dcodes, float* da,
+              float* dcost, hipStream_t s) {
+    std::mt19937 rng(static_cast<std::mt19937::result_type>(seed));
+    const int m = c->m;
+    auto next_orders = [&]() {
+        std::vector<int> order(static_cast<size_t>(m)), out;
+        std::iota(order.begin(), order.end(), 0);
+        for (int it = 0; it < icm_iters; ++it) {
+            std::shuffle(order.begin(), order.end(), rng);
+            out.insert(out.end(), order.begin(), order.end());
+        }
+        return out;
+    };
+    RC_TRY(RunIcmOrders(c, dxC, ldx, dnx2, n, icm_iters, use_abs, next_orders(), dcodes, da, dcost, s));
+    if (ils_iters <= 0 || perturb_k <= 0 || m <= 1) return STLQ_MI355_OK;
+    const size_t nm = static_cast<size_t>(n) * static_cast<size_t>(m);
+    HIP_TRY(c->ils_codes.Ensure(nm));
+    HIP_TRY(c->ils_a.Ensure(nm * 4));
+    HIP_TRY(c->ils_cost.Ensure(static_cast<size_t>(n) * 4));
+    uint8_t* cc = c->ils_codes.as<uint8_t>();
+    float* ca = c->ils_a.as<float>();
+    float* ccost = c->ils_cost.as<float>();
+    for (int outer = 0; outer < ils_iters; ++outer) {
+        HIP_TRY(hipMemcpyAsync(cc, dcodes, nm, hipMemcpyDeviceToDevice, s));
+        HIP_TRY(LaunchPerturb(cc, n, m, c->h_vec, perturb_k, seed, outer, id0, s));
+        RC_TRY(RunIcmOrders(c, dxC, ldx, dnx2, n, icm_iters, use_abs, next_orders(), cc, ca, ccost, s));
+        HIP_TRY(LaunchIlsAccept(dcodes, da, dcost, cc, ca, ccost, n, m, s));
+    }
+    return STLQ_MI355_OK;
+}
+
 struct EncodeOut {
     uint8_t* codes;  // device [n*m]
     float* a;        // device [n*m] or null
@@ -313,7 +357,7 @@ struct EncodeOut {
 // One tile of EncodeBase on device-resident X.
 // Beam, LS refit + costs and ICM of one tile whose ||x||^2 and xC are already on the device.
 int BeamAndRefit(stlq_mi355_ctx* c, const float* dxC, const float* dnx2, int64_t n, const stlq_mi355_encode_params& P,
-                 const EncodeOut& o, hipStream_t s, TileEvents* te) {
+                 const EncodeOut& o, hipStream_t s, TileEvents* te, uint64_t id0) {
     const int Hb = std::max(1, P.H_beam);
     auto rec = [&](int k) -> hipError_t {
         if (!te) return hipSuccess;
@@ -322,7 +366,8 @@ int BeamAndRefit(stlq_mi355_ctx* c, const float* dxC, const float* dnx2, int64_t
     };
     RC_TRY(RunBeam(c, dxC, c->H, dnx2, n, Hb, o.codes, o.best, s, te ? &te->beam_launches : nullptr, te));
     HIP_TRY(rec(3));
-    const bool need_ls = P.want_coeffs || P.icm_iters > 0;
+    const bool refine = P.icm_iters > 0 || P.ils_iters > 0;
+    const bool need_ls = P.want_coeffs || refine;
     float* da = o.a;
     float* dcost = o.cost;
     if (need_ls) {
@@ -339,8 +384,9 @@ int BeamAndRefit(stlq_mi355_ctx* c, const float* dxC, const float* dnx2, int64_t
         HIP_TRY(LaunchCosts(ls, s));
     }
     HIP_TRY(rec(4));
-    if (P.icm_iters > 0) {
-        RC_TRY(RunIcm(c, dxC, c->H, dnx2, n, P.icm_iters, P.use_abs, P.seed, o.codes, da, dcost, s));
+    if (refine) {
+        RC_TRY(RunIcmIls(c, dxC, c->H, dnx2, n, P.icm_iters, P.ils_iters, P.perturb_k, P.use_abs, P.seed, id0,
+                         o.codes, da, dcost, s));
     }
     HIP_TRY(rec(5));
     HIP_TRY(rec(6));
@@ -361,7 +407,7 @@ int64_t PipeSub() {
 }
 
 int EncodeTilePipelined(stlq_mi355_ctx* c, const float* dX, int64_t n, const stlq_mi355_encode_params& P,
-                        const EncodeOut& o, hipStream_t s, bool record) {
+                        const EncodeOut& o, hipStream_t s, bool record, uint64_t id0) {
     const int64_t sub = PipeSub();
     const int64_t nsub = (n + sub - 1) / sub;
     const size_t H = static_cast<size_t>(c->H), m = static_cast<size_t>(c->m);
@@ -406,7 +452,7 @@ int EncodeTilePipelined(stlq_mi355_ctx* c, const float* dX, int64_t n, const stl
         te.e[2] = ev(s);
         EncodeOut oi{o.codes + off * m, o.a ? o.a + off * m : nullptr, o.cost ? o.cost + off : nullptr,
                      o.best ? o.best + off : nullptr};
-        RC_TRY(BeamAndRefit(c, xcb[b], nxb[b], ni, P, oi, s, &te));
+        RC_TRY(BeamAndRefit(c, xcb[b], nxb[b], ni, P, oi, s, &te, id0 + static_cast<uint64_t>(off)));
         tile_done[static_cast<size_t>(i)] = te.e[6];
         if (!te.e[6]) return Fail(STLQ_MI355_ERR_HIP, "event creation failed");
     }
@@ -418,11 +464,12 @@ int EncodeTilePipelined(stlq_mi355_ctx* c, const float* dX, int64_t n, const stl
 }
 
 // allow_overlap = false keeps the whole tile's xC and ||x||^2 in c->xC / c->nx2 afterwards.
+// allow_overlap = false keeps the whole tile's xC and ||x||^2 in c->xC / c->nx2 afterwards.
+// id0: global id of the tile's first vector (ILS perturbation stream).
 int EncodeTile(stlq_mi355_ctx* c, const float* dX, int64_t n, const stlq_mi355_encode_params& P,
-               const EncodeOut& o, hipStream_t s, bool record, bool allow_overlap = true) {
+               const EncodeOut& o, hipStream_t s, bool record, bool allow_overlap = true, uint64_t id0 = 0) {
     const int64_t pipe = PipeSub();
-    if (allow_overlap && pipe > 0 && n >= 2 * pipe) return EncodeTilePipelined(c, dX, n, P, o, s, record);
-    const int Hb = std::max(1, P.H_beam);
+    if (allow_overlap && pipe > 0 && n >= 2 * pipe) return EncodeTilePipelined(c, dX, n, P, o, s, record, id0);
     HIP_TRY(c->nx2.Ensure(static_cast<size_t>(n) * 4));
     HIP_TRY(c->xC.Ensure(static_cast<size_t>(n) * c->H * 4));
     TileEvents te;
@@ -438,40 +485,15 @@ int EncodeTile(stlq_mi355_ctx* c, const float* dX, int64_t n, const stlq_mi355_e
     HIP_TRY(LaunchGemmXc(dX, n, c->d, c->C_all.as<float>(), c->H, c->xC.as<float>(), c->H, s));
     te.gemm_launches = 1;
     HIP_TRY(rec(2));
-    RC_TRY(RunBeam(c, c->xC.as<float>(), c->H, c->nx2.as<float>(), n, Hb, o.codes, o.best, s, &te.beam_launches,
-                   record ? &te : nullptr));
-    HIP_TRY(rec(3));
-    const bool need_ls = P.want_coeffs || P.icm_iters > 0;
-    float* da = o.a;
-    float* dcost = o.cost;
-    if (need_ls) {
-        if (!da) {
-            HIP_TRY(c->a.Ensure(static_cast<size_t>(n) * c->m * 4));
-            da = c->a.as<float>();
-        }
-        if (!dcost) {
-            HIP_TRY(c->cost.Ensure(static_cast<size_t>(n) * 4));
-            dcost = c->cost.as<float>();
-        }
-        LsArgs ls = MakeLs(c, c->xC.as<float>(), c->H, o.codes, da, c->nx2.as<float>(), dcost, n);
-        HIP_TRY(LaunchLsAll(ls, s));
-        HIP_TRY(LaunchCosts(ls, s));
-    }
-    HIP_TRY(rec(4));
-    if (P.icm_iters > 0) {
-        RC_TRY(RunIcm(c, c->xC.as<float>(), c->H, c->nx2.as<float>(), n, P.icm_iters, P.use_abs, P.seed, o.codes,
-                      da, dcost, s));
-    }
-    HIP_TRY(rec(5));
-    HIP_TRY(rec(6));
+    RC_TRY(BeamAndRefit(c, c->xC.as<float>(), c->nx2.as<float>(), n, P, o, s, record ? &te : nullptr, id0));
     if (record) c->tiles.push_back(te);
     return STLQ_MI355_OK;
 }
 
 int CheckParams(const stlq_mi355_encode_params* p) {
     if (!p) return Fail(STLQ_MI355_ERR_INVALID, "params is null");
-    if (p->ils_iters != 0) return Fail(STLQ_MI355_ERR_UNSUPPORTED, "ils_iters must be 0 (ILS is not part of this build)");
-    if (p->icm_iters < 0) return Fail(STLQ_MI355_ERR_INVALID, "icm_iters must be >= 0");
+    if (p->icm_iters < 0 || p->ils_iters < 0 || p->perturb_k < 0)
+        return Fail(STLQ_MI355_ERR_INVALID, "icm_iters, ils_iters and perturb_k must be >= 0");
     return CheckBeam(std::max(1, p->H_beam));
 }
 
@@ -522,7 +544,7 @@ int stlq_mi355_ctx_destroy(stlq_mi355_ctx* c) {
     DevBuf* bufs[] = {&c->C_all, &c->G_rm, &c->G_cm, &c->gdiag, &c->invnorm, &c->C0, &c->Cs, &c->norm0,
                       &c->G_small, &c->G0S, &c->gdiag_small, &c->X, &c->nx2, &c->xC, &c->xC_in, &c->codes, &c->a,
                       &c->cost, &c->best, &c->fails, &c->active, &c->changed, &c->mse, &c->gam0, &c->roots,
-                      &c->scores};
+                      &c->scores, &c->ils_codes, &c->ils_a, &c->ils_cost};
     if (c->g_shared) c->G_cm.p = nullptr;
     for (DevBuf* b : bufs) b->Release();
     for (int b = 0; b < 2; ++b) {
@@ -775,6 +797,50 @@ int stlq_mi355_icm(stlq_mi355_ctx* c, const float* X, const float* nx2, const fl
     return STLQ_MI355_OK;
 }
 
+int stlq_mi355_icm_ils(stlq_mi355_ctx* c, const float* X, const float* nx2, const float* xC, int64_t n,
+                       int icm_iters, int ils_iters, int perturb_k, int use_abs, uint32_t seed,
+                       uint64_t sample_id_offset, uint8_t* codes, float* a, float* cost) {
+    RC_TRY(CheckPre(c));
+    if (n < 0 || (n > 0 && (!xC || !codes || !a || !cost || (!X && !nx2))))
+        return Fail(STLQ_MI355_ERR_INVALID, "bad arguments");
+    if (icm_iters < 0 || ils_iters < 0 || perturb_k < 0)
+        return Fail(STLQ_MI355_ERR_INVALID, "icm_iters, ils_iters and perturb_k must be >= 0");
+    if (n == 0) return STLQ_MI355_OK;
+    RC_TRY(CheckCodes(c, codes, n));
+    c->ResetTimings();
+    const size_t m = static_cast<size_t>(c->m);
+    HIP_TRY(c->xC.Ensure(static_cast<size_t>(n) * c->H * 4));
+    HIP_TRY(c->codes.Ensure(static_cast<size_t>(n) * m));
+    HIP_TRY(c->a.Ensure(static_cast<size_t>(n) * m * 4));
+    HIP_TRY(c->nx2.Ensure(static_cast<size_t>(n) * 4));
+    HIP_TRY(c->cost.Ensure(static_cast<size_t>(n) * 4));
+    HIP_TRY(hipMemcpyAsync(c->xC.p, xC, static_cast<size_t>(n) * c->H * 4, hipMemcpyHostToDevice, c->stream));
+    HIP_TRY(hipMemcpyAsync(c->codes.p, codes, static_cast<size_t>(n) * m, hipMemcpyHostToDevice, c->stream));
+    if (nx2) {
+        HIP_TRY(hipMemcpyAsync(c->nx2.p, nx2, static_cast<size_t>(n) * 4, hipMemcpyHostToDevice, c->stream));
+    } else {
+        HIP_TRY(c->X.Ensure(static_cast<size_t>(n) * c->d * 4));
+        HIP_TRY(hipMemcpyAsync(c->X.p, X, static_cast<size_t>(n) * c->d * 4, hipMemcpyHostToDevice, c->stream));
+        HIP_TRY(LaunchXNorm2(c->X.as<float>(), c->d, n, c->nx2.as<float>(), c->stream));
+    }
+    HIP_TRY(LaunchFill8(c->fails.as<uint8_t>(), 0, 4, c->stream));  // a kernel, not a memset node, if captured
+    TileEvents te;
+    te.n = n;
+    te.e[0] = te.e[1] = te.e[2] = te.e[3] = te.e[4] = c->NextEvent();
+    HIP_TRY(hipEventRecord(te.e[0], c->stream));
+    RC_TRY(RunIcmIls(c, c->xC.as<float>(), c->H, c->nx2.as<float>(), n, icm_iters, ils_iters, perturb_k, use_abs,
+                     seed, sample_id_offset, c->codes.as<uint8_t>(), c->a.as<float>(), c->cost.as<float>(),
+                     c->stream));
+    te.e[5] = te.e[6] = c->NextEvent();
+    HIP_TRY(hipEventRecord(te.e[5], c->stream));
+    c->tiles.push_back(te);
+    HIP_TRY(hipMemcpyAsync(codes, c->codes.p, static_cast<size_t>(n) * m, hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(hipMemcpyAsync(a, c->a.p, static_cast<size_t>(n) * m * 4, hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(hipMemcpyAsync(cost, c->cost.p, static_cast<size_t>(n) * 4, hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    return STLQ_MI355_OK;
+}
+
 int stlq_mi355_encode(stlq_mi355_ctx* c, const float* X, int64_t n, const stlq_mi355_encode_params* params,
                       uint8_t* codes, float* a, float* cost, double* beam_mse, double* final_mse) {
     RC_TRY(CheckPre(c));
@@ -784,7 +850,7 @@ int stlq_mi355_encode(stlq_mi355_ctx* c, const float* X, int64_t n, const stlq_m
     c->ResetTimings();
     stlq_mi355_encode_params P = *params;
     const bool want_mse = beam_mse || final_mse;
-    const bool need_ls = P.want_coeffs || P.icm_iters > 0 || want_mse;
+    const bool need_ls = P.want_coeffs || P.icm_iters > 0 || P.ils_iters > 0 || want_mse;
     const int Hb = std::max(1, P.H_beam);
     const size_t m = static_cast<size_t>(c->m);
     const int64_t tile = TileVectors(n, c->d, c->m, c->H, Hb);
@@ -802,19 +868,22 @@ int stlq_mi355_encode(stlq_mi355_ctx* c, const float* X, int64_t n, const stlq_m
         EncodeOut o{c->codes.as<uint8_t>(), c->a.as<float>(), c->cost.as<float>(), nullptr};
         stlq_mi355_encode_params Pt = P;
         Pt.want_coeffs = need_ls ? 1 : 0;
-        if (want_mse && P.icm_iters > 0) {
-            // Beam MSE before ICM: run the beam + LS alone first, then ICM on the same codes.
+        if (want_mse && (P.icm_iters > 0 || P.ils_iters > 0)) {
+            // Beam MSE before ICM/ILS: run the beam + LS alone first, then ICM/ILS on the same codes.
             Pt.icm_iters = 0;
-            RC_TRY(EncodeTile(c, c->X.as<float>(), nt, Pt, o, c->stream, true, /*allow_overlap=*/false));
+            Pt.ils_iters = 0;
+            RC_TRY(EncodeTile(c, c->X.as<float>(), nt, Pt, o, c->stream, true, /*allow_overlap=*/false,
+                              static_cast<uint64_t>(t0)));
             beam_cost.resize(static_cast<size_t>(nt));
             HIP_TRY(hipMemcpyAsync(beam_cost.data(), c->cost.p, static_cast<size_t>(nt) * 4, hipMemcpyDeviceToHost,
                                    c->stream));
             HIP_TRY(hipStreamSynchronize(c->stream));
             beam_sum += Mean(beam_cost) * static_cast<double>(nt);
-            RC_TRY(RunIcm(c, c->xC.as<float>(), c->H, c->nx2.as<float>(), nt, P.icm_iters, P.use_abs, P.seed,
-                          o.codes, o.a, o.cost, c->stream));
+            RC_TRY(RunIcmIls(c, c->xC.as<float>(), c->H, c->nx2.as<float>(), nt, P.icm_iters, P.ils_iters,
+                             P.perturb_k, P.use_abs, P.seed, static_cast<uint64_t>(t0), o.codes, o.a, o.cost,
+                             c->stream));
         } else {
-            RC_TRY(EncodeTile(c, c->X.as<float>(), nt, Pt, o, c->stream, true));
+            RC_TRY(EncodeTile(c, c->X.as<float>(), nt, Pt, o, c->stream, true, true, static_cast<uint64_t>(t0)));
         }
         HIP_TRY(hipMemcpyAsync(codes + t0 * m, c->codes.p, static_cast<size_t>(nt) * m, hipMemcpyDeviceToHost,
                                c->stream));
@@ -853,7 +922,7 @@ int stlq_mi355_encode_device(stlq_mi355_ctx* c, const float* dX, int64_t n, cons
     for (int64_t t0 = 0; t0 < n; t0 += tile) {
         const int64_t nt = std::min(tile, n - t0);
         EncodeOut o{dcodes + t0 * m, da ? da + t0 * m : nullptr, dcost ? dcost + t0 : nullptr, nullptr};
-        RC_TRY(EncodeTile(c, dX + t0 * c->d, nt, *params, o, s, true));
+        RC_TRY(EncodeTile(c, dX + t0 * c->d, nt, *params, o, s, true, true, static_cast<uint64_t>(t0)));
     }
     return STLQ_MI355_OK;
 }
@@ -933,7 +1002,7 @@ int stlq_mi355_encode_stream(stlq_mi355_ctx* c, int64_t n_total, int64_t chunk, 
     const size_t esz = sp->input_u8 ? 1 : 4;
     chunk = std::min(chunk, n_total);
     const size_t ch = static_cast<size_t>(chunk);
-    const bool want = !lr && (sp->encode.want_coeffs || sp->encode.icm_iters > 0);
+    const bool want = !lr && (sp->encode.want_coeffs || sp->encode.icm_iters > 0 || sp->encode.ils_iters > 0);
     const size_t code_b = lr ? std::max<size_t>(m - 1, 1) : m;
     struct Slot {
         void* hin = nullptr;
@@ -1054,7 +1123,8 @@ int stlq_mi355_encode_stream(stlq_mi355_ctx* c, int64_t n_total, int64_t chunk, 
             } else {
                 EncodeOut o{sl.dcodes.as<uint8_t>() + t0 * m, want ? sl.da.as<float>() + t0 * m : nullptr,
                             want ? sl.dcost.as<float>() + t0 : nullptr, nullptr};
-                rc = EncodeTile(c, dX + t0 * d, nt, sp->encode, o, c->stream, true);
+                rc = EncodeTile(c, dX + t0 * d, nt, sp->encode, o, c->stream, true, true,
+                                static_cast<uint64_t>(sl.first + t0));
             }
         }
         if (rc != STLQ_MI355_OK) break;

@@ -117,6 +117,10 @@ struct IcmArgs {
 };
 hipError_t LaunchIcmLayer(const IcmArgs& a, hipStream_t s);
 hipError_t LaunchIcmDeactivate(uint8_t* active, const uint8_t* changed, int64_t n, hipStream_t s);
+hipError_t LaunchPerturb(uint8_t* codes, int64_t n, int m, const int* h_vec, int perturb_k, uint32_t seed, int outer,
+                         uint64_t id0, hipStream_t s);
+hipError_t LaunchIlsAccept(uint8_t* codes, float* a, float* cost, const uint8_t* cc, const float* ca, const float* ccost,
+                           int64_t n, int m, hipStream_t s);
 hipError_t LaunchFill8(uint8_t* p, uint8_t v, int64_t n, hipStream_t s);
 hipError_t LaunchCopy16(void* dst, const void* src, size_t n16, hipStream_t s);
 hipError_t LaunchU8ToF32(const uint8_t* in, float* out, size_t count, hipStream_t s);

@@ -238,6 +238,62 @@ __global__ void DeactivateKernel(uint8_t* active, const uint8_t* changed, int64_
     if (i < n && active[i] && !changed[i]) active[i] = 0;
 }
 
+// ILS perturbation (icm.cpp:946-972): per vector a SplitMix64 stream keyed by the seed, the round
+// and the global sample id picks min(perturb_k, m) (layer, new code) pairs in layers 1..m-1,
+// each new code uniform over the layer's codes other than the current one (Lemire multiply-high).
+struct PerturbArgs {
+    uint8_t* codes;  // [n*m], perturbed in place
+    int64_t n;
+    int m, ksel;
+    int h_vec[kMaxM];
+    uint32_t seed;
+    int outer;
+    uint64_t id0;  // global id of vector 0
+};
+
+__device__ __forceinline__ uint64_t SplitMixNext(uint64_t& st) {
+    uint64_t z = (st += 0x9e3779b97f4a7c15ULL);
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ULL;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebULL;
+    return z ^ (z >> 31);
+}
+__device__ __forceinline__ uint32_t UniformBelow(uint64_t& st, uint32_t bound) {
+    return static_cast<uint32_t>(__umul64hi(SplitMixNext(st), static_cast<uint64_t>(bound)));
+}
+
+__global__ __launch_bounds__(256) void PerturbKernel(PerturbArgs p) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= p.n) return;
+    const uint64_t ig = p.id0 + static_cast<uint64_t>(i);
+    uint64_t st = static_cast<uint64_t>(p.seed) ^ (static_cast<uint64_t>(p.outer + 1) * 0x9e3779b97f4a7c15ULL) ^
+                  ((ig + 1ULL) * 0xbf58476d1ce4e5b9ULL);
+    uint8_t* ci = p.codes + i * p.m;
+    const uint32_t span = static_cast<uint32_t>(p.m - 1);
+    for (int r = 0; r < p.ksel; ++r) {
+        const int layer = 1 + static_cast<int>(UniformBelow(st, span));
+        const int h = p.h_vec[layer];
+        if (h <= 1) continue;
+        const int old = ci[layer];
+        const int raw = static_cast<int>(UniformBelow(st, static_cast<uint32_t>(h - 1)));
+        ci[layer] = static_cast<uint8_t>(raw >= old ? raw + 1 : raw);
+    }
+}
+
+// Accept-if-better of one ILS round (icm.cpp:977-987): the candidate replaces the vector's codes,
+// coefficients and cost when cand + 1e-6 < cost.
+__global__ __launch_bounds__(256) void IlsAcceptKernel(uint8_t* codes, float* a, float* cost, const uint8_t* cc,
+                                                      const float* ca, const float* ccost, int64_t n, int m) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    if (ccost[i] + kEps < cost[i]) {
+        for (int l = 0; l < m; ++l) {
+            codes[i * m + l] = cc[i * m + l];
+            a[i * m + l] = ca[i * m + l];
+        }
+        cost[i] = ccost[i];
+    }
+}
+
 #define STLQ_LAUNCH_M(KER, M_, grid, block, s, a) \
     hipLaunchKernelGGL((KER<M_>), grid, block, 0, s, a)
 
@@ -286,6 +342,30 @@ hipError_t LaunchIcmLayer(const IcmArgs& a, hipStream_t s) {
     if (a.ls.n <= 0) return hipSuccess;
     const dim3 grid(static_cast<unsigned>((a.ls.n + 3) / 4)), block(256);
     STLQ_SWITCH_M(IcmLayerKernel, a.ls.m, grid, block, s, a);
+    return hipGetLastError();
+}
+
+hipError_t LaunchPerturb(uint8_t* codes, int64_t n, int m, const int* h_vec, int perturb_k, uint32_t seed, int outer,
+                         uint64_t id0, hipStream_t s) {
+    if (n <= 0 || m <= 1 || perturb_k <= 0) return hipSuccess;
+    PerturbArgs p;
+    p.codes = codes;
+    p.n = n;
+    p.m = m;
+    p.ksel = perturb_k < m ? perturb_k : m;
+    for (int l = 0; l < m; ++l) p.h_vec[l] = h_vec[l];
+    p.seed = seed;
+    p.outer = outer;
+    p.id0 = id0;
+    hipLaunchKernelGGL(PerturbKernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s, p);
+    return hipGetLastError();
+}
+
+hipError_t LaunchIlsAccept(uint8_t* codes, float* a, float* cost, const uint8_t* cc, const float* ca, const float* ccost,
+                           int64_t n, int m, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(IlsAcceptKernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s, codes, a, cost,
+                       cc, ca, ccost, n, m);
     return hipGetLastError();
 }
 

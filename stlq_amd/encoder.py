@@ -42,7 +42,7 @@ def _c(a, dt):
 
 @dataclass
 class EncodeConfig:
-    """base.encode.* (include/stlq/common/config.h:473-482); ils_iters must stay 0."""
+    """base.encode.* (include/stlq/common/config.h:473-482)."""
 
     H_beam: int = 2
     icm_iters: int = 4
@@ -179,6 +179,21 @@ class Context:
                                       _p(cost, _f32p)))
         return codes, a, cost
 
+    def icm_ils(self, xC, codes, icm_iters, ils_iters, perturb_k, use_abs, seed, X=None, nx2=None,
+                sample_id_offset=0):
+        """ICM followed by the ILS outer loop (icm.cpp:872-1003); returns (codes, a, cost)."""
+        xC = _c(xC, np.float32)
+        codes = np.array(codes, dtype=np.uint8, order="C", copy=True)
+        n = xC.shape[0]
+        Xc = _c(X, np.float32) if X is not None else None
+        nx = _c(nx2, np.float32) if nx2 is not None else None
+        a = np.empty((n, self.m), np.float32)
+        cost = np.empty(n, np.float32)
+        check(self.lib.stlq_mi355_icm_ils(self.h, _p(Xc, _f32p), _p(nx, _f32p), _p(xC, _f32p), n, int(icm_iters),
+                                          int(ils_iters), int(perturb_k), int(bool(use_abs)), int(seed) & 0xFFFFFFFF,
+                                          int(sample_id_offset), _p(codes, _u8p), _p(a, _f32p), _p(cost, _f32p)))
+        return codes, a, cost
+
     def encode(self, X, cfg: EncodeConfig, want_mse=False):
         X = _c(X, np.float32)
         n = X.shape[0]
@@ -243,7 +258,7 @@ class Context:
             d, m = self.lr[0], len(self.lr[1])
         else:
             d, m = self.d, self.m
-        want = (not large_root) and (cfg.want_coeffs or cfg.icm_iters > 0)
+        want = (not large_root) and (cfg.want_coeffs or cfg.icm_iters > 0 or cfg.ils_iters > 0)
         dt = np.uint8 if input_u8 else np.float32
         ctype = ctypes.c_uint8 if input_u8 else ctypes.c_float
         err = []
@@ -341,25 +356,24 @@ def ComputeCosts(ctx: Context, xC, B, a, X_norm2):
     return ctx.compute_costs(xC, B, a, X_norm2)
 
 
-def _dynamic_icm(ctx, X, xC, icm_iters, ils_iters, perturb_k, seed, B, use_abs):
-    if ils_iters and perturb_k > 0 and ctx.m > 1:
-        raise NotImplementedError("ILS (ils_iters > 0) is not part of this build")
-    codes, a, cost = ctx.icm(xC, B, icm_iters, use_abs, seed, X=X)
-    return codes, a, cost
+def _dynamic_icm(ctx, X, xC, icm_iters, ils_iters, perturb_k, seed, B, use_abs, sample_id_offset):
+    return ctx.icm_ils(xC, B, icm_iters, ils_iters, perturb_k, use_abs, seed, X=X, sample_id_offset=sample_id_offset)
 
 
-def DynamicIcmWithIlsAbsNoNormal(ctx: Context, X, xC, icm_iters, ils_iters, perturb_k, seed, B):
-    """src/quantizer/icm.cpp:1153-1170 (ils_iters = 0): returns (B, a, cost)."""
-    return _dynamic_icm(ctx, X, xC, icm_iters, ils_iters, perturb_k, seed, B, True)
+def DynamicIcmWithIlsAbsNoNormal(ctx: Context, X, xC, icm_iters, ils_iters, perturb_k, seed, B,
+                                 print_progress=True, sample_id_offset=0):
+    """src/quantizer/icm.cpp:1153-1170 (icm.h:33-43): returns (B, a, cost)."""
+    return _dynamic_icm(ctx, X, xC, icm_iters, ils_iters, perturb_k, seed, B, True, sample_id_offset)
 
 
-def DynamicIcmWithIlsNoAbsNoNormal(ctx: Context, X, xC, icm_iters, ils_iters, perturb_k, seed, B):
-    """src/quantizer/icm.cpp:1132-1151 (ils_iters = 0): returns (B, a, cost)."""
-    return _dynamic_icm(ctx, X, xC, icm_iters, ils_iters, perturb_k, seed, B, False)
+def DynamicIcmWithIlsNoAbsNoNormal(ctx: Context, X, xC, icm_iters, ils_iters, perturb_k, seed, B,
+                                   print_progress=True, sample_id_offset=0):
+    """src/quantizer/icm.cpp:1132-1151 (icm.h:15-31): returns (B, a, cost)."""
+    return _dynamic_icm(ctx, X, xC, icm_iters, ils_iters, perturb_k, seed, B, False, sample_id_offset)
 
 
 def EncodeBase(ctx: Context, X, cfg: EncodeConfig):
-    """src/quantizer/encoder_encode_base.inc:1-106 (ils_iters = 0): (BaseEncoding, beam_mse, final_mse)."""
+    """src/quantizer/encoder_encode_base.inc:1-106: (BaseEncoding, beam_mse, final_mse)."""
     if X.shape[0] == 0 or X.shape[1] == 0:
         raise ValueError("Empty base dataset.")
     if X.shape[1] != ctx.d:

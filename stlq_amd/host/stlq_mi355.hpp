@@ -213,29 +213,28 @@ namespace detail {
 inline void DynamicIcm(const ColMajorMatrix<float>& X, const Precomp& precomp, const ColMajorMatrix<float>& xC,
                        int icm_iters, int ils_iters, int perturb_k, std::uint32_t seed, bool use_abs,
                        ColMajorMatrix<FullCode>* B, ColMajorMatrix<float>* a, std::vector<float>* X_norm2,
-                       std::vector<float>* cost) {
-    if (ils_iters > 0 && perturb_k > 0 && precomp.m > 1)
-        throw std::runtime_error("stlq_mi355: ILS (ils_iters > 0) is not part of this build");
+                       std::vector<float>* cost, std::uint64_t sample_id_offset) {
     stlq_mi355_ctx* ctx = Bind(precomp);
     if (X_norm2 && X_norm2->empty()) ComputeXNorm2(X, X_norm2);
     std::vector<float> cost_local;
     std::vector<float>* c = cost ? cost : &cost_local;
     c->resize(static_cast<std::size_t>(B->cols));
     *a = ColMajorMatrix<float>(precomp.m, B->cols);
-    Check(stlq_mi355_icm(ctx, X.data.data(), X_norm2 ? X_norm2->data() : nullptr, xC.data.data(), B->cols,
-                         icm_iters, use_abs ? 1 : 0, seed, B->data.data(), a->data.data(), c->data()));
+    Check(stlq_mi355_icm_ils(ctx, X.data.data(), X_norm2 ? X_norm2->data() : nullptr, xC.data.data(), B->cols,
+                             icm_iters, ils_iters, perturb_k, use_abs ? 1 : 0, seed, sample_id_offset,
+                             B->data.data(), a->data.data(), c->data()));
 }
 }  // namespace detail
 
-// DynamicIcmWithIlsAbsNoNormal / ...NoAbsNoNormal (src/quantizer/icm.cpp:1132-1170), ils_iters = 0.
+// DynamicIcmWithIlsAbsNoNormal / ...NoAbsNoNormal (src/quantizer/icm.cpp:1132-1170, icm.h:15-43).
 inline void DynamicIcmWithIlsAbsNoNormal(const ColMajorMatrix<float>& X, const Precomp& precomp,
                                          const ColMajorMatrix<float>& xC, int icm_iters, int ils_iters, int perturb_k,
                                          std::uint32_t seed, ColMajorMatrix<FullCode>* B, ColMajorMatrix<float>* a,
                                          std::vector<float>* X_norm2, std::vector<float>* cost,
                                          bool print_progress = true, std::uint64_t sample_id_offset = 0) {
     (void)print_progress;
-    (void)sample_id_offset;  // only seeds ILS perturbations (icm.cpp:953-956)
-    detail::DynamicIcm(X, precomp, xC, icm_iters, ils_iters, perturb_k, seed, true, B, a, X_norm2, cost);
+    detail::DynamicIcm(X, precomp, xC, icm_iters, ils_iters, perturb_k, seed, true, B, a, X_norm2, cost,
+                       sample_id_offset);
 }
 
 inline void DynamicIcmWithIlsNoAbsNoNormal(const ColMajorMatrix<float>& X, const Precomp& precomp,
@@ -245,12 +244,12 @@ inline void DynamicIcmWithIlsNoAbsNoNormal(const ColMajorMatrix<float>& X, const
                                            std::vector<float>* cost, bool print_progress = true,
                                            std::uint64_t sample_id_offset = 0) {
     (void)print_progress;
-    (void)sample_id_offset;
-    detail::DynamicIcm(X, precomp, xC, icm_iters, ils_iters, perturb_k, seed, false, B, a, X_norm2, cost);
+    detail::DynamicIcm(X, precomp, xC, icm_iters, ils_iters, perturb_k, seed, false, B, a, X_norm2, cost,
+                       sample_id_offset);
 }
 
-// EncodeBase (src/quantizer/encoder_encode_base.inc:1-106) without the ILS outer loop; the
-// whole pipeline (xC GEMM, beam, LS, ICM, costs) runs on the device.
+// EncodeBase (src/quantizer/encoder_encode_base.inc:1-106); the whole pipeline (xC GEMM, beam,
+// LS, ICM, ILS, costs) runs on the device.
 inline bool EncodeBase(const EncodeOptions& opt, const ColMajorMatrix<float>& Xb, const CodebookPack& codebooks,
                        const Precomp& precomp, BaseEncoding* base, float* out_beam_mse, float* out_final_mse,
                        std::string* error) {
@@ -266,12 +265,8 @@ inline bool EncodeBase(const EncodeOptions& opt, const ColMajorMatrix<float>& Xb
         if (error) *error = "Precomp dimensions do not match codebooks or dataset.";
         return false;
     }
-    if (opt.ils_iters > 0 && opt.perturb_k > 0 && precomp.m > 1) {
-        if (error) *error = "ILS (ils_iters > 0) is not part of this build.";
-        return false;
-    }
-    stlq_mi355_encode_params p{std::max(1, opt.H_beam), opt.icm_iters, 0, opt.perturb_k, opt.use_abs ? 1 : 0,
-                               static_cast<std::uint32_t>(opt.seed), 1};
+    stlq_mi355_encode_params p{std::max(1, opt.H_beam), opt.icm_iters, opt.ils_iters, opt.perturb_k,
+                               opt.use_abs ? 1 : 0, static_cast<std::uint32_t>(opt.seed), 1};
     base->B = ColMajorMatrix<FullCode>(precomp.m, Xb.cols);
     base->a = ColMajorMatrix<float>(precomp.m, Xb.cols);
     double bm = 0.0, fm = 0.0;

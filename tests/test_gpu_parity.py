@@ -152,12 +152,39 @@ def test_icm_bit_exact(ctx, orc, use_abs, m, K, d, iters):
     assert np.array_equal(_bits(so), _bits(sg))
 
 
-def _oracle_encode(orc, X, C, h, Hb, icm_iters=0, use_abs=True, seed=38251450, gemm_mode=1):
+@pytest.mark.parametrize("m,K,d,icm,ils,pk,off", [(4, 64, 32, 2, 3, 2, 0), (5, 64, 32, 1, 4, 3, 5000),
+                                                  (8, 256, 96, 2, 2, 3, 0), (10, 32, 40, 0, 3, 10, 77)])
+def test_ils_bit_exact(ctx, orc, m, K, d, icm, ils, pk, off):
+    """ICM + ILS rounds (perturbation stream keyed by global sample id, continuing layer-order
+    stream, accept-if-better) match the oracle bit for bit."""
+    h = [K] * m
+    X, C = rvq_problem(60 + m, 1500, d, m, K, kind="sphere" if d == 96 else "gauss", train_n=max(2000, 4 * K),
+                       iters=4)
+    G, inv = _set(ctx, C, h)
+    nx2 = orc.xnorm2(X)
+    xC = orc.gemm_xc(C, X)
+    codes0, _ = orc.beam_search(nx2, xC, G, h, 2)
+    seed = 38251450
+    for use_abs in (True, False):
+        co, ao, so, _ = orc.icm_ils(xC, G, inv, h, nx2, codes0, icm, ils, pk, use_abs, seed, off)
+        cg, ag, sg = ctx.icm_ils(xC, codes0, icm, ils, pk, use_abs, seed, nx2=nx2, sample_id_offset=off)
+        if icm > 0:  # (without ICM sweeps a random perturbation is hardly ever an improvement)
+            ci, _, _, _ = orc.icm(xC, G, inv, h, nx2, codes0, icm, use_abs, seed)
+            assert np.any(co != ci)  # the ILS rounds moved some vectors
+        assert np.array_equal(co, cg), (use_abs, np.nonzero(np.any(co != cg, axis=1))[0][:10])
+        assert np.array_equal(_bits(ao), _bits(ag))
+        assert np.array_equal(_bits(so), _bits(sg))
+
+
+def _oracle_encode(orc, X, C, h, Hb, icm_iters=0, use_abs=True, seed=38251450, gemm_mode=1, ils_iters=0,
+                   perturb_k=3):
     G, inv = orc.build_precomp(C, h)
     nx2 = orc.xnorm2(X)
     xC = orc.gemm_xc(C, X, mode=gemm_mode)
     codes, err = orc.beam_search(nx2, xC, G, h, Hb)
-    if icm_iters:
+    if ils_iters:
+        codes, a, cost, _ = orc.icm_ils(xC, G, inv, h, nx2, codes, icm_iters, ils_iters, perturb_k, use_abs, seed)
+    elif icm_iters:
         codes, a, cost, _ = orc.icm(xC, G, inv, h, nx2, codes, icm_iters, use_abs, seed)
     else:
         a, _ = orc.solve_ls_all(xC, G, h, codes)
@@ -194,6 +221,38 @@ def test_encode_end_to_end_bit_exact(ctx, orc, cfg):
     assert np.isfinite(bm) and np.isfinite(fm) and fm <= bm * (1 + 1e-6)
     want_fm = np.mean(np.maximum(cost_o.astype(np.float64), 0.0))
     assert abs(fm - want_fm) <= 1e-9 * abs(want_fm)
+
+
+def test_encode_with_ils_end_to_end(ctx, orc, monkeypatch):
+    """EncodeBase with the production ILS defaults (4 ICM sweeps, 32 ILS rounds, 3 perturbed
+    codes): GPU end to end equals the oracle; tiled encodes (global sample ids per tile), the
+    device entry point and the stream agree with it too."""
+    X, C = rvq_problem(53, 3000, 32, 6, 64, train_n=2000, iters=3)
+    h = [64] * 6
+    ctx.set_codebooks(C, h)
+    cfg = EncodeConfig(H_beam=4, icm_iters=4, ils_iters=32, perturb_k=3, want_coeffs=True)
+    codes_g, a_g, cost_g, (bm, fm) = ctx.encode(X, cfg, want_mse=True)
+    codes_o, a_o, cost_o = _oracle_encode(orc, X, C, h, 4, icm_iters=4, ils_iters=32, perturb_k=3)
+    assert np.array_equal(codes_o, codes_g)
+    assert np.array_equal(_bits(a_o), _bits(a_g))
+    assert np.array_equal(_bits(cost_o), _bits(cost_g))
+    assert fm <= bm
+    monkeypatch.setenv("STLQ_MI355_WORKSPACE_GB", "0.0005")  # ~1k-vector tiles
+    codes_t, _, cost_t, _ = ctx.encode(X, cfg)
+    assert np.array_equal(codes_t, codes_g) and np.array_equal(_bits(cost_t), _bits(cost_g))
+    monkeypatch.delenv("STLQ_MI355_WORKSPACE_GB")
+    got = {}
+
+    def fill(first, count, dst):
+        dst[:] = X[first:first + count]
+
+    def sink(first, count, res):
+        got[first] = (res["codes"].copy(), res["cost"].copy())
+
+    ctx.encode_stream(X.shape[0], 700, cfg, fill, sink)
+    codes_s = np.concatenate([got[k][0] for k in sorted(got)])
+    cost_s = np.concatenate([got[k][1] for k in sorted(got)])
+    assert np.array_equal(codes_s, codes_g) and np.array_equal(_bits(cost_s), _bits(cost_g))
 
 
 @pytest.mark.parametrize("cfg", ["C1", "C2", "C3", "C4"])
@@ -319,7 +378,7 @@ def test_errors_are_reported(ctx):
     with pytest.raises(StlqError, match="H_beam"):
         ctx.beam_search(np.zeros((10, 8), np.float32), 65, nx2=np.ones(10, np.float32))
     with pytest.raises(StlqError, match="ils_iters"):
-        ctx.encode(X, EncodeConfig(H_beam=2, icm_iters=0, ils_iters=3))
+        ctx.encode(X, EncodeConfig(H_beam=2, icm_iters=0, ils_iters=-1))
     with pytest.raises(StlqError):
         ctx.set_codebooks(np.zeros((300, 8), np.float32), [300])
 

@@ -269,3 +269,24 @@ def test_forced_root(orc):
     g = X.astype(np.float64) @ C0.astype(np.float64).T
     want = np.argmax(g * g / np.sum(C0.astype(np.float64) ** 2, axis=1), axis=1)
     assert np.mean(cid1 == want) >= 0.99
+
+
+def test_ils_never_worse_and_shard_invariant(orc):
+    """ILS only accepts strict improvements, so every vector's cost is at most its ICM-only cost;
+    perturbations are keyed by the global sample id, so two shards with their offsets reproduce
+    the whole set exactly."""
+    h = [32] * 6
+    X, C = rvq_problem(61, 1200, 24, 6, 32, train_n=2000, iters=3)
+    G, inv, nx2, xC = _prep(orc, X, C, h)
+    codes, _ = orc.beam_search(nx2, xC, G, h, 4)
+    k0, a0, c0, _ = orc.icm(xC, G, inv, h, nx2, codes, 2, True, 9)
+    k1, a1, c1, _ = orc.icm_ils(xC, G, inv, h, nx2, codes, 2, 4, 3, True, 9)
+    assert np.all(c1 <= c0)
+    assert np.any(k1 != k0)  # the rounds did move some vectors
+    ka, aa, ca, _ = orc.icm_ils(xC[:700], G, inv, h, nx2[:700], codes[:700], 2, 4, 3, True, 9, 0)
+    kb, ab, cb, _ = orc.icm_ils(xC[700:], G, inv, h, nx2[700:], codes[700:], 2, 4, 3, True, 9, 700)
+    assert np.array_equal(np.concatenate([ka, kb]), k1)
+    assert np.array_equal(np.concatenate([ca, cb]).view(np.uint32), c1.view(np.uint32))
+    # ils_iters = 0 is the plain ICM
+    k2, _, c2, _ = orc.icm_ils(xC, G, inv, h, nx2, codes, 2, 0, 3, True, 9)
+    assert np.array_equal(k2, k0) and np.array_equal(c2.view(np.uint32), c0.view(np.uint32))
