@@ -162,7 +162,10 @@ int stlq_mi355_encode_device(stlq_mi355_ctx* ctx, const float* dX, int64_t n,
  *            otherwise fp32 (d floats each).
  *  large_root: encode with the large-root codebooks (stlq_mi355_set_large_root): the beam of
  *            BeamSearchPrefixLSLargeRoot with root_mode 0 (top-H_beam roots) or 1 (nearest
- *            root); the chunk output then carries cluster_id, B_small and best_err.
+ *            root); the chunk output then carries cluster_id, B_small and best_err, and, when
+ *            encode asks for coefficients or ICM/ILS, a and cost from the large-root refit
+ *            (SolveLeastSquaresAllLargeRoot + ComputeCostsLargeRoot, or
+ *            DynamicIcmWithIls*NoNormalLargeRoot; encode_base_streaming.cpp:1117-1210).
  *            Otherwise the full-precomp EncodeBase of `encode` (codes, and a/cost when wanted).
  * fill/sink return 0 on success. */
 typedef struct stlq_mi355_stream_params {
@@ -174,8 +177,8 @@ typedef struct stlq_mi355_stream_params {
 
 typedef struct stlq_mi355_chunk_out {
     const uint8_t* codes;       /* full precomp: m x count */
-    const float* a;             /* full precomp with coefficients: m x count, else NULL */
-    const float* cost;          /* full precomp with coefficients: count, else NULL */
+    const float* a;             /* with coefficients (or ICM/ILS): m x count, else NULL */
+    const float* cost;          /* with coefficients (or ICM/ILS): count, else NULL */
     const uint32_t* cluster_id; /* large root: count */
     const uint8_t* B_small;     /* large root: (m-1) x count */
     const float* best_err;      /* large root: count */
@@ -222,6 +225,33 @@ int stlq_mi355_beam_search_large_root(stlq_mi355_ctx* ctx, const float* X, const
                                       int64_t n, int H_beam, const uint32_t* forced_root,
                                       int root_mode, uint32_t* cluster_id, uint8_t* B_small,
                                       float* best_err);
+
+/* Large-root refit. Layer 0 of vector i is its root cluster_id[i] (< h0); B_small ((m-1) x n)
+ * holds layers 1..m-1. X (d x n) host; xC_small (Hs x n) host or NULL (device MFMA GEMM); nx2
+ * host or NULL (formed from X). b0 = <C0[:,root], x> is formed on the device in the reference's
+ * omp-simd order. */
+
+/* SolveLeastSquaresAllLargeRoot (src/quantizer/least_squares.cpp:667-745,
+ * include/stlq/quantizer/least_squares.h:54-59): a (m x n); a vector whose system fails even with
+ * the diagonal bumps gets a = 0 and is counted in fail_count (nullable). */
+int stlq_mi355_solve_ls_all_large_root(stlq_mi355_ctx* ctx, const float* X, const float* xC_small,
+                                       int64_t n, const uint32_t* cluster_id, const uint8_t* B_small,
+                                       float* a, int64_t* fail_count);
+
+/* ComputeCostsLargeRoot (src/quantizer/cost_utils.cpp:211-233, cost_utils.h:37-44): cost (n). */
+int stlq_mi355_compute_costs_large_root(stlq_mi355_ctx* ctx, const float* X, const float* xC_small,
+                                        int64_t n, const uint32_t* cluster_id, const uint8_t* B_small,
+                                        const float* a, const float* nx2, float* cost);
+
+/* DynamicIcmWithIls{Abs,NoAbs}NoNormalLargeRoot (src/quantizer/icm.cpp:1005-1120,
+ * include/stlq/quantizer/icm.h:45-75): LS refit and costs, icm_iters sweeps over layers 1..m-1
+ * (the roots stay), then ils_iters perturbation rounds keyed by (seed, round,
+ * sample_id_offset + i). B_small is updated in place; a (m x n) and cost (n) are outputs. */
+int stlq_mi355_icm_ils_large_root(stlq_mi355_ctx* ctx, const float* X, const float* nx2,
+                                  const float* xC_small, int64_t n, const uint32_t* cluster_id,
+                                  int icm_iters, int ils_iters, int perturb_k, int use_abs,
+                                  uint32_t seed, uint64_t sample_id_offset, uint8_t* B_small,
+                                  float* a, float* cost);
 
 #ifdef __cplusplus
 }

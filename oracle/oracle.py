@@ -67,6 +67,16 @@ def lib():
                                                  _u32p, _u8p, _f32p, _int]
         L.orc_large_root_candidates.argtypes = [_f32p, _int, _f32p, _f32p, _f32p, _int, _int, _i64, _u32p, _int,
                                                 _f32p, _i32p, _f32p, _f32p, _int]
+        L.orc_invnorm_small.argtypes = [_f32p, _int, _int, _f32p]
+        L.orc_solve_ls_all_large_root.argtypes = [_f32p, _int, _f32p, _f32p, _int, _f32p, _f32p, _f32p, _int, _int,
+                                                  _i32p, _u32p, _u8p, _i64, _f32p, _int]
+        L.orc_solve_ls_all_large_root.restype = _i64
+        L.orc_compute_costs_large_root.argtypes = [_f32p, _int, _f32p, _f32p, _int, _f32p, _f32p, _f32p, _int, _int,
+                                                   _i32p, _u32p, _u8p, _f32p, _f32p, _i64, _f32p, _int]
+        L.orc_icm_ils_large_root.argtypes = [_f32p, _int, _f32p, _f32p, _int, _f32p, _f32p, _f32p, _f32p, _int, _int,
+                                             _i32p, _u32p, _f32p, _i64, _int, _int, _int, _int, ctypes.c_uint32,
+                                             ctypes.c_uint64, _u8p, _f32p, _f32p, _int]
+        L.orc_icm_ils_large_root.restype = _i64
         _lib = L
     return _lib
 
@@ -271,3 +281,64 @@ def large_root_candidates(X, nx2, C0, norm0, H_beam, forced_root=None, root_mode
                                     H_beam, n, _p(fr, _u32p), root_mode, _p(errs, _f32p), _p(codes, _i32p),
                                     _p(a0, _f32p), _p(r00, _f32p), nthreads)
     return errs, codes, a0, r00
+
+
+def invnorm_small(C_small):
+    """invnorm_small_flat of BuildPrecompLargeRoot (precomp_large_root.cpp:101-114)."""
+    C_small = _c(C_small, np.float32)
+    Hs, d = C_small.shape
+    out = np.empty(Hs, np.float32)
+    lib().orc_invnorm_small(_p(C_small, _f32p), d, Hs, _p(out, _f32p))
+    return out
+
+
+def _lr_args(X, C0, norm0, xC_small, G_small, G0S, h_vec, cluster_id):
+    X = _c(X, np.float32)
+    C0 = _c(C0, np.float32)
+    n, d = X.shape
+    return (X, d, C0, _c(norm0, np.float32), C0.shape[0], _c(xC_small, np.float32), _c(G_small, np.float32),
+            _c(G0S, np.float32), _c(h_vec, np.int32), _c(cluster_id, np.uint32), n)
+
+
+def solve_ls_all_large_root(X, C0, norm0, xC_small, G_small, G0S, h_vec, cluster_id, B_small, nthreads=0):
+    """SolveLeastSquaresAllLargeRoot; returns (a (n, m), ls_fails). B_small is (n, m-1)."""
+    X, d, C0, norm0, h0, xs, Gs, G0S, hv, cid, n = _lr_args(X, C0, norm0, xC_small, G_small, G0S, h_vec, cluster_id)
+    Bs = _c(B_small, np.uint8)
+    m = len(hv)
+    a = np.empty((n, m), np.float32)
+    fails = lib().orc_solve_ls_all_large_root(_p(X, _f32p), d, _p(C0, _f32p), _p(norm0, _f32p), h0, _p(xs, _f32p),
+                                              _p(Gs, _f32p), _p(G0S, _f32p), Gs.shape[0], m, _p(hv, _i32p),
+                                              _p(cid, _u32p), _p(Bs, _u8p), n, _p(a, _f32p), nthreads)
+    return a, int(fails)
+
+
+def compute_costs_large_root(X, C0, norm0, xC_small, G_small, G0S, h_vec, cluster_id, B_small, a, nx2, nthreads=0):
+    """ComputeCostsLargeRoot; returns cost (n,)."""
+    X, d, C0, norm0, h0, xs, Gs, G0S, hv, cid, n = _lr_args(X, C0, norm0, xC_small, G_small, G0S, h_vec, cluster_id)
+    Bs = _c(B_small, np.uint8)
+    a = _c(a, np.float32)
+    nx2 = _c(nx2, np.float32)
+    cost = np.empty(n, np.float32)
+    lib().orc_compute_costs_large_root(_p(X, _f32p), d, _p(C0, _f32p), _p(norm0, _f32p), h0, _p(xs, _f32p),
+                                       _p(Gs, _f32p), _p(G0S, _f32p), Gs.shape[0], len(hv), _p(hv, _i32p),
+                                       _p(cid, _u32p), _p(Bs, _u8p), _p(a, _f32p), _p(nx2, _f32p), n,
+                                       _p(cost, _f32p), nthreads)
+    return cost
+
+
+def icm_ils_large_root(X, C0, norm0, xC_small, G_small, G0S, invs, h_vec, cluster_id, nx2, B_small, icm_iters,
+                       ils_iters, perturb_k, use_abs, seed, sample_id_offset=0, nthreads=0):
+    """DynamicIcmWithIls{Abs,NoAbs}NoNormalLargeRoot; returns (B_small, a, cost, ls_fails)."""
+    X, d, C0, norm0, h0, xs, Gs, G0S, hv, cid, n = _lr_args(X, C0, norm0, xC_small, G_small, G0S, h_vec, cluster_id)
+    Bs = np.array(B_small, dtype=np.uint8, copy=True, order="C")
+    invs = _c(invs, np.float32)
+    nx2 = _c(nx2, np.float32)
+    m = len(hv)
+    a = np.empty((n, m), np.float32)
+    cost = np.empty(n, np.float32)
+    fails = lib().orc_icm_ils_large_root(_p(X, _f32p), d, _p(C0, _f32p), _p(norm0, _f32p), h0, _p(xs, _f32p),
+                                         _p(Gs, _f32p), _p(G0S, _f32p), _p(invs, _f32p), Gs.shape[0], m,
+                                         _p(hv, _i32p), _p(cid, _u32p), _p(nx2, _f32p), n, icm_iters, ils_iters,
+                                         perturb_k, int(bool(use_abs)), seed & 0xFFFFFFFF, int(sample_id_offset),
+                                         _p(Bs, _u8p), _p(a, _f32p), _p(cost, _f32p), nthreads)
+    return Bs, a, cost, int(fails)

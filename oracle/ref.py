@@ -67,8 +67,15 @@ def lib():
         L.ref_solve_ls_all.argtypes = [_f32p, _f32p, _int, _i32p, _int, _u8p, _int, _f32p]
         L.ref_icm.argtypes = [_f32p, _int, _int, _f32p, _f32p, _f32p, _int, _i32p, _int, _int, _int, _int, _int,
                               ctypes.c_uint32, ctypes.c_uint64, _u8p, _f32p, _f32p]
+        L.ref_solve_ls_all_large_root.argtypes = [_f32p, _int, _int, _f32p, _f32p, _f32p, _int, _f32p, _i32p, _int,
+                                                  _f32p, _u32p, _u8p, _f32p]
+        L.ref_compute_costs_large_root.argtypes = [_f32p, _int, _int, _f32p, _f32p, _f32p, _int, _f32p, _i32p, _int,
+                                                   _f32p, _u32p, _u8p, _f32p, _f32p, _f32p]
+        L.ref_icm_large_root.argtypes = [_f32p, _int, _int, _f32p, _f32p, _f32p, _int, _f32p, _f32p, _i32p, _int,
+                                         _f32p, _u32p, _int, _int, _int, _int, ctypes.c_uint32, ctypes.c_uint64,
+                                         _u8p, _f32p, _f32p]
         for f in (L.ref_xnorm2, L.ref_beam_search, L.ref_compute_costs, L.ref_expand_large_root, L.ref_solve_ls_all,
-                  L.ref_icm):
+                  L.ref_icm, L.ref_solve_ls_all_large_root, L.ref_compute_costs_large_root, L.ref_icm_large_root):
             f.restype = None
         _lib = L
     return _lib
@@ -167,3 +174,46 @@ def expand_large_root(G_small, G0S, h_vec, xC_small, H_beam, root_errs, root_cod
                                 _p(_c(root_a0, np.float32), _f32p), _p(_c(root_r00, np.float32), _f32p),
                                 _p(cid, _u32p), _p(Bs, _u8p))
     return cid, Bs
+
+
+def _lr(X, C0, norm0, G_small, G0S, h_vec, xC_small, cluster_id):
+    X = _c(X, np.float32)
+    n, d = X.shape
+    return (X, d, n, _c(C0, np.float32), _c(norm0, np.float32), _c(G_small, np.float32), _c(G0S, np.float32),
+            _c(h_vec, np.int32), _c(xC_small, np.float32), _c(cluster_id, np.uint32))
+
+
+def solve_ls_all_large_root(X, C0, norm0, G_small, G0S, h_vec, xC_small, cluster_id, B_small):
+    """stlq::SolveLeastSquaresAllLargeRoot. G0S as the oracle returns it (numpy (Hs, h0))."""
+    X, d, n, C0, norm0, Gs, G0S, hv, xs, cid = _lr(X, C0, norm0, G_small, G0S, h_vec, xC_small, cluster_id)
+    a = np.empty((n, len(hv)), np.float32)
+    lib().ref_solve_ls_all_large_root(_p(X, _f32p), d, n, _p(C0, _f32p), _p(norm0, _f32p), _p(Gs, _f32p),
+                                      Gs.shape[0], _p(G0S, _f32p), _p(hv, _i32p), len(hv), _p(xs, _f32p),
+                                      _p(cid, _u32p), _p(_c(B_small, np.uint8), _u8p), _p(a, _f32p))
+    return a
+
+
+def compute_costs_large_root(X, C0, norm0, G_small, G0S, h_vec, xC_small, cluster_id, B_small, a, nx2):
+    """stlq::ComputeCostsLargeRoot."""
+    X, d, n, C0, norm0, Gs, G0S, hv, xs, cid = _lr(X, C0, norm0, G_small, G0S, h_vec, xC_small, cluster_id)
+    cost = np.empty(n, np.float32)
+    lib().ref_compute_costs_large_root(_p(X, _f32p), d, n, _p(C0, _f32p), _p(norm0, _f32p), _p(Gs, _f32p),
+                                       Gs.shape[0], _p(G0S, _f32p), _p(hv, _i32p), len(hv), _p(xs, _f32p),
+                                       _p(cid, _u32p), _p(_c(B_small, np.uint8), _u8p), _p(_c(a, np.float32), _f32p),
+                                       _p(_c(nx2, np.float32), _f32p), _p(cost, _f32p))
+    return cost
+
+
+def icm_large_root(X, C0, norm0, G_small, G0S, invs, h_vec, xC_small, cluster_id, B_small, icm_iters, use_abs, seed,
+                   ils_iters=0, perturb_k=3, sample_id_offset=0):
+    """stlq::DynamicIcmWithIls{Abs,NoAbs}NoNormalLargeRoot; returns (B_small, a, cost)."""
+    X, d, n, C0, norm0, Gs, G0S, hv, xs, cid = _lr(X, C0, norm0, G_small, G0S, h_vec, xC_small, cluster_id)
+    Bs = np.array(B_small, dtype=np.uint8, copy=True, order="C")
+    m = len(hv)
+    a = np.empty((n, m), np.float32)
+    cost = np.empty(n, np.float32)
+    lib().ref_icm_large_root(_p(X, _f32p), d, n, _p(C0, _f32p), _p(norm0, _f32p), _p(Gs, _f32p), Gs.shape[0],
+                             _p(G0S, _f32p), _p(_c(invs, np.float32), _f32p), _p(hv, _i32p), m, _p(xs, _f32p),
+                             _p(cid, _u32p), icm_iters, ils_iters, perturb_k, int(bool(use_abs)), seed & 0xFFFFFFFF,
+                             int(sample_id_offset), _p(Bs, _u8p), _p(a, _f32p), _p(cost, _f32p))
+    return Bs, a, cost

@@ -9,8 +9,8 @@
 // and linked against the image's MKL runtime for LAPACK spotrf_/spotrs_ (least_squares.cpp).
 // blas.cpp is not buildable here (it includes cblas.h, which the image lacks), so GemmRaw and
 // BlasSetThreads stay unresolved. They are only reached from the root-score GEMM of
-// BeamSearchPrefixLSLargeRoot (beam_search.cpp:623-690) and from ILS/large-root paths this
-// driver never calls; the library is loaded with lazy binding.
+// BeamSearchPrefixLSLargeRoot (beam_search.cpp:623-690), which this driver never calls; the
+// library is loaded with lazy binding.
 //
 // Array conventions (all column-major as in the reference's ColMajorMatrix):
 //   X d x n, xC H x n, G H x H, codes m x n (uint8), a m x n.
@@ -49,6 +49,37 @@ stlq::ColMajorMatrix<T> Wrap(const T* src, int rows, int cols) {
     stlq::ColMajorMatrix<T> M(rows, cols);
     if (src) std::memcpy(M.data.data(), src, sizeof(T) * M.data.size());
     return M;
+}
+
+// A PrecompLargeRoot (precomp_large_root.h:12-38) from arrays built by the caller: C0 d x h0,
+// norm0 h0, G_small Hs x Hs, G0S h0 x Hs, invnorm_small Hs (may be null), no G0S_T.
+stlq::PrecompLargeRoot MakePrecompLargeRoot(int d, int m, const int* h_vec, const float* C0, const float* norm0,
+                                            const float* G_small, int Hs, const float* G0S,
+                                            const float* invnorm_small) {
+    stlq::PrecompLargeRoot pre;
+    pre.d = d;
+    pre.m = m;
+    pre.h_vec.assign(h_vec, h_vec + m);
+    int off = 0;
+    for (int l = 0; l < m; ++l) {
+        pre.offsets.push_back(off);
+        off += h_vec[l];
+    }
+    const int h0 = h_vec[0];
+    pre.C0 = Wrap(C0, d, h0);
+    pre.norm0.assign(norm0, norm0 + h0);
+    pre.H_small = Hs;
+    pre.small_offsets.assign(m, 0);
+    int so = 0;
+    for (int l = 1; l < m; ++l) {
+        pre.small_offsets[l] = so;
+        so += h_vec[l];
+    }
+    pre.G_small = Wrap(G_small, Hs, Hs);
+    pre.G0S = Wrap(G0S, h0, Hs);
+    if (invnorm_small) pre.invnorm_small_flat.assign(invnorm_small, invnorm_small + Hs);
+    pre.ready = true;
+    return pre;
 }
 
 }  // namespace
@@ -152,6 +183,62 @@ void ref_expand_large_root(const float* G_small, int Hs, const float* G0S, int h
                                                              root_r00, &cid, &Bs);
     std::memcpy(cluster_id, cid.data(), sizeof(uint32_t) * static_cast<std::size_t>(n));
     std::memcpy(B_small, Bs.data.data(), Bs.data.size());
+}
+
+// stlq::SolveLeastSquaresAllLargeRoot (least_squares.cpp:667-745). B_small (m-1) x n.
+void ref_solve_ls_all_large_root(const float* X, int d, int n, const float* C0, const float* norm0,
+                                 const float* G_small, int Hs, const float* G0S, const int* h_vec, int m,
+                                 const float* xC_small, const uint32_t* cluster_id, const uint8_t* B_small, float* a) {
+    const auto pre = MakePrecompLargeRoot(d, m, h_vec, C0, norm0, G_small, Hs, G0S, nullptr);
+    const auto Xm = Wrap(X, d, n);
+    const auto xs = Wrap(xC_small, Hs, n);
+    const std::vector<std::uint32_t> cid(cluster_id, cluster_id + n);
+    const auto Bs = Wrap(B_small, m - 1, n);
+    stlq::ColMajorMatrix<float> am;
+    stlq::SolveLeastSquaresAllLargeRoot(pre, Xm, xs, cid, Bs, &am);
+    std::memcpy(a, am.data.data(), sizeof(float) * am.data.size());
+}
+
+// stlq::ComputeCostsLargeRoot (cost_utils.cpp:211-233).
+void ref_compute_costs_large_root(const float* X, int d, int n, const float* C0, const float* norm0,
+                                  const float* G_small, int Hs, const float* G0S, const int* h_vec, int m,
+                                  const float* xC_small, const uint32_t* cluster_id, const uint8_t* B_small,
+                                  const float* a, const float* nx2, float* cost) {
+    const auto pre = MakePrecompLargeRoot(d, m, h_vec, C0, norm0, G_small, Hs, G0S, nullptr);
+    const auto Xm = Wrap(X, d, n);
+    const auto xs = Wrap(xC_small, Hs, n);
+    const std::vector<std::uint32_t> cid(cluster_id, cluster_id + n);
+    const auto Bs = Wrap(B_small, m - 1, n);
+    const auto am = Wrap(a, m, n);
+    const std::vector<float> xn(nx2, nx2 + n);
+    std::vector<float> out;
+    stlq::ComputeCostsLargeRoot(pre, Xm, xs, cid, Bs, am, xn, &out);
+    std::memcpy(cost, out.data(), sizeof(float) * static_cast<std::size_t>(n));
+}
+
+// stlq::DynamicIcmWithIls{Abs,NoAbs}NoNormalLargeRoot (icm.cpp:1005-1120, wrappers below it):
+// LS refit, costs, ICM sweeps and ILS rounds with the roots fixed. B_small is updated in place.
+void ref_icm_large_root(const float* X, int d, int n, const float* C0, const float* norm0, const float* G_small,
+                        int Hs, const float* G0S, const float* invnorm_small, const int* h_vec, int m,
+                        const float* xC_small, const uint32_t* cluster_id, int icm_iters, int ils_iters,
+                        int perturb_k, int use_abs, uint32_t seed, uint64_t sample_id_offset, uint8_t* B_small,
+                        float* a, float* cost) {
+    const auto pre = MakePrecompLargeRoot(d, m, h_vec, C0, norm0, G_small, Hs, G0S, invnorm_small);
+    const auto Xm = Wrap(X, d, n);
+    const auto xs = Wrap(xC_small, Hs, n);
+    const std::vector<std::uint32_t> cid(cluster_id, cluster_id + n);
+    auto Bs = Wrap(B_small, m - 1, n);
+    stlq::ColMajorMatrix<float> am;
+    std::vector<float> xn2, cst;
+    if (use_abs)
+        stlq::DynamicIcmWithIlsAbsNoNormalLargeRoot(Xm, pre, xs, icm_iters, ils_iters, perturb_k, seed, cid, &Bs, &am,
+                                                   &xn2, &cst, false, sample_id_offset);
+    else
+        stlq::DynamicIcmWithIlsNoAbsNoNormalLargeRoot(Xm, pre, xs, icm_iters, ils_iters, perturb_k, seed, cid, &Bs,
+                                                     &am, &xn2, &cst, false, sample_id_offset);
+    std::memcpy(B_small, Bs.data.data(), Bs.data.size());
+    std::memcpy(a, am.data.data(), sizeof(float) * am.data.size());
+    std::memcpy(cost, cst.data(), sizeof(float) * cst.size());
 }
 
 }  // extern "C"

@@ -970,3 +970,308 @@ int orc_large_root_candidates(const float* X, int d, const float* nx2, const flo
 }
 
 }  // extern "C"
+
+// ---------------------------------------------------------------------------------------------
+// Large root: LS refit, costs and ICM/ILS with layer 0 fixed to the vector's root code.
+namespace {
+
+// Dot product in the reference build's OpenMP-simd order (least_squares.cpp:35-42 Dot,
+// icm.cpp:67-74 DotF32, cost_utils.cpp:55-60): the four-lane order of SimdLane4SumSq.
+inline float SimdLane4Dot(const float* a, const float* b, int d) {
+    float p0 = 0.0f, p1 = 0.0f, p2 = 0.0f, p3 = 0.0f;
+    const int d4 = d & ~3;
+    for (int t = 0; t < d4; t += 4) {
+        p0 += a[t] * b[t];
+        p1 += a[t + 1] * b[t + 1];
+        p2 += a[t + 2] * b[t + 2];
+        p3 += a[t + 3] * b[t + 3];
+    }
+    for (int t = d4; t < d; ++t) p0 += a[t] * b[t];
+    float s = 0.0f;
+    s += p0;
+    s += p1;
+    s += p2;
+    s += p3;
+    return s;
+}
+
+// The large-root precomp and per-vector inputs (precomp_large_root.h:12-38). G0S is the
+// reference's h0 x Hs column-major matrix: G0S(root, flat) = G0S[flat*h0 + root]; G_small is
+// Hs x Hs column-major; B_small holds m-1 codes per vector (layers 1..m-1).
+struct LrView {
+    const float* X;
+    int d;
+    const float* C0;
+    const float* norm0;
+    int h0;
+    const float* xCs;
+    const float* Gs;
+    const float* G0S;
+    int Hs;
+    int m;
+    const int* h_vec;
+    std::vector<int> soff;
+    const uint32_t* cid;
+
+    float G0SAt(uint32_t root, int flat) const { return G0S[static_cast<std::size_t>(flat) * h0 + root]; }
+    float GsAt(int row, int col) const { return Gs[static_cast<std::size_t>(col) * Hs + row]; }
+    const float* XCol(int64_t i) const { return xCs + static_cast<std::size_t>(i) * Hs; }
+    float RootDot(int64_t i) const {
+        return SimdLane4Dot(C0 + static_cast<std::size_t>(cid[i]) * d, X + static_cast<std::size_t>(i) * d, d);
+    }
+};
+
+LrView MakeLrView(const float* X, int d, const float* C0, const float* norm0, int h0, const float* xCs,
+                  const float* Gs, const float* G0S, int Hs, int m, const int* h_vec, const uint32_t* cid) {
+    LrView v{X, d, C0, norm0, h0, xCs, Gs, G0S, Hs, m, h_vec, std::vector<int>(static_cast<std::size_t>(m), 0), cid};
+    int o = 0;
+    for (int l = 1; l < m; ++l) {  // precomp_large_root.cpp:95-98
+        v.soff[l] = o;
+        o += h_vec[l];
+    }
+    return v;
+}
+
+// least_squares.cpp:131-190 SolveLeastSquaresSampleLargeRootFixed (and its WithB0 twin,
+// :192-250; the LAPACK variant :567-665 fills the same system): row 0 of the system is the
+// root (norm0[cid], G0S(cid, .), b0 = <C0[:,cid], x>), rows 1..m-1 the small layers.
+bool SolveLsSampleLargeRoot(const LrView& v, int64_t i, float b0, const u8* bs, float* a_out, float* A, float* b,
+                            float* x, float* y) {
+    const int m = v.m;
+    const bool lapack_test = !(m == 5 || m == 10);
+    const uint32_t c = v.cid[i];
+    const float* xCi = v.XCol(i);
+    auto fill = [&](float lambda) {
+        std::fill(A, A + m * m, 0.0f);
+        b[0] = b0;
+        A[0] = v.norm0[c] + lambda;
+        for (int j = 1; j < m; ++j) {
+            const int fj = v.soff[j] + bs[j - 1];
+            b[j] = xCi[fj];
+            A[j] = v.G0SAt(c, fj);
+            for (int k = 1; k <= j; ++k) A[k * m + j] = v.GsAt(v.soff[k] + bs[k - 1], fj);
+            A[j * m + j] += lambda;
+        }
+    };
+    fill(0.0f);
+    bool ok = CholUpper(A, m, lapack_test);
+    if (!ok) {
+        float bump = kEps;
+        for (int attempt = 0; attempt < 3 && !ok; ++attempt) {
+            fill(bump);
+            ok = CholUpper(A, m, lapack_test);
+            bump *= 10.0f;
+        }
+    }
+    if (!ok) return false;
+    SolveUpper(A, m, m, b, x, y);
+    std::copy(x, x + m, a_out);
+    return true;
+}
+
+// cost_utils.cpp:42-84 SampleCostLargeRootFixed (the generic :160-209 has the same order):
+// nx2 - 2*(a0*<c0,x> + sum_l a_l xC_l) + (a0*a0*norm0 + sum_j (2*a0*a_j*G0S + sum_k a_j a_k G)).
+float SampleCostLargeRoot(const LrView& v, int64_t i, float xc0, const u8* bs, const float* a, float nx2) {
+    const int m = v.m;
+    const uint32_t c = v.cid[i];
+    const float* xCi = v.XCol(i);
+    float term1 = a[0] * xc0;
+    for (int l = 1; l < m; ++l) term1 += a[l] * xCi[v.soff[l] + bs[l - 1]];
+    float term2 = 0.0f;
+    term2 += a[0] * a[0] * v.norm0[c];
+    for (int j = 1; j < m; ++j) {
+        const float aj = a[j];
+        const int fj = v.soff[j] + bs[j - 1];
+        term2 += 2.0f * a[0] * aj * v.G0SAt(c, fj);
+        for (int k = 1; k < m; ++k) term2 += aj * a[k] * v.GsAt(fj, v.soff[k] + bs[k - 1]);
+    }
+    return nx2 - 2.0f * term1 + term2;
+}
+
+int64_t LsAllLargeRoot(const LrView& v, const u8* Bs, int64_t n, float* a) {
+    const int m = v.m, mb = std::max(m - 1, 0);
+    int64_t fails = 0;
+    #pragma omp parallel reduction(+ : fails)
+    {
+        std::vector<float> A(static_cast<std::size_t>(m) * m), b(m), x(m), y(m);
+        #pragma omp for schedule(static)
+        for (int64_t i = 0; i < n; ++i) {
+            float* ai = a + static_cast<std::size_t>(i) * m;
+            if (!SolveLsSampleLargeRoot(v, i, v.RootDot(i), Bs + static_cast<std::size_t>(i) * mb, ai, A.data(),
+                                        b.data(), x.data(), y.data())) {
+                std::fill(ai, ai + m, 0.0f);  // least_squares.cpp:690-694
+                ++fails;
+            }
+        }
+    }
+    return fails;
+}
+
+void CostsLargeRoot(const LrView& v, const u8* Bs, const float* a, const float* nx2, int64_t n, float* cost) {
+    const int m = v.m, mb = std::max(m - 1, 0);
+    #pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; ++i)
+        cost[i] = SampleCostLargeRoot(v, i, v.RootDot(i), Bs + static_cast<std::size_t>(i) * mb,
+                                      a + static_cast<std::size_t>(i) * m, nx2[i]);
+}
+
+// RunIcmLargeRoot (icm.cpp:347-870) with the sweep orders given: LS refit and costs, then
+// icm_iters sweeps over layers 1..m-1 of the active vectors. The score of code t of layer j is
+// (xC_small(t) - a0*G0S(cid, t) - sum_{l>=1, l!=j} a_l G_small(t, flat_l)) * invnorm_small(t),
+// subtractions in that order (:437-503); b0 is cached once per vector (:381-389).
+int64_t RunIcmLargeRootOrders(const LrView& v, const float* invs, const float* nx2, int64_t n, int icm_iters,
+                              int use_abs, const int* orders, u8* Bs, float* a, float* cost) {
+    const int m = v.m, mb = std::max(m - 1, 0);
+    int64_t ls_fail = LsAllLargeRoot(v, Bs, n, a);
+    CostsLargeRoot(v, Bs, a, nx2, n, cost);
+    std::vector<float> b0(static_cast<std::size_t>(n));
+    for (int64_t i = 0; i < n; ++i) b0[i] = v.RootDot(i);
+    std::vector<u8> active(static_cast<std::size_t>(n), 1), changed(static_cast<std::size_t>(n), 0);
+    int max_h = 0;
+    for (int l = 0; l < m; ++l) max_h = std::max(max_h, v.h_vec[l]);
+    for (int it = 0; it < icm_iters; ++it) {
+        std::fill(changed.begin(), changed.end(), 0);
+        for (int oi = 0; oi < m; ++oi) {
+            const int j = orders[static_cast<std::size_t>(it) * m + oi];
+            if (j == 0) continue;
+            const int startf = v.soff[j];
+            const int hj = v.h_vec[j];
+            if (hj <= 1) continue;
+            #pragma omp parallel reduction(+ : ls_fail)
+            {
+                std::vector<float> tmp(max_h), backup(m), A(static_cast<std::size_t>(m) * m), b(m), x(m), y(m);
+                #pragma omp for schedule(static)
+                for (int64_t i = 0; i < n; ++i) {
+                    if (!active[i]) continue;
+                    u8* bi = Bs + static_cast<std::size_t>(i) * mb;
+                    float* ai = a + static_cast<std::size_t>(i) * m;
+                    const float* xCi = v.XCol(i);
+                    const uint32_t c = v.cid[i];
+                    const int old_code = bi[j - 1];
+                    for (int t = 0; t < hj; ++t) tmp[t] = xCi[startf + t];
+                    const float a0 = ai[0];
+                    for (int t = 0; t < hj; ++t) tmp[t] -= a0 * v.G0SAt(c, startf + t);
+                    for (int l = 1; l < m; ++l) {
+                        if (l == j) continue;
+                        const float al = ai[l];
+                        const int fl = v.soff[l] + bi[l - 1];
+                        for (int t = 0; t < hj; ++t) tmp[t] -= al * v.GsAt(startf + t, fl);
+                    }
+                    int best_code = old_code;
+                    float best_score = -kInf;
+                    for (int t = 0; t < hj; ++t) {
+                        const float val = tmp[t] * invs[startf + t];
+                        const float score = use_abs ? std::fabs(val) : val;
+                        if (score > best_score) {
+                            best_score = score;
+                            best_code = t;
+                        }
+                    }
+                    if (best_code == old_code) continue;
+                    std::copy(ai, ai + m, backup.begin());
+                    bi[j - 1] = static_cast<u8>(best_code);
+                    if (!SolveLsSampleLargeRoot(v, i, b0[i], bi, ai, A.data(), b.data(), x.data(), y.data())) {
+                        bi[j - 1] = static_cast<u8>(old_code);
+                        std::copy(backup.begin(), backup.end(), ai);
+                        ++ls_fail;
+                        continue;
+                    }
+                    const float new_cost = SampleCostLargeRoot(v, i, v.RootDot(i), bi, ai, nx2[i]);
+                    if (new_cost + kEps < cost[i]) {  // icm.cpp:522-531, :601-611
+                        cost[i] = new_cost;
+                        changed[i] = 1;
+                    } else {
+                        bi[j - 1] = static_cast<u8>(old_code);
+                        std::copy(backup.begin(), backup.end(), ai);
+                    }
+                }
+            }
+        }
+        for (int64_t i = 0; i < n; ++i) {
+            if (active[i] && !changed[i]) active[i] = 0;
+        }
+    }
+    return ls_fail;
+}
+
+}  // namespace
+
+extern "C" {
+
+void orc_invnorm_small(const float* C_small, int d, int Hs, float* out) {
+    for (int f = 0; f < Hs; ++f) {
+        const float n2 = SimdLane4SumSq(C_small + static_cast<std::size_t>(f) * d, d);
+        out[f] = n2 > 0.0f ? 1.0f / std::sqrt(n2) : 0.0f;
+    }
+}
+
+int64_t orc_solve_ls_all_large_root(const float* X, int d, const float* C0, const float* norm0, int h0,
+                                    const float* xC_small, const float* G_small, const float* G0S, int Hs, int m,
+                                    const int* h_vec, const uint32_t* cluster_id, const uint8_t* B_small, int64_t n,
+                                    float* a, int nthreads) {
+    SetThreads(nthreads);
+    const LrView v = MakeLrView(X, d, C0, norm0, h0, xC_small, G_small, G0S, Hs, m, h_vec, cluster_id);
+    return LsAllLargeRoot(v, B_small, n, a);
+}
+
+void orc_compute_costs_large_root(const float* X, int d, const float* C0, const float* norm0, int h0,
+                                  const float* xC_small, const float* G_small, const float* G0S, int Hs, int m,
+                                  const int* h_vec, const uint32_t* cluster_id, const uint8_t* B_small,
+                                  const float* a, const float* nx2, int64_t n, float* cost, int nthreads) {
+    SetThreads(nthreads);
+    const LrView v = MakeLrView(X, d, C0, norm0, h0, xC_small, G_small, G0S, Hs, m, h_vec, cluster_id);
+    CostsLargeRoot(v, B_small, a, nx2, n, cost);
+}
+
+int64_t orc_icm_ils_large_root(const float* X, int d, const float* C0, const float* norm0, int h0,
+                               const float* xC_small, const float* G_small, const float* G0S,
+                               const float* invnorm_small, int Hs, int m, const int* h_vec,
+                               const uint32_t* cluster_id, const float* nx2, int64_t n, int icm_iters, int ils_iters,
+                               int perturb_k, int use_abs, uint32_t seed, uint64_t sample_id_offset,
+                               uint8_t* B_small, float* a, float* cost, int nthreads) {
+    SetThreads(nthreads);
+    const LrView v = MakeLrView(X, d, C0, norm0, h0, xC_small, G_small, G0S, Hs, m, h_vec, cluster_id);
+    // DynamicIcmWithIlsLargeRootImpl (icm.cpp:1005-1120)
+    std::mt19937 rng(static_cast<std::mt19937::result_type>(seed));
+    std::vector<int> ord = NextOrders(rng, m, std::max(0, icm_iters));
+    int64_t fails = RunIcmLargeRootOrders(v, invnorm_small, nx2, n, icm_iters, use_abs, ord.data(), B_small, a, cost);
+    if (ils_iters <= 0 || perturb_k <= 0 || m <= 1) return fails;
+    const int mb = m - 1;
+    const int ksel = std::min(perturb_k, m);
+    std::vector<uint8_t> Bc(static_cast<std::size_t>(n) * mb);
+    std::vector<float> ac(static_cast<std::size_t>(n) * m), cc(static_cast<std::size_t>(n));
+    for (int outer = 0; outer < ils_iters; ++outer) {
+        std::memcpy(Bc.data(), B_small, Bc.size());
+        #pragma omp parallel for schedule(static)
+        for (int64_t i = 0; i < n; ++i) {  // icm.cpp:1079-1098
+            const uint64_t ig = sample_id_offset + static_cast<uint64_t>(i);
+            SplitMix64 r{static_cast<uint64_t>(seed) ^ (static_cast<uint64_t>(outer + 1) * 0x9e3779b97f4a7c15ULL) ^
+                         ((ig + 1) * 0xbf58476d1ce4e5b9ULL)};
+            uint8_t* bi = Bc.data() + static_cast<std::size_t>(i) * mb;
+            for (int k = 0; k < ksel; ++k) {
+                const int layer = 1 + static_cast<int>(UniformBelow(r, static_cast<uint32_t>(mb)));
+                const int h = h_vec[layer];
+                if (h <= 1) continue;
+                const int old = bi[layer - 1];
+                const int raw = static_cast<int>(UniformBelow(r, static_cast<uint32_t>(h - 1)));
+                bi[layer - 1] = static_cast<uint8_t>(raw >= old ? raw + 1 : raw);
+            }
+        }
+        ord = NextOrders(rng, m, std::max(0, icm_iters));
+        fails += RunIcmLargeRootOrders(v, invnorm_small, nx2, n, icm_iters, use_abs, ord.data(), Bc.data(),
+                                       ac.data(), cc.data());
+        #pragma omp parallel for schedule(static)
+        for (int64_t i = 0; i < n; ++i) {  // icm.cpp:1104-1116
+            if (cc[i] + kEps < cost[i]) {
+                std::memcpy(B_small + static_cast<std::size_t>(i) * mb, Bc.data() + static_cast<std::size_t>(i) * mb,
+                            mb);
+                std::memcpy(a + static_cast<std::size_t>(i) * m, ac.data() + static_cast<std::size_t>(i) * m,
+                            sizeof(float) * m);
+                cost[i] = cc[i];
+            }
+        }
+    }
+    return fails;
+}
+
+}  // extern "C"

@@ -112,6 +112,36 @@ int orc_large_root_candidates(const float* X, int d, const float* nx2, const flo
                               const uint32_t* forced_root, int root_mode, float* root_errs,
                               int* root_codes, float* root_a0, float* root_r00, int nthreads);
 
+/* precomp_large_root.cpp:101-114: invnorm_small_flat = 1/sqrt(Norm2(c)) (0 for a zero codeword),
+ * Norm2 in the OpenMP-simd order of ||x||^2. */
+void orc_invnorm_small(const float* C_small, int d, int Hs, float* out);
+
+/* Large root (layer 0 = the vector's root cluster_id[i], layers 1..m-1 = B_small, (m-1) x n).
+ * G_small Hs x Hs and G0S h0 x Hs as in orc_build_precomp_large_root; xC_small Hs x n.
+ * b0 = <C0[:,cid], x> is the reference's omp-simd dot (same four-lane order as ||x||^2). */
+
+/* least_squares.cpp:667-745 SolveLeastSquaresAllLargeRoot. Returns the failure count. */
+int64_t orc_solve_ls_all_large_root(const float* X, int d, const float* C0, const float* norm0, int h0,
+                                    const float* xC_small, const float* G_small, const float* G0S, int Hs, int m,
+                                    const int* h_vec, const uint32_t* cluster_id, const uint8_t* B_small, int64_t n,
+                                    float* a, int nthreads);
+
+/* cost_utils.cpp:42-84, :160-233 ComputeCostsLargeRoot. */
+void orc_compute_costs_large_root(const float* X, int d, const float* C0, const float* norm0, int h0,
+                                  const float* xC_small, const float* G_small, const float* G0S, int Hs, int m,
+                                  const int* h_vec, const uint32_t* cluster_id, const uint8_t* B_small,
+                                  const float* a, const float* nx2, int64_t n, float* cost, int nthreads);
+
+/* icm.cpp:347-870 RunIcmLargeRoot + :1005-1120 DynamicIcmWithIlsLargeRootImpl: LS refit, costs,
+ * icm_iters sweeps over layers 1..m-1 (the root stays), then ils_iters perturb + ICM + accept
+ * rounds. B_small is updated in place; a (m x n) and cost (n) are outputs. */
+int64_t orc_icm_ils_large_root(const float* X, int d, const float* C0, const float* norm0, int h0,
+                               const float* xC_small, const float* G_small, const float* G0S,
+                               const float* invnorm_small, int Hs, int m, const int* h_vec,
+                               const uint32_t* cluster_id, const float* nx2, int64_t n, int icm_iters, int ils_iters,
+                               int perturb_k, int use_abs, uint32_t seed, uint64_t sample_id_offset,
+                               uint8_t* B_small, float* a, float* cost, int nthreads);
+
 #ifdef __cplusplus
 }
 #endif

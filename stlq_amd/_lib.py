@@ -110,6 +110,10 @@ SIGNATURES = {
     "stlq_mi355_last_timings": ([_vp, ctypes.POINTER(Timings)], _int),
     "stlq_mi355_set_large_root": ([_vp, _int, _int, _i32p, _f32p, _f32p], _int),
     "stlq_mi355_beam_search_large_root": ([_vp, _f32p, _f32p, _i64, _int, _u32p, _int, _u32p, _u8p, _f32p], _int),
+    "stlq_mi355_solve_ls_all_large_root": ([_vp, _f32p, _f32p, _i64, _u32p, _u8p, _f32p, _i64p], _int),
+    "stlq_mi355_compute_costs_large_root": ([_vp, _f32p, _f32p, _i64, _u32p, _u8p, _f32p, _f32p, _f32p], _int),
+    "stlq_mi355_icm_ils_large_root": ([_vp, _f32p, _f32p, _f32p, _i64, _u32p, _int, _int, _int, _int, ctypes.c_uint32,
+                                       ctypes.c_uint64, _u8p, _f32p, _f32p], _int),
     "stlq_mi355_dev_alloc": ([_vp, ctypes.c_size_t, ctypes.POINTER(_vp)], _int),
     "stlq_mi355_dev_free": ([_vp, _vp], _int),
     "stlq_mi355_copy_h2d": ([_vp, _vp, _vp, ctypes.c_size_t], _int),

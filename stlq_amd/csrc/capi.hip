@@ -101,10 +101,10 @@ struct stlq_mi355_ctx {
     bool has_lr = false;
     int lr_d = 0, lr_m = 0, h0 = 0, Hs = 0;
     int lr_h[kMaxM] = {}, soff[kMaxM] = {};
-    DevBuf C0, Cs, norm0, G_small, G0S, gdiag_small;
+    DevBuf C0, Cs, norm0, G_small, G0S, gdiag_small, invnorm_small;
 
     // Work buffers (grown on demand, reused across calls).
-    DevBuf X, nx2, xC, xC_in, codes, a, cost, best, fails, active, changed, mse, gam0, roots, scores;
+    DevBuf X, nx2, xC, xC_in, codes, a, cost, best, fails, active, changed, mse, gam0, roots, scores, b0;
     DevBuf ils_codes, ils_a, ils_cost;  // ILS candidate state
     DevBuf st_rec[2], st_curH[2];
 
@@ -253,7 +253,53 @@ LsArgs MakeLs(stlq_mi355_ctx* c, const float* dxC, int64_t ldx, const uint8_t* d
     p.cost = dcost;
     p.fails = c->fails.as<int>();
     p.n = n;
+    p.cstride = c->m;
     return p;
+}
+
+// What one ICM / ILS run works on: the full precomp (G, invnorm, m codes per vector), or a large
+// root (the small layers' G and invnorm, the roots' G0S rows and b0, m-1 codes per vector).
+struct IcmProblem {
+    LsArgs ls;  // all but codes, a and cost
+    const float* G_cm = nullptr;
+    const float* invnorm = nullptr;
+    const int* h_vec = nullptr;  // host, m entries
+    int lfirst = 0;              // layer of the first stored code
+};
+
+IcmProblem FullProblem(stlq_mi355_ctx* c, const float* dxC, int64_t ldx, const float* dnx2, int64_t n) {
+    IcmProblem P;
+    P.ls = MakeLs(c, dxC, ldx, nullptr, nullptr, dnx2, nullptr, n);
+    P.G_cm = c->G_cm.as<float>();
+    P.invnorm = c->invnorm.as<float>();
+    P.h_vec = c->h_vec;
+    return P;
+}
+
+// droot/db0: per-vector root ids and <C0[:,root], x> on the device; dxs: xC_small (Hs per vector).
+IcmProblem LargeRootProblem(stlq_mi355_ctx* c, const float* dxs, const float* dnx2, const uint32_t* droot,
+                            const float* db0, int64_t n) {
+    IcmProblem P;
+    LsArgs& p = P.ls;
+    p.xC = dxs;
+    p.ldx = c->Hs;
+    p.G_rm = c->G_small.as<float>();
+    p.H = c->Hs;
+    p.m = c->lr_m;
+    for (int l = 0; l < c->lr_m; ++l) p.off[l] = c->soff[l];
+    p.nx2 = dnx2;
+    p.fails = c->fails.as<int>();
+    p.n = n;
+    p.cstride = c->lr_m - 1;
+    p.root = droot;
+    p.b0 = db0;
+    p.norm0 = c->norm0.as<float>();
+    p.G0S_rm = c->G0S.as<float>();
+    P.G_cm = c->G_small.as<float>();  // symmetric: its rows are its columns
+    P.invnorm = c->invnorm_small.as<float>();
+    P.h_vec = c->lr_h;
+    P.lfirst = 1;
+    return P;
 }
 
 std::vector<int> IcmOrders(int m, int iters, uint32_t seed) {
@@ -269,12 +315,16 @@ std::vector<int> IcmOrders(int m, int iters, uint32_t seed) {
     return all;
 }
 
-// RunIcm (icm.cpp:89-344) on one tile: LS refit + costs, then icm_iters sweeps.
-// RunIcm (icm.cpp:89-344) with the layer order of every sweep given (iters x m).
-int RunIcmOrders(stlq_mi355_ctx* c, const float* dxC, int64_t ldx, const float* dnx2, int64_t n, int iters,
-                 int use_abs, const std::vector<int>& orders, uint8_t* dcodes, float* da, float* dcost,
-                 hipStream_t s) {
-    LsArgs ls = MakeLs(c, dxC, ldx, dcodes, da, dnx2, dcost, n);
+// RunIcm (icm.cpp:89-344) / RunIcmLargeRoot (:347-870) on one tile: LS refit + costs, then
+// `iters` sweeps with the layer order of every sweep given (iters x m).
+int RunIcmOrders(stlq_mi355_ctx* c, const IcmProblem& P, int iters, int use_abs, const std::vector<int>& orders,
+                 uint8_t* dcodes, float* da, float* dcost, hipStream_t s) {
+    LsArgs ls = P.ls;
+    ls.codes = dcodes;
+    ls.a = da;
+    ls.cost = dcost;
+    const int64_t n = ls.n;
+    const int m = ls.m;
     HIP_TRY(LaunchLsAll(ls, s));
     HIP_TRY(LaunchCosts(ls, s));
     if (iters <= 0) return STLQ_MI355_OK;
@@ -284,20 +334,20 @@ int RunIcmOrders(stlq_mi355_ctx* c, const float* dxC, int64_t ldx, const float* 
     IcmArgs q;
     q.ls = ls;
     q.codes_rw = dcodes;
-    q.G_cm = c->G_cm.as<float>();
-    q.invnorm = c->invnorm.as<float>();
+    q.G_cm = P.G_cm;
+    q.invnorm = P.invnorm;
     q.active = c->active.as<uint8_t>();
     q.changed = c->changed.as<uint8_t>();
     q.fails = c->fails.as<int>();
     q.use_abs = use_abs ? 1 : 0;
     for (int it = 0; it < iters; ++it) {
         HIP_TRY(LaunchFill8(q.changed, 0, n, s));
-        for (int oi = 0; oi < c->m; ++oi) {
-            const int j = orders[static_cast<size_t>(it) * c->m + oi];
-            if (j == 0) continue;                 // icm.cpp:250: layer 0 frozen
-            if (c->h_vec[j] <= 1) continue;        // icm.cpp:255
+        for (int oi = 0; oi < m; ++oi) {
+            const int j = orders[static_cast<size_t>(it) * m + oi];
+            if (j == 0) continue;             // icm.cpp:250: layer 0 frozen (the root, for a large root)
+            if (P.h_vec[j] <= 1) continue;    // icm.cpp:255
             q.j = j;
-            q.hj = c->h_vec[j];
+            q.hj = P.h_vec[j];
             HIP_TRY(LaunchIcmLayer(q, s));
         }
         HIP_TRY(LaunchIcmDeactivate(q.active, q.changed, n, s));
@@ -305,21 +355,22 @@ int RunIcmOrders(stlq_mi355_ctx* c, const float* dxC, int64_t ldx, const float* 
     return STLQ_MI355_OK;
 }
 
-int RunIcm(stlq_mi355_ctx* c, const float* dxC, int64_t ldx, const float* dnx2, int64_t n, int iters,
-           int use_abs, uint32_t seed, uint8_t* dcodes, float* da, float* dcost, hipStream_t s) {
-    return RunIcmOrders(c, dxC, ldx, dnx2, n, iters, use_abs, IcmOrders(c->m, iters, seed), dcodes, da, dcost, s);
+int RunIcm(stlq_mi355_ctx* c, const IcmProblem& P, int iters, int use_abs, uint32_t seed, uint8_t* dcodes, float* da,
+           float* dcost, hipStream_t s) {
+    return RunIcmOrders(c, P, iters, use_abs, IcmOrders(P.ls.m, iters, seed), dcodes, da, dcost, s);
 }
 
-// DynamicIcmWithIls{Abs,NoAbs}NoNormal (icm.cpp:872-1003): RunIcm, then ils_iters rounds of
-// perturb (PerturbKernel) -> RunIcm on the candidate codes -> accept-if-better. One
-// std::mt19937(seed) stream supplies every RunIcm's layer orders, each RunIcm starting from the
-// identity order (icm.cpp:121-137). id0 is the global id of vector 0 (the reference's
-// sample_id_offset), so a tile of a larger set perturbs exactly as the whole set would.
-int RunIcmIls(stlq_mi355_ctx* c, const float* dxC, int64_t ldx, const float* dnx2, int64_t n, int icm_iters,
-              int ils_iters, int perturb_k, int use_abs, uint32_t seed, uint64_t id0, uint8_t* dcodes, float* da,
-              float* dcost, hipStream_t s) {
+// DynamicIcmWithIls{Abs,NoAbs}NoNormal[LargeRoot] (icm.cpp:872-1003, :1005-1120): RunIcm, then
+// ils_iters rounds of perturb (PerturbKernel) -> RunIcm on the candidate codes ->
+// accept-if-better. One std::mt19937(seed) stream supplies every RunIcm's layer orders, each
+// RunIcm starting from the identity order (icm.cpp:121-137). id0 is the global id of vector 0
+// (the reference's sample_id_offset), so a tile of a larger set perturbs exactly as the whole set
+// would.
+int RunIcmIls(stlq_mi355_ctx* c, const IcmProblem& P, int icm_iters, int ils_iters, int perturb_k, int use_abs,
+              uint32_t seed, uint64_t id0, uint8_t* dcodes, float* da, float* dcost, hipStream_t s) {
     std::mt19937 rng(static_cast<std::mt19937::result_type>(seed));
-    const int m = c->m;
+    const int m = P.ls.m;
+    const int64_t n = P.ls.n;
     auto next_orders = [&]() {
         std::vector<int> order(static_cast<size_t>(m)), out;
         std::iota(order.begin(), order.end(), 0);
@@ -329,20 +380,21 @@ int RunIcmIls(stlq_mi355_ctx* c, const float* dxC, int64_t ldx, const float* dnx
         }
         return out;
     };
-    RC_TRY(RunIcmOrders(c, dxC, ldx, dnx2, n, icm_iters, use_abs, next_orders(), dcodes, da, dcost, s));
+    RC_TRY(RunIcmOrders(c, P, icm_iters, use_abs, next_orders(), dcodes, da, dcost, s));
     if (ils_iters <= 0 || perturb_k <= 0 || m <= 1) return STLQ_MI355_OK;
+    const size_t ncodes = static_cast<size_t>(n) * static_cast<size_t>(P.ls.cstride);
     const size_t nm = static_cast<size_t>(n) * static_cast<size_t>(m);
-    HIP_TRY(c->ils_codes.Ensure(nm));
+    HIP_TRY(c->ils_codes.Ensure(ncodes));
     HIP_TRY(c->ils_a.Ensure(nm * 4));
     HIP_TRY(c->ils_cost.Ensure(static_cast<size_t>(n) * 4));
     uint8_t* cc = c->ils_codes.as<uint8_t>();
     float* ca = c->ils_a.as<float>();
     float* ccost = c->ils_cost.as<float>();
     for (int outer = 0; outer < ils_iters; ++outer) {
-        HIP_TRY(hipMemcpyAsync(cc, dcodes, nm, hipMemcpyDeviceToDevice, s));
-        HIP_TRY(LaunchPerturb(cc, n, m, c->h_vec, perturb_k, seed, outer, id0, s));
-        RC_TRY(RunIcmOrders(c, dxC, ldx, dnx2, n, icm_iters, use_abs, next_orders(), cc, ca, ccost, s));
-        HIP_TRY(LaunchIlsAccept(dcodes, da, dcost, cc, ca, ccost, n, m, s));
+        HIP_TRY(hipMemcpyAsync(cc, dcodes, ncodes, hipMemcpyDeviceToDevice, s));
+        HIP_TRY(LaunchPerturb(cc, n, m, P.ls.cstride, P.lfirst, P.h_vec, perturb_k, seed, outer, id0, s));
+        RC_TRY(RunIcmOrders(c, P, icm_iters, use_abs, next_orders(), cc, ca, ccost, s));
+        HIP_TRY(LaunchIlsAccept(dcodes, da, dcost, cc, ca, ccost, n, m, P.ls.cstride, s));
     }
     return STLQ_MI355_OK;
 }
@@ -379,13 +431,16 @@ int BeamAndRefit(stlq_mi355_ctx* c, const float* dxC, const float* dnx2, int64_t
             HIP_TRY(c->cost.Ensure(static_cast<size_t>(n) * 4));
             dcost = c->cost.as<float>();
         }
-        LsArgs ls = MakeLs(c, dxC, c->H, o.codes, da, dnx2, dcost, n);
-        HIP_TRY(LaunchLsAll(ls, s));
-        HIP_TRY(LaunchCosts(ls, s));
+        if (!refine) {  // with refinement, RunIcm starts with this same refit
+            LsArgs ls = MakeLs(c, dxC, c->H, o.codes, da, dnx2, dcost, n);
+            HIP_TRY(LaunchLsAll(ls, s));
+            HIP_TRY(LaunchCosts(ls, s));
+        }
     }
     HIP_TRY(rec(4));
     if (refine) {
-        RC_TRY(RunIcmIls(c, dxC, c->H, dnx2, n, P.icm_iters, P.ils_iters, P.perturb_k, P.use_abs, P.seed, id0,
+        RC_TRY(RunIcmIls(c, FullProblem(c, dxC, c->H, dnx2, n), P.icm_iters, P.ils_iters, P.perturb_k, P.use_abs,
+                         P.seed, id0,
                          o.codes, da, dcost, s));
     }
     HIP_TRY(rec(5));
@@ -544,7 +599,7 @@ int stlq_mi355_ctx_destroy(stlq_mi355_ctx* c) {
     DevBuf* bufs[] = {&c->C_all, &c->G_rm, &c->G_cm, &c->gdiag, &c->invnorm, &c->C0, &c->Cs, &c->norm0,
                       &c->G_small, &c->G0S, &c->gdiag_small, &c->X, &c->nx2, &c->xC, &c->xC_in, &c->codes, &c->a,
                       &c->cost, &c->best, &c->fails, &c->active, &c->changed, &c->mse, &c->gam0, &c->roots,
-                      &c->scores, &c->ils_codes, &c->ils_a, &c->ils_cost};
+                      &c->scores, &c->ils_codes, &c->ils_a, &c->ils_cost, &c->b0, &c->invnorm_small};
     if (c->g_shared) c->G_cm.p = nullptr;
     for (DevBuf* b : bufs) b->Release();
     for (int b = 0; b < 2; ++b) {
@@ -785,7 +840,7 @@ int stlq_mi355_icm(stlq_mi355_ctx* c, const float* X, const float* nx2, const fl
     te.n = n;
     te.e[0] = te.e[1] = te.e[2] = te.e[3] = te.e[4] = c->NextEvent();
     HIP_TRY(hipEventRecord(te.e[0], c->stream));
-    RC_TRY(RunIcm(c, c->xC.as<float>(), c->H, c->nx2.as<float>(), n, icm_iters, use_abs, seed,
+    RC_TRY(RunIcm(c, FullProblem(c, c->xC.as<float>(), c->H, c->nx2.as<float>(), n), icm_iters, use_abs, seed,
                   c->codes.as<uint8_t>(), c->a.as<float>(), c->cost.as<float>(), c->stream));
     te.e[5] = te.e[6] = c->NextEvent();
     HIP_TRY(hipEventRecord(te.e[5], c->stream));
@@ -828,7 +883,8 @@ int stlq_mi355_icm_ils(stlq_mi355_ctx* c, const float* X, const float* nx2, cons
     te.n = n;
     te.e[0] = te.e[1] = te.e[2] = te.e[3] = te.e[4] = c->NextEvent();
     HIP_TRY(hipEventRecord(te.e[0], c->stream));
-    RC_TRY(RunIcmIls(c, c->xC.as<float>(), c->H, c->nx2.as<float>(), n, icm_iters, ils_iters, perturb_k, use_abs,
+    RC_TRY(RunIcmIls(c, FullProblem(c, c->xC.as<float>(), c->H, c->nx2.as<float>(), n), icm_iters, ils_iters,
+                     perturb_k, use_abs,
                      seed, sample_id_offset, c->codes.as<uint8_t>(), c->a.as<float>(), c->cost.as<float>(),
                      c->stream));
     te.e[5] = te.e[6] = c->NextEvent();
@@ -879,7 +935,8 @@ int stlq_mi355_encode(stlq_mi355_ctx* c, const float* X, int64_t n, const stlq_m
                                    c->stream));
             HIP_TRY(hipStreamSynchronize(c->stream));
             beam_sum += Mean(beam_cost) * static_cast<double>(nt);
-            RC_TRY(RunIcmIls(c, c->xC.as<float>(), c->H, c->nx2.as<float>(), nt, P.icm_iters, P.ils_iters,
+            RC_TRY(RunIcmIls(c, FullProblem(c, c->xC.as<float>(), c->H, c->nx2.as<float>(), nt), P.icm_iters,
+                             P.ils_iters,
                              P.perturb_k, P.use_abs, P.seed, static_cast<uint64_t>(t0), o.codes, o.a, o.cost,
                              c->stream));
         } else {
@@ -971,7 +1028,8 @@ int CheckLargeRoot(stlq_mi355_ctx* c, int H_beam, int root_mode);
 int64_t LargeRootTileVectors(stlq_mi355_ctx* c, int64_t n, int Hb, bool forced);
 int LargeRootTile(stlq_mi355_ctx* c, const float* dX, int64_t nt, int Hb, int root_mode, const uint32_t* d_forced,
                   const float* dxC_given, uint32_t* d_cluster, uint8_t* d_codes, float* d_best, hipStream_t s,
-                  TileEvents* te);
+                  TileEvents* te, const stlq_mi355_encode_params* refine = nullptr, float* d_a = nullptr,
+                  float* d_cost = nullptr, uint64_t id0 = 0);
 }  // namespace
 
 extern "C" {
@@ -987,6 +1045,7 @@ int stlq_mi355_encode_stream(stlq_mi355_ctx* c, int64_t n_total, int64_t chunk, 
     const bool lr = sp->large_root != 0;
     if (lr) {
         RC_TRY(CheckLargeRoot(c, sp->encode.H_beam, sp->root_mode));
+        RC_TRY(CheckParams(&sp->encode));
     } else {
         RC_TRY(CheckPre(c));
         RC_TRY(CheckParams(&sp->encode));
@@ -1002,7 +1061,7 @@ int stlq_mi355_encode_stream(stlq_mi355_ctx* c, int64_t n_total, int64_t chunk, 
     const size_t esz = sp->input_u8 ? 1 : 4;
     chunk = std::min(chunk, n_total);
     const size_t ch = static_cast<size_t>(chunk);
-    const bool want = !lr && (sp->encode.want_coeffs || sp->encode.icm_iters > 0 || sp->encode.ils_iters > 0);
+    const bool want = sp->encode.want_coeffs || sp->encode.icm_iters > 0 || sp->encode.ils_iters > 0;
     const size_t code_b = lr ? std::max<size_t>(m - 1, 1) : m;
     struct Slot {
         void* hin = nullptr;
@@ -1068,6 +1127,8 @@ int stlq_mi355_encode_stream(stlq_mi355_ctx* c, int64_t n_total, int64_t chunk, 
             out.cluster_id = sl.hcluster;
             out.B_small = m > 1 ? sl.hcodes : nullptr;
             out.best_err = sl.hbest;
+            out.a = want ? sl.ha : nullptr;
+            out.cost = want ? sl.hcost : nullptr;
         } else {
             out.codes = sl.hcodes;
             out.a = want ? sl.ha : nullptr;
@@ -1118,7 +1179,9 @@ int stlq_mi355_encode_stream(stlq_mi355_ctx* c, int64_t n_total, int64_t chunk, 
                 TileEvents te;
                 rc = LargeRootTile(c, dX + t0 * d, nt, Hb, sp->root_mode, nullptr, nullptr,
                                    sl.dcluster.as<uint32_t>() + t0, sl.dcodes.as<uint8_t>() + t0 * code_b,
-                                   sl.dbest.as<float>() + t0, c->stream, &te);
+                                   sl.dbest.as<float>() + t0, c->stream, &te, want ? &sp->encode : nullptr,
+                                   want ? sl.da.as<float>() + t0 * m : nullptr,
+                                   want ? sl.dcost.as<float>() + t0 : nullptr, static_cast<uint64_t>(sl.first + t0));
                 if (rc == STLQ_MI355_OK) c->tiles.push_back(te);
             } else {
                 EncodeOut o{sl.dcodes.as<uint8_t>() + t0 * m, want ? sl.da.as<float>() + t0 * m : nullptr,
@@ -1180,7 +1243,8 @@ int CheckLargeRoot(stlq_mi355_ctx* c, int H_beam, int root_mode) {
 int64_t LargeRootTileVectors(stlq_mi355_ctx* c, int64_t n, int Hb, bool forced) {
     const int m = c->lr_m;
     const int64_t per = 4LL * c->lr_d + 4 + 8LL * std::max(c->Hs, 1) + (forced ? 8 : 4LL * c->h0) +
-                        2 * (4LL * Hb * BeamRecordStride(m) + 4) + m + 16;
+                        2 * (4LL * Hb * BeamRecordStride(m) + 4) + m + 16 +
+                        (5LL * m + 16);  // refit: b0, ICM flags, ILS candidate codes/coefficients/cost
     int64_t t = std::max<int64_t>(EnvWorkspaceBytes() / per, 1024);
     return std::min<int64_t>(t, std::max<int64_t>(n, 1));
 }
@@ -1188,10 +1252,13 @@ int64_t LargeRootTileVectors(stlq_mi355_ctx* c, int64_t n, int Hb, bool forced) 
 // One tile of BeamSearchPrefixLSLargeRoot on device-resident fp32 X (nt x d): ||x||^2, xC_small
 // (MFMA GEMM unless given), root candidates (forced root, nearest root or top-H roots from the
 // MFMA score GEMM), then the expansion layers. Outputs cluster ids, B_small ((m-1) x nt) and the
-// selected errors, all device pointers.
+// selected errors, all device pointers. With `refine`, the streaming encode's refit follows
+// (encode_base_streaming.cpp:1117-1210): SolveLeastSquaresAllLargeRoot + ComputeCostsLargeRoot,
+// or DynamicIcmWithIls*NoNormalLargeRoot when ICM/ILS is asked for, into d_a / d_cost; id0 is
+// the global id of the tile's first vector.
 int LargeRootTile(stlq_mi355_ctx* c, const float* dX, int64_t nt, int Hb, int root_mode, const uint32_t* d_forced,
                   const float* dxC_given, uint32_t* d_cluster, uint8_t* d_codes, float* d_best, hipStream_t s,
-                  TileEvents* te) {
+                  TileEvents* te, const stlq_mi355_encode_params* refine, float* d_a, float* d_cost, uint64_t id0) {
     const int m = c->lr_m, Hs = c->Hs, h0 = c->h0, d = c->lr_d;
     HIP_TRY(c->nx2.Ensure(static_cast<size_t>(nt) * 4));
     HIP_TRY(c->xC.Ensure(static_cast<size_t>(nt) * std::max(Hs, 1) * 4));
@@ -1275,7 +1342,28 @@ int LargeRootTile(stlq_mi355_ctx* c, const float* dX, int64_t nt, int Hb, int ro
         }
     }
     HIP_TRY(rec(3));
-    if (te) te->e[4] = te->e[5] = te->e[6] = te->e[3];
+    if (!refine || !d_a || !d_cost) {
+        if (te) te->e[4] = te->e[5] = te->e[6] = te->e[3];
+        return STLQ_MI355_OK;
+    }
+    HIP_TRY(c->b0.Ensure(static_cast<size_t>(nt) * 4));
+    HIP_TRY(LaunchRootDot(dX, d, c->C0.as<float>(), d_cluster, nt, c->b0.as<float>(), s));
+    const IcmProblem P = LargeRootProblem(c, dxs, c->nx2.as<float>(), d_cluster, c->b0.as<float>(), nt);
+    const bool icm = refine->icm_iters > 0 || refine->ils_iters > 0;
+    if (!icm) {
+        LsArgs ls = P.ls;
+        ls.codes = d_codes;
+        ls.a = d_a;
+        ls.cost = d_cost;
+        HIP_TRY(LaunchLsAll(ls, s));
+        HIP_TRY(LaunchCosts(ls, s));
+    }
+    HIP_TRY(rec(4));
+    if (icm)
+        RC_TRY(RunIcmIls(c, P, refine->icm_iters, refine->ils_iters, refine->perturb_k, refine->use_abs, refine->seed,
+                         id0, d_codes, d_a, d_cost, s));
+    HIP_TRY(rec(5));
+    HIP_TRY(rec(6));
     return STLQ_MI355_OK;
 }
 
@@ -1308,6 +1396,7 @@ int stlq_mi355_set_large_root(stlq_mi355_ctx* c, int d, int m, const int* h_vec,
     HIP_TRY(c->G_small.Ensure(Hs * Hs * 4));
     HIP_TRY(c->G0S.Ensure(h0 * Hs * 4));
     HIP_TRY(c->gdiag_small.Ensure(Hs * 4));
+    HIP_TRY(c->invnorm_small.Ensure(Hs * 4));
     HIP_TRY(hipMemcpyAsync(c->C0.p, C0, h0 * d * 4, hipMemcpyHostToDevice, c->stream));
     HIP_TRY(LaunchNorms(c->C0.as<float>(), d, c->h0, true, c->norm0.as<float>(), nullptr, c->stream));
     if (c->Hs > 0) {
@@ -1315,6 +1404,8 @@ int stlq_mi355_set_large_root(stlq_mi355_ctx* c, int d, int m, const int* h_vec,
         HIP_TRY(LaunchGram(c->Cs.as<float>(), d, c->Hs, c->G_small.as<float>(), c->stream));
         HIP_TRY(LaunchCross(c->C0.as<float>(), c->h0, c->Cs.as<float>(), c->Hs, d, c->G0S.as<float>(), c->stream));
         HIP_TRY(LaunchDiag(c->G_small.as<float>(), c->Hs, c->gdiag_small.as<float>(), c->stream));
+        // precomp_large_root.cpp:101-114: invnorm_small_flat from the omp-simd Norm2
+        HIP_TRY(LaunchNorms(c->Cs.as<float>(), d, c->Hs, true, nullptr, c->invnorm_small.as<float>(), c->stream));
     }
     HIP_TRY(hipStreamSynchronize(c->stream));
     c->has_lr = true;
@@ -1368,6 +1459,139 @@ int stlq_mi355_beam_search_large_root(stlq_mi355_ctx* c, const float* X, const f
         HIP_TRY(hipStreamSynchronize(s));
     }
     return STLQ_MI355_OK;
+}
+
+}  // extern "C"
+
+namespace {
+
+enum class LrOp { kLs, kCosts, kIcm };
+
+struct LrIcm {
+    int icm_iters, ils_iters, perturb_k, use_abs;
+    uint32_t seed;
+    uint64_t id0;
+};
+
+// Host-buffer large-root refit, tiled over the workspace budget: per tile X, the roots and B_small
+// (and xC_small, ||x||^2 and a when given) go up, b0 = <C0[:,root], x> is formed on the device,
+// the op runs and its results come back. B_small is written only by kIcm.
+int LargeRootRefit(stlq_mi355_ctx* c, LrOp op, const float* X, const float* nx2, const float* xC_small, int64_t n,
+                   const uint32_t* cluster_id, uint8_t* B_small, const float* a_in, const LrIcm* ip, float* a_out,
+                   float* cost_out, int64_t* fail_count) {
+    RC_TRY(CheckLargeRoot(c, 1, 0));
+    const int m = c->lr_m, Hs = c->Hs, d = c->lr_d, mb = c->lr_m - 1;
+    if (n < 0 || (n > 0 && (!X || !cluster_id || (mb > 0 && !B_small)))) return Fail(STLQ_MI355_ERR_INVALID, "bad arguments");
+    if (fail_count) *fail_count = 0;
+    if (n == 0) return STLQ_MI355_OK;
+    for (int64_t i = 0; i < n; ++i) {
+        if (cluster_id[i] >= static_cast<uint32_t>(c->h0))
+            return Fail(STLQ_MI355_ERR_INVALID, "root " + std::to_string(cluster_id[i]) + " of vector " +
+                                                    std::to_string(i) + " >= h0");
+        for (int l = 0; l < mb; ++l)
+            if (B_small[i * mb + l] >= c->lr_h[l + 1])
+                return Fail(STLQ_MI355_ERR_INVALID, "code " + std::to_string(B_small[i * mb + l]) + " of vector " +
+                                                        std::to_string(i) + " exceeds layer " + std::to_string(l + 1) +
+                                                        " size " + std::to_string(c->lr_h[l + 1]));
+    }
+    c->ResetTimings();
+    const int64_t per = 4LL * d + 4LL * Hs + 16 + 2LL * mb + 12LL * m + 16;
+    const int64_t tile = std::min<int64_t>(std::max<int64_t>(EnvWorkspaceBytes() / per, 1024), n);
+    const size_t T = static_cast<size_t>(tile);
+    HIP_TRY(c->X.Ensure(T * d * 4));
+    HIP_TRY(c->xC.Ensure(T * std::max(Hs, 1) * 4));
+    HIP_TRY(c->roots.Ensure(T * 4));
+    HIP_TRY(c->codes.Ensure(T * std::max(mb, 1)));
+    HIP_TRY(c->a.Ensure(T * m * 4));
+    HIP_TRY(c->cost.Ensure(T * 4));
+    HIP_TRY(c->nx2.Ensure(T * 4));
+    HIP_TRY(c->b0.Ensure(T * 4));
+    hipStream_t s = c->stream;
+    HIP_TRY(LaunchFill8(c->fails.as<uint8_t>(), 0, 4, s));
+    for (int64_t t0 = 0; t0 < n; t0 += tile) {
+        const int64_t nt = std::min(tile, n - t0);
+        const size_t N = static_cast<size_t>(nt);
+        HIP_TRY(hipMemcpyAsync(c->X.p, X + t0 * d, N * d * 4, hipMemcpyHostToDevice, s));
+        HIP_TRY(hipMemcpyAsync(c->roots.p, cluster_id + t0, N * 4, hipMemcpyHostToDevice, s));
+        if (mb > 0) HIP_TRY(hipMemcpyAsync(c->codes.p, B_small + t0 * mb, N * mb, hipMemcpyHostToDevice, s));
+        if (xC_small) {
+            if (Hs > 0) HIP_TRY(hipMemcpyAsync(c->xC.p, xC_small + t0 * Hs, N * Hs * 4, hipMemcpyHostToDevice, s));
+        } else if (Hs > 0) {
+            HIP_TRY(LaunchGemmXc(c->X.as<float>(), nt, d, c->Cs.as<float>(), Hs, c->xC.as<float>(), Hs, s));
+        }
+        if (op != LrOp::kLs) {
+            if (nx2) {
+                HIP_TRY(hipMemcpyAsync(c->nx2.p, nx2 + t0, N * 4, hipMemcpyHostToDevice, s));
+            } else {
+                HIP_TRY(LaunchXNorm2(c->X.as<float>(), d, nt, c->nx2.as<float>(), s));
+            }
+        }
+        HIP_TRY(LaunchRootDot(c->X.as<float>(), d, c->C0.as<float>(), c->roots.as<uint32_t>(), nt, c->b0.as<float>(), s));
+        const IcmProblem P =
+            LargeRootProblem(c, c->xC.as<float>(), c->nx2.as<float>(), c->roots.as<uint32_t>(), c->b0.as<float>(), nt);
+        LsArgs ls = P.ls;
+        ls.codes = c->codes.as<uint8_t>();
+        ls.a = c->a.as<float>();
+        ls.cost = c->cost.as<float>();
+        if (op == LrOp::kLs) {
+            HIP_TRY(LaunchLsAll(ls, s));
+            HIP_TRY(hipMemcpyAsync(a_out + t0 * m, c->a.p, N * m * 4, hipMemcpyDeviceToHost, s));
+        } else if (op == LrOp::kCosts) {
+            HIP_TRY(hipMemcpyAsync(c->a.p, a_in + t0 * m, N * m * 4, hipMemcpyHostToDevice, s));
+            HIP_TRY(LaunchCosts(ls, s));
+            HIP_TRY(hipMemcpyAsync(cost_out + t0, c->cost.p, N * 4, hipMemcpyDeviceToHost, s));
+        } else {
+            TileEvents te;
+            te.n = nt;
+            te.e[0] = te.e[1] = te.e[2] = te.e[3] = te.e[4] = c->NextEvent();
+            HIP_TRY(hipEventRecord(te.e[0], s));
+            RC_TRY(RunIcmIls(c, P, ip->icm_iters, ip->ils_iters, ip->perturb_k, ip->use_abs, ip->seed,
+                             ip->id0 + static_cast<uint64_t>(t0), c->codes.as<uint8_t>(), ls.a, ls.cost, s));
+            te.e[5] = te.e[6] = c->NextEvent();
+            HIP_TRY(hipEventRecord(te.e[5], s));
+            c->tiles.push_back(te);
+            if (mb > 0) HIP_TRY(hipMemcpyAsync(B_small + t0 * mb, c->codes.p, N * mb, hipMemcpyDeviceToHost, s));
+            HIP_TRY(hipMemcpyAsync(a_out + t0 * m, c->a.p, N * m * 4, hipMemcpyDeviceToHost, s));
+            HIP_TRY(hipMemcpyAsync(cost_out + t0, c->cost.p, N * 4, hipMemcpyDeviceToHost, s));
+        }
+        HIP_TRY(hipStreamSynchronize(s));
+    }
+    int fails = 0;
+    HIP_TRY(hipMemcpyAsync(&fails, c->fails.p, 4, hipMemcpyDeviceToHost, s));
+    HIP_TRY(hipStreamSynchronize(s));
+    if (fail_count) *fail_count = fails;
+    return STLQ_MI355_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int stlq_mi355_solve_ls_all_large_root(stlq_mi355_ctx* c, const float* X, const float* xC_small, int64_t n,
+                                       const uint32_t* cluster_id, const uint8_t* B_small, float* a,
+                                       int64_t* fail_count) {
+    if (n > 0 && !a) return Fail(STLQ_MI355_ERR_INVALID, "a is null");
+    return LargeRootRefit(c, LrOp::kLs, X, nullptr, xC_small, n, cluster_id, const_cast<uint8_t*>(B_small), nullptr,
+                          nullptr, a, nullptr, fail_count);
+}
+
+int stlq_mi355_compute_costs_large_root(stlq_mi355_ctx* c, const float* X, const float* xC_small, int64_t n,
+                                        const uint32_t* cluster_id, const uint8_t* B_small, const float* a,
+                                        const float* nx2, float* cost) {
+    if (n > 0 && (!a || !cost)) return Fail(STLQ_MI355_ERR_INVALID, "bad arguments");
+    return LargeRootRefit(c, LrOp::kCosts, X, nx2, xC_small, n, cluster_id, const_cast<uint8_t*>(B_small), a,
+                          nullptr, nullptr, cost, nullptr);
+}
+
+int stlq_mi355_icm_ils_large_root(stlq_mi355_ctx* c, const float* X, const float* nx2, const float* xC_small,
+                                  int64_t n, const uint32_t* cluster_id, int icm_iters, int ils_iters, int perturb_k,
+                                  int use_abs, uint32_t seed, uint64_t sample_id_offset, uint8_t* B_small, float* a,
+                                  float* cost) {
+    if (n > 0 && (!a || !cost)) return Fail(STLQ_MI355_ERR_INVALID, "bad arguments");
+    if (icm_iters < 0 || ils_iters < 0 || perturb_k < 0)
+        return Fail(STLQ_MI355_ERR_INVALID, "icm_iters, ils_iters and perturb_k must be >= 0");
+    const LrIcm ip{icm_iters, ils_iters, perturb_k, use_abs, seed, sample_id_offset};
+    return LargeRootRefit(c, LrOp::kIcm, X, nx2, xC_small, n, cluster_id, B_small, nullptr, &ip, a, cost, nullptr);
 }
 
 }  // extern "C"

@@ -74,6 +74,8 @@ struct RootArgs {
 hipError_t LaunchGram(const float* C, int d, int H, float* G_rm, hipStream_t s);
 hipError_t LaunchCross(const float* C0, int h0, const float* Cs, int Hs, int d, float* G0S_rm, hipStream_t s);
 hipError_t LaunchNorms(const float* C, int d, int H, bool lane4, float* norm2, float* invnorm, hipStream_t s);
+hipError_t LaunchRootDot(const float* X, int d, const float* C0, const uint32_t* root, int64_t n, float* out,
+                         hipStream_t s);
 hipError_t LaunchDiag(const float* G_rm, int H, float* diag, hipStream_t s);
 hipError_t LaunchTranspose(const float* in, int rows, int cols, float* out, hipStream_t s);
 hipError_t LaunchXNorm2(const float* X, int d, int64_t n, float* out, hipStream_t s);
@@ -99,6 +101,14 @@ struct LsArgs {
     float* cost = nullptr;
     int* fails = nullptr;            // device counter
     int64_t n = 0;
+    int cstride = 0;                 // codes per vector: m, or m-1 for a large root
+    // Large root: layer 0 is the vector's root code root[i] from C0 (h0 codewords) and codes
+    // holds layers 1..m-1; H, G_rm, off and xC then describe the small layers. Null for the full
+    // precomp.
+    const uint32_t* root = nullptr;  // [n]
+    const float* b0 = nullptr;       // [n] <C0[:,root], x>
+    const float* norm0 = nullptr;    // [h0] ||C0[:,r]||^2
+    const float* G0S_rm = nullptr;   // [h0*H] row r: <C0[:,r], C_small[:,f]>
 };
 hipError_t LaunchLsAll(const LsArgs& a, hipStream_t s);
 hipError_t LaunchCosts(const LsArgs& a, hipStream_t s);
@@ -117,10 +127,11 @@ struct IcmArgs {
 };
 hipError_t LaunchIcmLayer(const IcmArgs& a, hipStream_t s);
 hipError_t LaunchIcmDeactivate(uint8_t* active, const uint8_t* changed, int64_t n, hipStream_t s);
-hipError_t LaunchPerturb(uint8_t* codes, int64_t n, int m, const int* h_vec, int perturb_k, uint32_t seed, int outer,
-                         uint64_t id0, hipStream_t s);
+// Codes are stored `cstride` per vector starting at layer `lfirst` (0, or 1 for a large root).
+hipError_t LaunchPerturb(uint8_t* codes, int64_t n, int m, int cstride, int lfirst, const int* h_vec, int perturb_k,
+                         uint32_t seed, int outer, uint64_t id0, hipStream_t s);
 hipError_t LaunchIlsAccept(uint8_t* codes, float* a, float* cost, const uint8_t* cc, const float* ca, const float* ccost,
-                           int64_t n, int m, hipStream_t s);
+                           int64_t n, int m, int cstride, hipStream_t s);
 hipError_t LaunchFill8(uint8_t* p, uint8_t v, int64_t n, hipStream_t s);
 hipError_t LaunchCopy16(void* dst, const void* src, size_t n16, hipStream_t s);
 hipError_t LaunchU8ToF32(const uint8_t* in, float* out, size_t count, hipStream_t s);

@@ -3,6 +3,10 @@
 //  * LsAllKernel     SolveLeastSquaresAll (src/quantizer/least_squares.cpp:406-565)
 //  * CostsKernel     ComputeCosts / SampleCost (src/quantizer/cost_utils.cpp:112-158)
 //  * IcmLayerKernel  one layer of RunIcm (src/quantizer/icm.cpp:249-329)
+//  * *LargeRoot*     the same for a large root: SolveLeastSquaresAllLargeRoot
+//                    (least_squares.cpp:667-745), ComputeCostsLargeRoot (cost_utils.cpp:211-233),
+//                    one layer of RunIcmLargeRoot (icm.cpp:347-870)
+//  * PerturbKernel, IlsAcceptKernel   the ILS rounds (icm.cpp:944-1001, :1070-1116)
 //
 // The Cholesky is the hand-written one of least_squares.cpp:44-84 (row-major upper factor,
 // true division, retry with diagonal bumps 1e-6, 1e-5, 1e-4). Its failure test is the
@@ -60,21 +64,51 @@ __device__ __forceinline__ void SolveUpper(const float (&A)[M * M], const float 
     }
 }
 
-// SolveLeastSquaresSampleFixed (least_squares.cpp:86-129) for one vector.
-template <int M>
+// Flat code of each layer of one vector. Large root: layer 0 is the root (flat[0] unused) and
+// the stored codes start at layer 1.
+template <int M, bool LR>
+__device__ __forceinline__ void Flats(const LsArgs& p, const uint8_t* __restrict__ c, int (&flat)[M]) {
+#pragma unroll
+    for (int l = 0; l < M; ++l) {
+        if constexpr (LR) {
+            flat[l] = l == 0 ? 0 : p.off[l] + c[l - 1];
+        } else {
+            flat[l] = p.off[l] + c[l];
+        }
+    }
+}
+
+// SolveLeastSquaresSampleFixed (least_squares.cpp:86-129) for one vector; for a large root
+// SolveLeastSquaresSampleLargeRootFixed[WithB0] (:131-250), whose row 0 is the root:
+// A(0,0) = norm0[root], A(0,j) = G0S(root, flat_j), b0 = <C0[:,root], x>.
+template <int M, bool LR>
 __device__ __forceinline__ bool SolveLs(const LsArgs& p, const float* __restrict__ xCi, const int (&flat)[M],
-                                        float (&x)[M]) {
+                                        uint32_t root, float b0, float (&x)[M]) {
     float A[M * M];
     float b[M];
     auto fill = [&](float lambda) {
 #pragma unroll
         for (int q = 0; q < M * M; ++q) A[q] = 0.0f;
+        if constexpr (LR) {
+            const float* g0 = p.G0S_rm + static_cast<int64_t>(root) * p.H;
+            b[0] = b0;
+            A[0] = p.norm0[root] + lambda;
 #pragma unroll
-        for (int j = 0; j < M; ++j) {
-            b[j] = xCi[flat[j]];
+            for (int j = 1; j < M; ++j) {
+                b[j] = xCi[flat[j]];
+                A[j] = g0[flat[j]];
 #pragma unroll
-            for (int k = 0; k <= j; ++k) A[k * M + j] = p.G_rm[static_cast<int64_t>(flat[k]) * p.H + flat[j]];
-            A[j * M + j] = A[j * M + j] + lambda;
+                for (int k = 1; k <= j; ++k) A[k * M + j] = p.G_rm[static_cast<int64_t>(flat[k]) * p.H + flat[j]];
+                A[j * M + j] = A[j * M + j] + lambda;
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < M; ++j) {
+                b[j] = xCi[flat[j]];
+#pragma unroll
+                for (int k = 0; k <= j; ++k) A[k * M + j] = p.G_rm[static_cast<int64_t>(flat[k]) * p.H + flat[j]];
+                A[j * M + j] = A[j * M + j] + lambda;
+            }
         }
     };
     fill(0.0f);
@@ -93,57 +127,82 @@ __device__ __forceinline__ bool SolveLs(const LsArgs& p, const float* __restrict
 }
 
 // SampleCost (cost_utils.cpp:112-137): nx2 - 2*sum a_l xC_l + sum_l sum_k a_l a_k G(l,k).
-template <int M>
+// Large root (SampleCostLargeRootFixed, :42-84): term1 = a0*<c0,x> + sum_{l>=1} a_l xC_l and
+// term2 = a0*a0*norm0 + sum_{j>=1} (2*a0*a_j*G0S(root,j) + sum_{k>=1} a_j a_k G(j,k)).
+template <int M, bool LR>
 __device__ __forceinline__ float Cost(const LsArgs& p, const float* __restrict__ xCi, const int (&flat)[M],
-                                      const float (&a)[M], float nx2) {
-    float term1 = 0.0f, term2 = 0.0f;
+                                      uint32_t root, float xc0, const float (&a)[M], float nx2) {
+    if constexpr (LR) {
+        const float* g0 = p.G0S_rm + static_cast<int64_t>(root) * p.H;
+        float term1 = a[0] * xc0;
 #pragma unroll
-    for (int l = 0; l < M; ++l) {
-        const float al = a[l];
-        term1 = term1 + al * xCi[flat[l]];
-        const float* Grow = p.G_rm + static_cast<int64_t>(flat[l]) * p.H;
+        for (int l = 1; l < M; ++l) term1 = term1 + a[l] * xCi[flat[l]];
+        float term2 = 0.0f;
+        term2 = term2 + (a[0] * a[0]) * p.norm0[root];
 #pragma unroll
-        for (int k = 0; k < M; ++k) term2 = term2 + (al * a[k]) * Grow[flat[k]];
+        for (int j = 1; j < M; ++j) {
+            const float aj = a[j];
+            term2 = term2 + ((2.0f * a[0]) * aj) * g0[flat[j]];
+            const float* Grow = p.G_rm + static_cast<int64_t>(flat[j]) * p.H;
+#pragma unroll
+            for (int k = 1; k < M; ++k) term2 = term2 + (aj * a[k]) * Grow[flat[k]];
+        }
+        return nx2 - 2.0f * term1 + term2;
+    } else {
+        float term1 = 0.0f, term2 = 0.0f;
+#pragma unroll
+        for (int l = 0; l < M; ++l) {
+            const float al = a[l];
+            term1 = term1 + al * xCi[flat[l]];
+            const float* Grow = p.G_rm + static_cast<int64_t>(flat[l]) * p.H;
+#pragma unroll
+            for (int k = 0; k < M; ++k) term2 = term2 + (al * a[k]) * Grow[flat[k]];
+        }
+        return nx2 - 2.0f * term1 + term2;
     }
-    return nx2 - 2.0f * term1 + term2;
 }
 
-template <int M>
-__device__ __forceinline__ void Flats(const LsArgs& p, const uint8_t* __restrict__ c, int (&flat)[M]) {
-#pragma unroll
-    for (int l = 0; l < M; ++l) flat[l] = p.off[l] + c[l];
-}
-
-template <int M>
-__global__ __launch_bounds__(256) void LsAllKernel(LsArgs p) {
+template <int M, bool LR>
+__device__ __forceinline__ void LsAllBody(const LsArgs& p) {
     const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (i >= p.n) return;
     int flat[M];
-    Flats<M>(p, p.codes + i * M, flat);
+    Flats<M, LR>(p, p.codes + i * p.cstride, flat);
+    const uint32_t root = LR ? p.root[i] : 0u;
+    const float b0 = LR ? p.b0[i] : 0.0f;
     const float* xCi = p.xC + i * p.ldx;
     float x[M];
     float* ai = p.a + i * M;
-    if (SolveLs<M>(p, xCi, flat, x)) {
+    if (SolveLs<M, LR>(p, xCi, flat, root, b0, x)) {
 #pragma unroll
         for (int l = 0; l < M; ++l) ai[l] = x[l];
     } else {
 #pragma unroll
-        for (int l = 0; l < M; ++l) ai[l] = 0.0f;  // least_squares.cpp:452-455
+        for (int l = 0; l < M; ++l) ai[l] = 0.0f;  // least_squares.cpp:452-455, :690-694
         if (p.fails) atomicAdd(p.fails, 1);
     }
 }
 
-template <int M>
-__global__ __launch_bounds__(256) void CostsKernel(LsArgs p) {
+template <int M, bool LR>
+__device__ __forceinline__ void CostsBody(const LsArgs& p) {
     const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (i >= p.n) return;
     int flat[M];
-    Flats<M>(p, p.codes + i * M, flat);
+    Flats<M, LR>(p, p.codes + i * p.cstride, flat);
     float a[M];
 #pragma unroll
     for (int l = 0; l < M; ++l) a[l] = p.a[i * M + l];
-    p.cost[i] = Cost<M>(p, p.xC + i * p.ldx, flat, a, p.nx2[i]);
+    p.cost[i] = Cost<M, LR>(p, p.xC + i * p.ldx, flat, LR ? p.root[i] : 0u, LR ? p.b0[i] : 0.0f, a, p.nx2[i]);
 }
+
+template <int M>
+__global__ __launch_bounds__(256) void LsAllKernel(LsArgs p) { LsAllBody<M, false>(p); }
+template <int M>
+__global__ __launch_bounds__(256) void LsAllLargeRootKernel(LsArgs p) { LsAllBody<M, true>(p); }
+template <int M>
+__global__ __launch_bounds__(256) void CostsKernel(LsArgs p) { CostsBody<M, false>(p); }
+template <int M>
+__global__ __launch_bounds__(256) void CostsLargeRootKernel(LsArgs p) { CostsBody<M, true>(p); }
 
 __device__ __forceinline__ float ReadLane(float v, int l) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
@@ -164,9 +223,12 @@ __device__ __forceinline__ float WaveMax(float v) {
 // t = lane + 64*jj of layer j:
 //   val(t) = (xC(start+t) - sum_{l != j} a_l G(start+t, flat_l)) * invnorm(start+t)
 // (subtractions in ascending l), pick the first maximum of val (or |val|), and if it differs
-// from the current code, re-solve LS and accept iff new_cost + 1e-6 < cost.
-template <int M>
-__global__ __launch_bounds__(256) void IcmLayerKernel(IcmArgs q) {
+// from the current code, re-solve LS and accept iff new_cost + 1e-6 < cost. For a large root
+// (RunIcmLargeRoot, icm.cpp:437-611) layer 0's term is a0*G0S(root, start+t), the G and
+// invnorm arrays are the small layers' (G_small is symmetric, so its rows serve as columns),
+// and b0 is the vector's cached <C0[:,root], x>.
+template <int M, bool LR>
+__device__ __forceinline__ void IcmLayerBody(const IcmArgs& q) {
     const LsArgs& p = q.ls;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
@@ -175,17 +237,19 @@ __global__ __launch_bounds__(256) void IcmLayerKernel(IcmArgs q) {
     if (!q.active[i]) return;
     const int j = q.j, hj = q.hj;
     const int start = p.off[j];
-    uint8_t* ci = q.codes_rw + i * M;
+    uint8_t* ci = q.codes_rw + i * p.cstride;
+    const int jc = LR ? j - 1 : j;  // position of layer j among the stored codes
     float* ai = p.a + i * M;
     const float* xCi = p.xC + i * p.ldx;
+    const uint32_t root = LR ? p.root[i] : 0u;
+    const float b0 = LR ? p.b0[i] : 0.0f;
     int flat[M];
     float a[M];
+    Flats<M, LR>(p, ci, flat);
 #pragma unroll
-    for (int l = 0; l < M; ++l) {
-        flat[l] = p.off[l] + ci[l];
-        a[l] = ai[l];
-    }
-    const int old_code = ci[j];
+    for (int l = 0; l < M; ++l) a[l] = ai[l];
+    const int old_code = ci[jc];
+    const float* g0 = LR ? p.G0S_rm + static_cast<int64_t>(root) * p.H : nullptr;
 
     float best_val = -kInfF;
     int best_t = 0x7fffffff;
@@ -194,8 +258,9 @@ __global__ __launch_bounds__(256) void IcmLayerKernel(IcmArgs q) {
         float score = -kInfF;
         if (t < hj) {
             float tmp = xCi[start + t];
+            if constexpr (LR) tmp = tmp - a[0] * g0[start + t];
 #pragma unroll
-            for (int l = 0; l < M; ++l) {
+            for (int l = LR ? 1 : 0; l < M; ++l) {
                 if (l == j) continue;
                 tmp = tmp - a[l] * q.G_cm[static_cast<int64_t>(flat[l]) * p.H + start + t];
             }
@@ -219,19 +284,24 @@ __global__ __launch_bounds__(256) void IcmLayerKernel(IcmArgs q) {
 #pragma unroll
     for (int l = 0; l < M; ++l) nflat[l] = (l == j) ? start + best_code : flat[l];
     float x[M];
-    if (!SolveLs<M>(p, xCi, nflat, x)) {
+    if (!SolveLs<M, LR>(p, xCi, nflat, root, b0, x)) {
         atomicAdd(q.fails, 1);
         return;  // icm.cpp:313-318: roll back (nothing was written)
     }
-    const float new_cost = Cost<M>(p, xCi, nflat, x, p.nx2[i]);
+    const float new_cost = Cost<M, LR>(p, xCi, nflat, root, b0, x, p.nx2[i]);
     if (new_cost + kEps < p.cost[i]) {
-        ci[j] = static_cast<uint8_t>(best_code);
+        ci[jc] = static_cast<uint8_t>(best_code);
 #pragma unroll
         for (int l = 0; l < M; ++l) ai[l] = x[l];
         p.cost[i] = new_cost;
         q.changed[i] = 1;
     }
 }
+
+template <int M>
+__global__ __launch_bounds__(256) void IcmLayerKernel(IcmArgs q) { IcmLayerBody<M, false>(q); }
+template <int M>
+__global__ __launch_bounds__(256) void IcmLayerLargeRootKernel(IcmArgs q) { IcmLayerBody<M, true>(q); }
 
 __global__ void DeactivateKernel(uint8_t* active, const uint8_t* changed, int64_t n) {
     const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -242,9 +312,10 @@ __global__ void DeactivateKernel(uint8_t* active, const uint8_t* changed, int64_
 // and the global sample id picks min(perturb_k, m) (layer, new code) pairs in layers 1..m-1,
 // each new code uniform over the layer's codes other than the current one (Lemire multiply-high).
 struct PerturbArgs {
-    uint8_t* codes;  // [n*m], perturbed in place
+    uint8_t* codes;  // [n*cstride], perturbed in place
     int64_t n;
     int m, ksel;
+    int cstride, lfirst;  // codes per vector and the layer of the first stored code
     int h_vec[kMaxM];
     uint32_t seed;
     int outer;
@@ -267,29 +338,28 @@ __global__ __launch_bounds__(256) void PerturbKernel(PerturbArgs p) {
     const uint64_t ig = p.id0 + static_cast<uint64_t>(i);
     uint64_t st = static_cast<uint64_t>(p.seed) ^ (static_cast<uint64_t>(p.outer + 1) * 0x9e3779b97f4a7c15ULL) ^
                   ((ig + 1ULL) * 0xbf58476d1ce4e5b9ULL);
-    uint8_t* ci = p.codes + i * p.m;
+    uint8_t* ci = p.codes + i * p.cstride;  // layer l's code at ci[l - lfirst]
     const uint32_t span = static_cast<uint32_t>(p.m - 1);
     for (int r = 0; r < p.ksel; ++r) {
         const int layer = 1 + static_cast<int>(UniformBelow(st, span));
         const int h = p.h_vec[layer];
         if (h <= 1) continue;
-        const int old = ci[layer];
+        const int old = ci[layer - p.lfirst];
         const int raw = static_cast<int>(UniformBelow(st, static_cast<uint32_t>(h - 1)));
-        ci[layer] = static_cast<uint8_t>(raw >= old ? raw + 1 : raw);
+        ci[layer - p.lfirst] = static_cast<uint8_t>(raw >= old ? raw + 1 : raw);
     }
 }
 
-// Accept-if-better of one ILS round (icm.cpp:977-987): the candidate replaces the vector's codes,
-// coefficients and cost when cand + 1e-6 < cost.
+// Accept-if-better of one ILS round (icm.cpp:977-987, :1104-1116): the candidate replaces the
+// vector's codes (cstride per vector), coefficients (m) and cost when cand + 1e-6 < cost.
 __global__ __launch_bounds__(256) void IlsAcceptKernel(uint8_t* codes, float* a, float* cost, const uint8_t* cc,
-                                                      const float* ca, const float* ccost, int64_t n, int m) {
+                                                      const float* ca, const float* ccost, int64_t n, int m,
+                                                      int cstride) {
     const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (i >= n) return;
     if (ccost[i] + kEps < cost[i]) {
-        for (int l = 0; l < m; ++l) {
-            codes[i * m + l] = cc[i * m + l];
-            a[i * m + l] = ca[i * m + l];
-        }
+        for (int l = 0; l < cstride; ++l) codes[i * cstride + l] = cc[i * cstride + l];
+        for (int l = 0; l < m; ++l) a[i * m + l] = ca[i * m + l];
         cost[i] = ccost[i];
     }
 }
@@ -327,31 +397,45 @@ __global__ __launch_bounds__(256) void IlsAcceptKernel(uint8_t* codes, float* a,
 hipError_t LaunchLsAll(const LsArgs& a, hipStream_t s) {
     if (a.n <= 0) return hipSuccess;
     const dim3 grid(static_cast<unsigned>((a.n + 255) / 256)), block(256);
-    STLQ_SWITCH_M(LsAllKernel, a.m, grid, block, s, a);
+    if (a.root) {
+        STLQ_SWITCH_M(LsAllLargeRootKernel, a.m, grid, block, s, a);
+    } else {
+        STLQ_SWITCH_M(LsAllKernel, a.m, grid, block, s, a);
+    }
     return hipGetLastError();
 }
 
 hipError_t LaunchCosts(const LsArgs& a, hipStream_t s) {
     if (a.n <= 0) return hipSuccess;
     const dim3 grid(static_cast<unsigned>((a.n + 255) / 256)), block(256);
-    STLQ_SWITCH_M(CostsKernel, a.m, grid, block, s, a);
+    if (a.root) {
+        STLQ_SWITCH_M(CostsLargeRootKernel, a.m, grid, block, s, a);
+    } else {
+        STLQ_SWITCH_M(CostsKernel, a.m, grid, block, s, a);
+    }
     return hipGetLastError();
 }
 
 hipError_t LaunchIcmLayer(const IcmArgs& a, hipStream_t s) {
     if (a.ls.n <= 0) return hipSuccess;
     const dim3 grid(static_cast<unsigned>((a.ls.n + 3) / 4)), block(256);
-    STLQ_SWITCH_M(IcmLayerKernel, a.ls.m, grid, block, s, a);
+    if (a.ls.root) {
+        STLQ_SWITCH_M(IcmLayerLargeRootKernel, a.ls.m, grid, block, s, a);
+    } else {
+        STLQ_SWITCH_M(IcmLayerKernel, a.ls.m, grid, block, s, a);
+    }
     return hipGetLastError();
 }
 
-hipError_t LaunchPerturb(uint8_t* codes, int64_t n, int m, const int* h_vec, int perturb_k, uint32_t seed, int outer,
-                         uint64_t id0, hipStream_t s) {
+hipError_t LaunchPerturb(uint8_t* codes, int64_t n, int m, int cstride, int lfirst, const int* h_vec, int perturb_k,
+                         uint32_t seed, int outer, uint64_t id0, hipStream_t s) {
     if (n <= 0 || m <= 1 || perturb_k <= 0) return hipSuccess;
     PerturbArgs p;
     p.codes = codes;
     p.n = n;
     p.m = m;
+    p.cstride = cstride;
+    p.lfirst = lfirst;
     p.ksel = perturb_k < m ? perturb_k : m;
     for (int l = 0; l < m; ++l) p.h_vec[l] = h_vec[l];
     p.seed = seed;
@@ -362,10 +446,10 @@ hipError_t LaunchPerturb(uint8_t* codes, int64_t n, int m, const int* h_vec, int
 }
 
 hipError_t LaunchIlsAccept(uint8_t* codes, float* a, float* cost, const uint8_t* cc, const float* ca, const float* ccost,
-                           int64_t n, int m, hipStream_t s) {
+                           int64_t n, int m, int cstride, hipStream_t s) {
     if (n <= 0) return hipSuccess;
     hipLaunchKernelGGL(IlsAcceptKernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s, codes, a, cost,
-                       cc, ca, ccost, n, m);
+                       cc, ca, ccost, n, m, cstride);
     return hipGetLastError();
 }
 

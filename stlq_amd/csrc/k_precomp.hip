@@ -82,6 +82,31 @@ __device__ __forceinline__ float SimdLane4SumSq(const float* __restrict__ x, int
     return (((0.0f + p0) + p1) + p2) + p3;
 }
 
+// Dot product in the same `omp simd` order (least_squares.cpp:35-42 Dot, icm.cpp:67-74 DotF32,
+// cost_utils.cpp:55-60): the large-root LS right-hand side b0 = <C0[:,root], x>.
+__device__ __forceinline__ float SimdLane4Dot(const float* __restrict__ a, const float* __restrict__ b, int d) {
+    float p0 = 0.0f, p1 = 0.0f, p2 = 0.0f, p3 = 0.0f;
+    const int d4 = d & ~3;
+    for (int t = 0; t < d4; t += 4) {
+        p0 = p0 + a[t] * b[t];
+        p1 = p1 + a[t + 1] * b[t + 1];
+        p2 = p2 + a[t + 2] * b[t + 2];
+        p3 = p3 + a[t + 3] * b[t + 3];
+    }
+    for (int t = d4; t < d; ++t) p0 = p0 + a[t] * b[t];
+    return (((0.0f + p0) + p1) + p2) + p3;
+}
+
+// b0[i] = <C0[:,root[i]], x_i>, one thread per vector (d mul+adds; the C0 rows are shared
+// through L2, the X rows are read once).
+__global__ __launch_bounds__(256) void RootDotKernel(const float* __restrict__ X, int d, const float* __restrict__ C0,
+                                                     const uint32_t* __restrict__ root, int64_t n,
+                                                     float* __restrict__ out) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    out[i] = SimdLane4Dot(C0 + static_cast<int64_t>(root[i]) * d, X + i * d, d);
+}
+
 // ||c||^2 and 1/sqrt(||c||^2) per codeword. lane4 = false: the sequential loop of
 // encoder_precomp.inc:31-39 (invnorm_flat); lane4 = true: Norm2 of precomp_large_root.cpp:14-23
 // (norm0, invnorm_small_flat), an `omp simd` reduction.
@@ -209,6 +234,14 @@ hipError_t LaunchCross(const float* C0, int h0, const float* Cs, int Hs, int d, 
     if (h0 <= 0 || Hs <= 0) return hipSuccess;
     dim3 grid((Hs + kDotTile - 1) / kDotTile, (h0 + kDotTile - 1) / kDotTile);
     hipLaunchKernelGGL(SeqDotKernel, grid, dim3(256), 0, s, C0, h0, Cs, Hs, d, G0S_rm, static_cast<int64_t>(Hs));
+    return hipGetLastError();
+}
+
+hipError_t LaunchRootDot(const float* X, int d, const float* C0, const uint32_t* root, int64_t n, float* out,
+                         hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(RootDotKernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s, X, d, C0, root,
+                       n, out);
     return hipGetLastError();
 }
 

@@ -198,7 +198,7 @@ class Context:
         X = _c(X, np.float32)
         n = X.shape[0]
         codes = np.empty((n, self.m), np.uint8)
-        want = cfg.want_coeffs or cfg.icm_iters > 0
+        want = cfg.want_coeffs or cfg.icm_iters > 0 or cfg.ils_iters > 0
         a = np.empty((n, self.m), np.float32) if want else None
         cost = np.empty(n, np.float32) if want else None
         bm, fm = ctypes.c_double(0), ctypes.c_double(0)
@@ -253,12 +253,13 @@ class Context:
                       root_mode=1):
         """Streaming encode. fill(first, count, out) fills `out` ((count, d) float32, or uint8 when
         input_u8). sink(first, count, result) receives a dict of numpy copies: full precomp ->
-        codes (and a, cost when coefficients are wanted); large root -> cluster_id, B_small, best_err."""
+        codes; large root -> cluster_id, B_small, best_err; both with a and cost when coefficients
+        or ICM/ILS are asked for."""
         if large_root:
             d, m = self.lr[0], len(self.lr[1])
         else:
             d, m = self.d, self.m
-        want = (not large_root) and (cfg.want_coeffs or cfg.icm_iters > 0 or cfg.ils_iters > 0)
+        want = cfg.want_coeffs or cfg.icm_iters > 0 or cfg.ils_iters > 0
         dt = np.uint8 if input_u8 else np.float32
         ctype = ctypes.c_uint8 if input_u8 else ctypes.c_float
         err = []
@@ -283,6 +284,9 @@ class Context:
                     res["B_small"] = (np.ctypeslib.as_array(o.B_small, shape=(count * (m - 1),)).reshape(count, m - 1).copy()
                                       if m > 1 else np.zeros((count, 0), np.uint8))
                     res["best_err"] = np.ctypeslib.as_array(o.best_err, shape=(count,)).copy()
+                    if want:
+                        res["a"] = np.ctypeslib.as_array(o.a, shape=(count * m,)).reshape(count, m).copy()
+                        res["cost"] = np.ctypeslib.as_array(o.cost, shape=(count,)).copy()
                 else:
                     res["codes"] = np.ctypeslib.as_array(o.codes, shape=(count * m,)).reshape(count, m).copy()
                     if want:
@@ -327,6 +331,47 @@ class Context:
                                                          _p(fr, _u32p), int(root_mode), _p(cid, _u32p), _p(Bs, _u8p),
                                                          _p(err, _f32p)))
         return cid, Bs, err
+
+    def _lr_inputs(self, X, cluster_id, B_small, xC_small):
+        X = _c(X, np.float32)
+        n = X.shape[0]
+        m = len(self.lr[1])
+        cid = _c(cluster_id, np.uint32)
+        Bs = np.array(B_small, dtype=np.uint8, order="C", copy=True).reshape(n, max(m - 1, 0))
+        xs = _c(xC_small, np.float32) if xC_small is not None else None
+        return X, n, m, cid, Bs, xs
+
+    def solve_ls_all_large_root(self, X, cluster_id, B_small, xC_small=None):
+        """SolveLeastSquaresAllLargeRoot (least_squares.cpp:667-745); returns (a, fail_count)."""
+        X, n, m, cid, Bs, xs = self._lr_inputs(X, cluster_id, B_small, xC_small)
+        a = np.empty((n, m), np.float32)
+        fails = ctypes.c_int64(0)
+        check(self.lib.stlq_mi355_solve_ls_all_large_root(self.h, _p(X, _f32p), _p(xs, _f32p), n, _p(cid, _u32p),
+                                                          _p(Bs, _u8p), _p(a, _f32p), ctypes.byref(fails)))
+        return a, int(fails.value)
+
+    def compute_costs_large_root(self, X, cluster_id, B_small, a, nx2=None, xC_small=None):
+        """ComputeCostsLargeRoot (cost_utils.cpp:211-233)."""
+        X, n, m, cid, Bs, xs = self._lr_inputs(X, cluster_id, B_small, xC_small)
+        a = _c(a, np.float32)
+        nx = _c(nx2, np.float32) if nx2 is not None else None
+        cost = np.empty(n, np.float32)
+        check(self.lib.stlq_mi355_compute_costs_large_root(self.h, _p(X, _f32p), _p(xs, _f32p), n, _p(cid, _u32p),
+                                                           _p(Bs, _u8p), _p(a, _f32p), _p(nx, _f32p), _p(cost, _f32p)))
+        return cost
+
+    def icm_ils_large_root(self, X, cluster_id, B_small, icm_iters, ils_iters, perturb_k, use_abs, seed,
+                           nx2=None, xC_small=None, sample_id_offset=0):
+        """DynamicIcmWithIls{Abs,NoAbs}NoNormalLargeRoot (icm.cpp:1005-1120); returns (B_small, a, cost)."""
+        X, n, m, cid, Bs, xs = self._lr_inputs(X, cluster_id, B_small, xC_small)
+        nx = _c(nx2, np.float32) if nx2 is not None else None
+        a = np.empty((n, m), np.float32)
+        cost = np.empty(n, np.float32)
+        check(self.lib.stlq_mi355_icm_ils_large_root(self.h, _p(X, _f32p), _p(nx, _f32p), _p(xs, _f32p), n,
+                                                     _p(cid, _u32p), int(icm_iters), int(ils_iters), int(perturb_k),
+                                                     int(bool(use_abs)), int(seed) & 0xFFFFFFFF, int(sample_id_offset),
+                                                     _p(Bs, _u8p), _p(a, _f32p), _p(cost, _f32p)))
+        return Bs, a, cost
 
 
 # ---- reference-named free functions ----------------------------------------------------------
@@ -389,7 +434,8 @@ def EncodeBaseStreamingF32(ctx: Context, n_total, chunk, cfg: EncodeConfig, fill
 
 def EncodeBaseStreaming(ctx: Context, n_total, chunk, cfg: EncodeConfig, fill, sink, root_mode=1):
     """src/quantizer/encode_base_streaming.cpp:1913 (large pipeline): uint8 chunks widened on the
-    device, large-root beam; sink gets cluster_id, B_small and best_err per chunk."""
+    device, large-root beam, then the large-root refit (:1117-1210) when cfg asks for
+    coefficients or ICM/ILS; sink gets cluster_id, B_small, best_err (and a, cost) per chunk."""
     return ctx.encode_stream(n_total, chunk, cfg, fill, sink, input_u8=True, large_root=True, root_mode=root_mode)
 
 
@@ -402,3 +448,27 @@ def BeamSearchPrefixLSLargeRoot(ctx: Context, X, xC_small, H_beam, forced_root=N
     """src/quantizer/beam_search.cpp:579-726: (cluster_id, B_small)."""
     cid, Bs, _ = ctx.beam_search_large_root(X, H_beam, xC_small=xC_small, forced_root=forced_root)
     return cid, Bs
+
+
+def SolveLeastSquaresAllLargeRoot(ctx: Context, X, xC_small, cluster_id, B_small):
+    """src/quantizer/least_squares.cpp:667-745: a (n, m); failed vectors get zero coefficients."""
+    return ctx.solve_ls_all_large_root(X, cluster_id, B_small, xC_small=xC_small)[0]
+
+
+def ComputeCostsLargeRoot(ctx: Context, X, xC_small, cluster_id, B_small, a, X_norm2):
+    """src/quantizer/cost_utils.cpp:211-233."""
+    return ctx.compute_costs_large_root(X, cluster_id, B_small, a, nx2=X_norm2, xC_small=xC_small)
+
+
+def DynamicIcmWithIlsAbsNoNormalLargeRoot(ctx: Context, X, xC_small, icm_iters, ils_iters, perturb_k, seed,
+                                          cluster_id, B_small, print_progress=True, sample_id_offset=0):
+    """src/quantizer/icm.cpp:1005-1120 (icm.h:62-75), |score|: returns (B_small, a, cost)."""
+    return ctx.icm_ils_large_root(X, cluster_id, B_small, icm_iters, ils_iters, perturb_k, True, seed,
+                                  xC_small=xC_small, sample_id_offset=sample_id_offset)
+
+
+def DynamicIcmWithIlsNoAbsNoNormalLargeRoot(ctx: Context, X, xC_small, icm_iters, ils_iters, perturb_k, seed,
+                                            cluster_id, B_small, print_progress=True, sample_id_offset=0):
+    """src/quantizer/icm.cpp:1005-1120 (icm.h:47-60), signed score: returns (B_small, a, cost)."""
+    return ctx.icm_ils_large_root(X, cluster_id, B_small, icm_iters, ils_iters, perturb_k, False, seed,
+                                  xC_small=xC_small, sample_id_offset=sample_id_offset)

@@ -124,3 +124,23 @@ def degenerate_problem(case):
         C[12 + 3] = 2.0 * C[1]
         C[24 + 6] = -0.5 * C[12 + 8]
     return X, C, h
+
+
+def large_root_problem(orc, seed, n, d, h0, K, m, H_beam=4, root_mode=1, kind="gauss"):
+    """A large-root problem (root codebook of h0 codewords + m-1 residual books of K) with the
+    oracle's precomp, xC_small, and the oracle's large-root beam codes as the starting point."""
+    from stlq_amd import workloads
+
+    mix = workloads.Mixture(kind, d, 128, seed)
+    rng = np.random.default_rng(seed)
+    C0 = mix.sample(5_000_000, h0)
+    Xtr = mix.sample(1_000_000, 2000)
+    Cs = workloads.residual_codebooks(Xtr - C0[rng.integers(0, h0, 2000)], m - 1, K, 3, seed + 1)
+    X = mix.sample(0, n)
+    h = [h0] + [K] * (m - 1)
+    norm0, Gs, G0S = orc.build_precomp_large_root(C0, Cs)
+    invs = orc.invnorm_small(Cs)
+    nx2 = orc.xnorm2(X)
+    xs = orc.gemm_xc(Cs, X, mode=1)
+    cid, Bs, _ = orc.beam_search_large_root(X, nx2, C0, norm0, xs, Gs, G0S, h, H_beam, root_mode=root_mode)
+    return dict(X=X, C0=C0, Cs=Cs, h=h, norm0=norm0, Gs=Gs, G0S=G0S, invs=invs, nx2=nx2, xs=xs, cid=cid, Bs=Bs)

@@ -477,3 +477,80 @@ def test_stream_chunk_larger_than_workspace(ctx, monkeypatch):
 
     ctx.encode_stream(6000, 6000, cfg, fill, sink)
     assert np.array_equal(codes, got)
+
+
+def _lr_refit_problem(ctx, orc, m, seed, n=2000, d=32, h0=1500, K=64):
+    from tests.helpers import large_root_problem
+
+    p = large_root_problem(orc, seed, n, d, h0, K, m, H_beam=4, root_mode=1, kind="desc" if d >= 32 else "gauss")
+    ctx.set_large_root(p["C0"], p["Cs"], p["h"])
+    return p
+
+
+@pytest.mark.parametrize("m", [2, 5, 8, 11])
+def test_large_root_ls_costs_bit_exact(ctx, orc, m):
+    """SolveLeastSquaresAllLargeRoot + ComputeCostsLargeRoot on the device: b0 = <C0[:,root], x> in
+    the omp-simd order, the root row of the system from norm0/G0S, the reference's cost order."""
+    p = _lr_refit_problem(ctx, orc, m, 300 + m)
+    print(f"lr refit m={m} n={p['X'].shape[0]}", flush=True)
+    a_o, _ = orc.solve_ls_all_large_root(p["X"], p["C0"], p["norm0"], p["xs"], p["Gs"], p["G0S"], p["h"], p["cid"],
+                                         p["Bs"])
+    c_o = orc.compute_costs_large_root(p["X"], p["C0"], p["norm0"], p["xs"], p["Gs"], p["G0S"], p["h"], p["cid"],
+                                       p["Bs"], a_o, p["nx2"])
+    for xs in (p["xs"], None):  # given xC_small, or the device GEMM (same fused order as the oracle's mode 1)
+        a_g, fails = ctx.solve_ls_all_large_root(p["X"], p["cid"], p["Bs"], xC_small=xs)
+        assert fails == 0
+        assert np.array_equal(_bits(a_g), _bits(a_o))
+        c_g = ctx.compute_costs_large_root(p["X"], p["cid"], p["Bs"], a_o, xC_small=xs)
+        assert np.array_equal(_bits(c_g), _bits(c_o))
+
+
+@pytest.mark.parametrize("m,icm,ils,pk,off,use_abs", [(5, 2, 0, 3, 0, True), (5, 1, 3, 2, 777, False),
+                                                      (8, 2, 2, 3, 10_000, True), (3, 0, 3, 3, 5, True)])
+def test_large_root_icm_ils_bit_exact(ctx, orc, m, icm, ils, pk, off, use_abs):
+    """DynamicIcmWithIls*NoNormalLargeRoot on the device: roots fixed, ICM over layers 1..m-1
+    with the root's G0S row, ILS rounds keyed by the global id; codes, a and cost identical."""
+    p = _lr_refit_problem(ctx, orc, m, 400 + m + icm + ils)
+    print(f"lr icm m={m} icm={icm} ils={ils} pk={pk} off={off} abs={use_abs}", flush=True)
+    B_o, a_o, c_o, _ = orc.icm_ils_large_root(p["X"], p["C0"], p["norm0"], p["xs"], p["Gs"], p["G0S"], p["invs"],
+                                              p["h"], p["cid"], p["nx2"], p["Bs"], icm, ils, pk, use_abs, 38251450,
+                                              off)
+    B_g, a_g, c_g = ctx.icm_ils_large_root(p["X"], p["cid"], p["Bs"], icm, ils, pk, use_abs, 38251450,
+                                           sample_id_offset=off)
+    if icm > 0:
+        assert np.any(B_o != p["Bs"])
+    assert np.array_equal(B_g, B_o), np.nonzero(np.any(B_g != B_o, axis=1))[0][:10]
+    assert np.array_equal(_bits(a_g), _bits(a_o))
+    assert np.array_equal(_bits(c_g), _bits(c_o))
+
+
+@pytest.mark.parametrize("icm,ils", [(0, 0), (1, 2)])
+def test_stream_large_root_refit(ctx, orc, icm, ils):
+    """The large-root streaming encode with the refit (encode_base_streaming.cpp:1117-1210): per
+    chunk cluster ids and codes of the beam, then LS/ICM/ILS with sample_id_offset = the chunk's
+    global start; equal to the in-memory beam followed by the oracle's refit over all vectors."""
+    m, n, chunk = 6, 5000, 1700
+    p = _lr_refit_problem(ctx, orc, m, 500 + icm, n=n, d=64, h0=2048, K=128)
+    Xu8 = np.clip(np.rint(p["X"]), 0, 255).astype(np.uint8)
+    Xf = Xu8.astype(np.float32)
+    cid, Bs, _ = ctx.beam_search_large_root(Xf, 8, root_mode=1)
+    nx2 = orc.xnorm2(Xf)
+    xs = orc.gemm_xc(p["Cs"], Xf, mode=1)
+    B_o, a_o, c_o, _ = orc.icm_ils_large_root(Xf, p["C0"], p["norm0"], xs, p["Gs"], p["G0S"], p["invs"], p["h"], cid,
+                                              nx2, Bs, icm, ils, 3, True, 38251450, 0)
+    got = {"cluster_id": np.zeros_like(cid), "B_small": np.zeros_like(Bs), "a": np.zeros_like(a_o),
+           "cost": np.zeros_like(c_o)}
+
+    def fill(first, count, out):
+        out[:] = Xu8[first:first + count]
+
+    def sink(first, count, res):
+        for k in got:
+            got[k][first:first + count] = res[k]
+
+    cfg = EncodeConfig(H_beam=8, icm_iters=icm, ils_iters=ils, perturb_k=3, want_coeffs=True)
+    ctx.encode_stream(n, chunk, cfg, fill, sink, input_u8=True, large_root=True, root_mode=1)
+    assert np.array_equal(got["cluster_id"], cid)
+    assert np.array_equal(got["B_small"], B_o)
+    assert np.array_equal(_bits(got["a"]), _bits(a_o))
+    assert np.array_equal(_bits(got["cost"]), _bits(c_o))

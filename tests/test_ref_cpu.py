@@ -13,6 +13,9 @@ Pinned here, bit for bit, on the same inputs:
   * the large-root expansion BeamSearchPrefixLSLargeRootExpandFromRootCandidates
     (beam_search.cpp:728-992) from the oracle's root candidates, for top-H, nearest and forced
     roots.
+  * the large-root LS refit, costs, ICM and ILS (SolveLeastSquaresAllLargeRoot,
+    ComputeCostsLargeRoot, DynamicIcmWithIls*NoNormalLargeRoot) for m in {5, 10}; costs for
+    every m.
 For m not in {5, 10} the reference solves the LS systems with LAPACK spotrf/spotrs (here the
 image's MKL, whose kernels are chosen per CPU), so their bits are not fixed by the reference.
 There the tests bound the deviation instead: equal-quality LS solutions (fp64 objective within
@@ -189,3 +192,66 @@ def test_ils_lapack_path_same_quality(orc, m):
     mo = orc.mse_fp64_refit(X, C, h, k_o)
     mr = orc.mse_fp64_refit(X, C, h, k_r)
     assert abs(mo.mean() - mr.mean()) <= 1e-3 * mr.mean()
+
+
+def _lr(orc, m, d=32, seed=61):
+    from tests.helpers import large_root_problem
+
+    return large_root_problem(orc, seed + m, 1500, d, 700, 64, m)
+
+
+@pytest.mark.parametrize("m,d", [(5, 32), (10, 24), (5, 13)])
+def test_ls_large_root_matches_reference(orc, m, d):
+    """SolveLeastSquaresAllLargeRoot (least_squares.cpp:667-745) where the reference runs its own
+    Cholesky: coefficients bit for bit, which also pins b0 = <C0[:,cid], x> in the omp-simd order."""
+    p = _lr(orc, m, d)
+    a_o, fails = orc.solve_ls_all_large_root(p["X"], p["C0"], p["norm0"], p["xs"], p["Gs"], p["G0S"], p["h"],
+                                             p["cid"], p["Bs"])
+    a_r = ref.solve_ls_all_large_root(p["X"], p["C0"], p["norm0"], p["Gs"], p["G0S"], p["h"], p["xs"], p["cid"],
+                                      p["Bs"])
+    assert fails == 0
+    assert np.array_equal(_bits(a_o), _bits(a_r))
+
+
+@pytest.mark.parametrize("m", [2, 3, 5, 8, 10])
+def test_costs_large_root_match_reference(orc, m):
+    """ComputeCostsLargeRoot (cost_utils.cpp:42-84, :160-233) on the same coefficients."""
+    p = _lr(orc, m)
+    a = ref.solve_ls_all_large_root(p["X"], p["C0"], p["norm0"], p["Gs"], p["G0S"], p["h"], p["xs"], p["cid"], p["Bs"])
+    c_o = orc.compute_costs_large_root(p["X"], p["C0"], p["norm0"], p["xs"], p["Gs"], p["G0S"], p["h"], p["cid"],
+                                       p["Bs"], a, p["nx2"])
+    c_r = ref.compute_costs_large_root(p["X"], p["C0"], p["norm0"], p["Gs"], p["G0S"], p["h"], p["xs"], p["cid"],
+                                       p["Bs"], a, p["nx2"])
+    assert np.array_equal(_bits(c_o), _bits(c_r))
+
+
+@pytest.mark.parametrize("use_abs", [True, False])
+@pytest.mark.parametrize("m,icm,ils,pk,off", [(5, 2, 0, 3, 0), (5, 1, 3, 2, 777), (10, 2, 2, 4, 40_000)])
+def test_icm_ils_large_root_matches_reference(orc, m, icm, ils, pk, off, use_abs):
+    """DynamicIcmWithIls{Abs,NoAbs}NoNormalLargeRoot (icm.cpp:347-870, :1005-1120): roots fixed,
+    ICM over layers 1..m-1 with the root's G0S row, perturbations keyed by the global id."""
+    p = _lr(orc, m)
+    B_o, a_o, c_o, _ = orc.icm_ils_large_root(p["X"], p["C0"], p["norm0"], p["xs"], p["Gs"], p["G0S"], p["invs"],
+                                              p["h"], p["cid"], p["nx2"], p["Bs"], icm, ils, pk, use_abs, 38251450,
+                                              off)
+    B_r, a_r, c_r = ref.icm_large_root(p["X"], p["C0"], p["norm0"], p["Gs"], p["G0S"], p["invs"], p["h"], p["xs"],
+                                       p["cid"], p["Bs"], icm, use_abs, 38251450, ils_iters=ils, perturb_k=pk,
+                                       sample_id_offset=off)
+    assert np.any(B_o != p["Bs"])
+    assert np.array_equal(B_o, B_r)
+    assert np.array_equal(_bits(a_o), _bits(a_r))
+    assert np.array_equal(_bits(c_o), _bits(c_r))
+
+
+@pytest.mark.parametrize("m", [3, 8])
+def test_icm_large_root_lapack_path_bounded(orc, m):
+    """m not in {5, 10}: the reference's large-root LS goes through LAPACK. Coefficients agree in
+    quality (costs within 1e-5 relative of ||x||^2 scale) and at most 3% of the code tuples differ."""
+    p = _lr(orc, m)
+    B_o, a_o, c_o, _ = orc.icm_ils_large_root(p["X"], p["C0"], p["norm0"], p["xs"], p["Gs"], p["G0S"], p["invs"],
+                                              p["h"], p["cid"], p["nx2"], p["Bs"], 2, 2, 2, True, 38251450)
+    B_r, a_r, c_r = ref.icm_large_root(p["X"], p["C0"], p["norm0"], p["Gs"], p["G0S"], p["invs"], p["h"], p["xs"],
+                                       p["cid"], p["Bs"], 2, True, 38251450, ils_iters=2, perturb_k=2)
+    assert np.mean(np.any(B_o != B_r, axis=1)) <= 0.03
+    same = np.all(B_o == B_r, axis=1)
+    assert np.max(np.abs(c_o[same] - c_r[same]) / p["nx2"][same]) <= 1e-5
