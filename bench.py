@@ -317,7 +317,8 @@ def main():
 
 def bench_stream_large_root(args, w):
     """C5: streaming encode of uint8-valued descriptor vectors in pinned chunks, nearest root of a
-    65,536-codeword root codebook forced, then 16 residual codebooks x 256, beam 32."""
+    65,536-codeword root codebook forced, then 16 residual codebooks x 256, beam 32, then the
+    large-root LS refit and per-vector cost (the coefficients the streaming encode stores)."""
     from stlq_amd import workloads
     from stlq_amd.encoder import Context, EncodeConfig
 
@@ -335,7 +336,7 @@ def bench_stream_large_root(args, w):
     ctx = Context(0)
     dev_name, cus = ctx.device_info()
     ctx.set_large_root(C0, Cs, h)
-    cfg = EncodeConfig(H_beam=w.H_beam, icm_iters=0, want_coeffs=False)
+    cfg = EncodeConfig(H_beam=w.H_beam, icm_iters=0, want_coeffs=True)
     P = pool.shape[0]
     keep = min(2000, chunk)
     first_codes = {}
@@ -352,6 +353,8 @@ def bench_stream_large_root(args, w):
         if first == 0:
             first_codes["cid"] = res["cluster_id"][:keep].copy()
             first_codes["Bs"] = res["B_small"][:keep].copy()
+            first_codes["a"] = res["a"][:keep].copy()
+            first_codes["cost"] = res["cost"][:keep].copy()
 
     warm = min(chunk, 100_000)
     ctx.encode_stream(warm, warm, cfg, fill, sink, input_u8=True, large_root=True, root_mode=1)
@@ -384,7 +387,7 @@ def bench_stream_large_root(args, w):
         "data": "synthetic",
         "config": {"workload": f"streaming encode of {n} uint8-valued d=128 vectors (C2 generator) in {chunk}-vector "
                                "pinned chunks, double-buffered H2D; nearest of 65,536 root codewords forced, then "
-                               "16 residual codebooks x 256, beam 32",
+                               "16 residual codebooks x 256, beam 32, then the large-root LS refit and cost",
                    "name": "C5", "n": n, "chunk": chunk, "d": w.d, "h0": h0, "M_small": M - 1, "K": w.K,
                    "H_beam": w.H_beam},
         "roofline": {
@@ -412,6 +415,7 @@ def bench_stream_large_root(args, w):
             "gemm_ms_per_chunk": t.gemm_ms / nch,
             "root_seed_ms_per_chunk": layer_ms[0] / nch,
             "beam_layer_ms_per_chunk": [round(x / nch, 3) for x in layer_ms[:M]],
+            "refit_ms_per_chunk": (t.ls_ms + t.icm_ms) / nch,
             "device_total_ms_per_chunk": t.total_ms / nch,
         },
         "device": {"arch": dev_name, "cus": cus},
@@ -433,26 +437,39 @@ def bench_stream_large_root(args, w):
                                                               nthreads=threads)
             t_root = time.perf_counter() - tc
             cid_o, Bs_o = ref.expand_large_root(Gs, G0S, h, xs, w.H_beam, errs, rcodes, a0, r00)
+            t_beam = time.perf_counter() - tc
+            a_o = ref.solve_ls_all_large_root(Xs, C0, norm0, Gs, G0S, h, xs, cid_o, Bs_o)
+            c_o = ref.compute_costs_large_root(Xs, C0, norm0, Gs, G0S, h, xs, cid_o, Bs_o, a_o, nx2)
         else:
             cid_o, Bs_o, _ = orc.beam_search_large_root(Xs, nx2, C0, norm0, xs, Gs, G0S, h, w.H_beam, root_mode=1,
                                                         nthreads=threads)
             t_root = 0.0
+            t_beam = time.perf_counter() - tc
+            a_o, _ = orc.solve_ls_all_large_root(Xs, C0, norm0, xs, Gs, G0S, h, cid_o, Bs_o, nthreads=threads)
+            c_o = orc.compute_costs_large_root(Xs, C0, norm0, xs, Gs, G0S, h, cid_o, Bs_o, a_o, nx2, nthreads=threads)
         t_cpu = time.perf_counter() - tc
         log(f"cpu {'reference' if use_ref else 'oracle'}: {ns} vectors in {t_cpu:.1f}s on {threads} threads")
         if use_ref:
-            what = (f"reference ComputeXNorm2 + BeamSearchPrefixLSLargeRootExpandFromRootCandidates (its own sources, "
-                    f"g++ -O3 -fopenmp) for the 16-layer beam 32; xC_small and the nearest-root scan over 65,536 "
-                    f"roots by the oracle (the reference's root GEMM needs BLAS); stages s: xnorm+xC+root "
-                    f"{t_root:.2f}, expansion {t_cpu - t_root:.2f}")
+            what = (f"reference ComputeXNorm2 + BeamSearchPrefixLSLargeRootExpandFromRootCandidates + "
+                    f"SolveLeastSquaresAllLargeRoot + ComputeCostsLargeRoot (its own sources, g++ -O3 -fopenmp, "
+                    f"LAPACK from MKL for m=17) for the 16-layer beam 32 and the refit; xC_small and the "
+                    f"nearest-root scan over 65,536 roots by the oracle (the reference's root GEMM needs BLAS); "
+                    f"stages s: xnorm+xC+root {t_root:.2f}, expansion {t_beam - t_root:.2f}, refit "
+                    f"{t_cpu - t_beam:.2f}")
         else:
-            what = "oracle port: ||x||^2 + xC_small + nearest-root scan over 65,536 roots + 16-layer beam 32"
+            what = ("oracle port: ||x||^2 + xC_small + nearest-root scan over 65,536 roots + 16-layer beam 32 + "
+                    "large-root LS refit and cost")
         out["cpu_baseline"] = {
             "value": ns / t_cpu, "unit": "vectors/s", "cores": threads,
             "kind": "reference" if use_ref else "port",
             "sample": f"first {ns} vectors of the stream; {what}; cpu: {_cpu_model()}"}
         same = (cid_o == first_codes["cid"][:ns]) & np.all(Bs_o == first_codes["Bs"][:ns], axis=1)
+        cg = first_codes["cost"][:ns]
+        rel = np.abs(cg[same].astype(np.float64) - c_o[same]) / np.maximum(nx2[same].astype(np.float64), 1e-30)
         out["parity"] = {"sample": ns, "against": "reference" if use_ref else "oracle",
-                         "codes_identical_frac": float(np.mean(same))}
+                         "codes_identical_frac": float(np.mean(same)),
+                         "costs_identical_frac": float(np.mean(cg[same].view(np.uint32) == c_o[same].view(np.uint32))),
+                         "cost_max_rel_diff_vs_norm2": float(rel.max()) if rel.size else 0.0}
     ctx.close()
     print(json.dumps(out), flush=True)
 

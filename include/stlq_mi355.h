@@ -95,8 +95,9 @@ int stlq_mi355_set_precomp(stlq_mi355_ctx* ctx, int d, int m, const int* h_vec,
 /* Copies the device precomp back (G column-major H x H, invnorm H). Either may be NULL. */
 int stlq_mi355_get_precomp(stlq_mi355_ctx* ctx, float* G, float* invnorm);
 
-/* ComputeXNorm2 (src/quantizer/cost_utils.cpp:88-110), sequential order per vector. */
-int stlq_mi355_xnorm2(stlq_mi355_ctx* ctx, const float* X, int64_t n, float* out);
+/* ComputeXNorm2 (src/quantizer/cost_utils.cpp:88-110, cost_utils.h:12) in the reference build's
+ * omp-simd order. X is d x n; no codebooks are needed. */
+int stlq_mi355_xnorm2(stlq_mi355_ctx* ctx, const float* X, int d, int64_t n, float* out);
 
 /* StreamKernelProvider::Gemm(true,false,C_all,X) (include/stlq/core/kernel_provider.h:54-77,
  * call site encoder_encode_base.inc:86-90): xC = C_all^T X on fp32 MFMA. */

@@ -95,7 +95,7 @@ SIGNATURES = {
     "stlq_mi355_set_codebooks": ([_vp, _int, _int, _i32p, _f32p], _int),
     "stlq_mi355_set_precomp": ([_vp, _int, _int, _i32p, _f32p, _f32p, _f32p], _int),
     "stlq_mi355_get_precomp": ([_vp, _f32p, _f32p], _int),
-    "stlq_mi355_xnorm2": ([_vp, _f32p, _i64, _f32p], _int),
+    "stlq_mi355_xnorm2": ([_vp, _f32p, _int, _i64, _f32p], _int),
     "stlq_mi355_gemm_xc": ([_vp, _f32p, _i64, _f32p], _int),
     "stlq_mi355_beam_search": ([_vp, _f32p, _f32p, _f32p, _i64, _int, _u8p, _f32p], _int),
     "stlq_mi355_solve_ls_all": ([_vp, _f32p, _u8p, _i64, _f32p, _i64p], _int),

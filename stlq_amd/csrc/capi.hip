@@ -679,14 +679,14 @@ int stlq_mi355_get_precomp(stlq_mi355_ctx* c, float* G, float* invnorm) {
     return STLQ_MI355_OK;
 }
 
-int stlq_mi355_xnorm2(stlq_mi355_ctx* c, const float* X, int64_t n, float* out) {
-    RC_TRY(CheckPre(c));
-    if (n < 0 || (n > 0 && (!X || !out))) return Fail(STLQ_MI355_ERR_INVALID, "bad arguments");
+int stlq_mi355_xnorm2(stlq_mi355_ctx* c, const float* X, int d, int64_t n, float* out) {
+    RC_TRY(CheckCtx(c));
+    if (d < 1 || n < 0 || (n > 0 && (!X || !out))) return Fail(STLQ_MI355_ERR_INVALID, "bad arguments");
     if (n == 0) return STLQ_MI355_OK;
-    HIP_TRY(c->X.Ensure(static_cast<size_t>(n) * c->d * 4));
+    HIP_TRY(c->X.Ensure(static_cast<size_t>(n) * d * 4));
     HIP_TRY(c->nx2.Ensure(static_cast<size_t>(n) * 4));
-    HIP_TRY(hipMemcpyAsync(c->X.p, X, static_cast<size_t>(n) * c->d * 4, hipMemcpyHostToDevice, c->stream));
-    HIP_TRY(LaunchXNorm2(c->X.as<float>(), c->d, n, c->nx2.as<float>(), c->stream));
+    HIP_TRY(hipMemcpyAsync(c->X.p, X, static_cast<size_t>(n) * d * 4, hipMemcpyHostToDevice, c->stream));
+    HIP_TRY(LaunchXNorm2(c->X.as<float>(), d, n, c->nx2.as<float>(), c->stream));
     HIP_TRY(hipMemcpyAsync(out, c->nx2.p, static_cast<size_t>(n) * 4, hipMemcpyDeviceToHost, c->stream));
     HIP_TRY(hipStreamSynchronize(c->stream));
     return STLQ_MI355_OK;

@@ -126,7 +126,7 @@ class Context:
     def xnorm2(self, X):
         X = _c(X, np.float32)
         out = np.empty(X.shape[0], np.float32)
-        check(self.lib.stlq_mi355_xnorm2(self.h, _p(X, _f32p), X.shape[0], _p(out, _f32p)))
+        check(self.lib.stlq_mi355_xnorm2(self.h, _p(X, _f32p), X.shape[1], X.shape[0], _p(out, _f32p)))
         return out
 
     def gemm_xc(self, X):

@@ -166,15 +166,10 @@ inline bool BuildPrecomp(const CodebookPack& codebooks, Precomp* precomp) {
     return true;
 }
 
-// ComputeXNorm2 (src/quantizer/cost_utils.cpp:88-110, cost_utils.h:12). The reference's
-// signature carries no precomp; the device routine runs on this thread's context, which must
-// already hold a Precomp (BuildPrecomp or any call that takes one) of dimension X.rows.
+// ComputeXNorm2 (src/quantizer/cost_utils.cpp:88-110, cost_utils.h:12), on this thread's context.
 inline void ComputeXNorm2(const ColMajorMatrix<float>& X, std::vector<float>* X_norm2) {
-    detail::Session& s = detail::ThreadSession();
-    if (!s.owner || s.d != X.rows)
-        throw std::runtime_error("stlq_mi355: ComputeXNorm2 needs a bound Precomp with d == X.rows");
     X_norm2->resize(static_cast<std::size_t>(X.cols));
-    detail::Check(stlq_mi355_xnorm2(s.ctx, X.data.data(), X.cols, X_norm2->data()));
+    detail::Check(stlq_mi355_xnorm2(detail::ThreadSession().ctx, X.data.data(), X.rows, X.cols, X_norm2->data()));
 }
 
 // xC = C_all^T X (StreamKernelProvider::Gemm call site, encoder_encode_base.inc:86-90).
@@ -402,6 +397,81 @@ inline void BeamSearchPrefixLSLargeRoot(const ColMajorMatrix<float>& X, const Pr
         timing->root_update = 0.0;
         timing->expand = t.beam_ms * 1e-3;
     }
+}
+
+// SolveLeastSquaresAllLargeRoot (src/quantizer/least_squares.cpp:667-745, least_squares.h:54-59).
+// An empty xC_small (rows == 0) has the device compute C_small^T X itself.
+inline void SolveLeastSquaresAllLargeRoot(const PrecompLargeRoot& pre, const ColMajorMatrix<float>& X,
+                                          const ColMajorMatrix<float>& xC_small,
+                                          const std::vector<std::uint32_t>& cluster_id,
+                                          const ColMajorMatrix<Code>& B_small, ColMajorMatrix<float>* a) {
+    stlq_mi355_ctx* ctx = detail::BindLargeRoot(pre);
+    *a = ColMajorMatrix<float>(pre.m, X.cols);
+    const float* xcs = xC_small.rows > 0 ? xC_small.data.data() : nullptr;
+    detail::Check(stlq_mi355_solve_ls_all_large_root(ctx, X.data.data(), xcs, X.cols, cluster_id.data(),
+                                                     B_small.data.data(), a->data.data(), nullptr));
+}
+
+// ComputeCostsLargeRoot (src/quantizer/cost_utils.cpp:211-233, cost_utils.h:37-44).
+inline void ComputeCostsLargeRoot(const PrecompLargeRoot& pre, const ColMajorMatrix<float>& X,
+                                  const ColMajorMatrix<float>& xC_small, const std::vector<std::uint32_t>& cluster_id,
+                                  const ColMajorMatrix<Code>& B_small, const ColMajorMatrix<float>& a,
+                                  const std::vector<float>& X_norm2, std::vector<float>* out_cost) {
+    if (!out_cost) return;
+    stlq_mi355_ctx* ctx = detail::BindLargeRoot(pre);
+    out_cost->resize(static_cast<std::size_t>(std::max(0, B_small.cols)));
+    const float* xcs = xC_small.rows > 0 ? xC_small.data.data() : nullptr;
+    const float* nx2 = X_norm2.empty() ? nullptr : X_norm2.data();
+    detail::Check(stlq_mi355_compute_costs_large_root(ctx, X.data.data(), xcs, X.cols, cluster_id.data(),
+                                                      B_small.data.data(), a.data.data(), nx2, out_cost->data()));
+}
+
+namespace detail {
+inline void DynamicIcmLargeRoot(const ColMajorMatrix<float>& X, const PrecompLargeRoot& pre,
+                                const ColMajorMatrix<float>& xC_small, int icm_iters, int ils_iters, int perturb_k,
+                                std::uint32_t seed, bool use_abs, const std::vector<std::uint32_t>& cluster_id,
+                                ColMajorMatrix<Code>* B_small, ColMajorMatrix<float>* a, std::vector<float>* X_norm2,
+                                std::vector<float>* cost, std::uint64_t sample_id_offset) {
+    if (!B_small || !a) return;  // icm.cpp:1020-1022
+    stlq_mi355_ctx* ctx = BindLargeRoot(pre);
+    if (X_norm2->empty()) {  // icm.cpp:368-370
+        X_norm2->resize(static_cast<std::size_t>(X.cols));
+        Check(stlq_mi355_xnorm2(ctx, X.data.data(), X.rows, X.cols, X_norm2->data()));
+    }
+    *a = ColMajorMatrix<float>(pre.m, B_small->cols);
+    std::vector<float> local;
+    std::vector<float>* c = cost ? cost : &local;
+    c->resize(static_cast<std::size_t>(B_small->cols));
+    const float* xcs = xC_small.rows > 0 ? xC_small.data.data() : nullptr;
+    Check(stlq_mi355_icm_ils_large_root(ctx, X.data.data(), X_norm2->data(), xcs, X.cols, cluster_id.data(),
+                                        icm_iters, ils_iters, perturb_k, use_abs ? 1 : 0, seed, sample_id_offset,
+                                        B_small->data.data(), a->data.data(), c->data()));
+}
+}  // namespace detail
+
+// DynamicIcmWithIls{NoAbs,Abs}NoNormalLargeRoot (src/quantizer/icm.cpp:1005-1120, icm.h:45-75).
+inline void DynamicIcmWithIlsNoAbsNoNormalLargeRoot(const ColMajorMatrix<float>& X, const PrecompLargeRoot& pre,
+                                                    const ColMajorMatrix<float>& xC_small, int icm_iters,
+                                                    int ils_iters, int perturb_k, std::uint32_t seed,
+                                                    const std::vector<std::uint32_t>& cluster_id,
+                                                    ColMajorMatrix<Code>* B_small, ColMajorMatrix<float>* a,
+                                                    std::vector<float>* X_norm2, std::vector<float>* cost,
+                                                    bool print_progress = true, std::uint64_t sample_id_offset = 0) {
+    (void)print_progress;
+    detail::DynamicIcmLargeRoot(X, pre, xC_small, icm_iters, ils_iters, perturb_k, seed, false, cluster_id, B_small,
+                                a, X_norm2, cost, sample_id_offset);
+}
+
+inline void DynamicIcmWithIlsAbsNoNormalLargeRoot(const ColMajorMatrix<float>& X, const PrecompLargeRoot& pre,
+                                                  const ColMajorMatrix<float>& xC_small, int icm_iters,
+                                                  int ils_iters, int perturb_k, std::uint32_t seed,
+                                                  const std::vector<std::uint32_t>& cluster_id,
+                                                  ColMajorMatrix<Code>* B_small, ColMajorMatrix<float>* a,
+                                                  std::vector<float>* X_norm2, std::vector<float>* cost,
+                                                  bool print_progress = true, std::uint64_t sample_id_offset = 0) {
+    (void)print_progress;
+    detail::DynamicIcmLargeRoot(X, pre, xC_small, icm_iters, ils_iters, perturb_k, seed, true, cluster_id, B_small, a,
+                                X_norm2, cost, sample_id_offset);
 }
 
 }  // namespace stlq

@@ -95,8 +95,12 @@ int mirror_encode(int d, int m, const int* h_vec, const float* C_all, const floa
 
 // BuildPrecompLargeRoot -> BeamSearchPrefixLSLargeRoot (xC_small computed on the device).
 // C0: d x h_vec[0]; C_small: d x sum(h_vec[1..m-1]); outputs cluster_id (n), B_small ((m-1) x n).
+// BuildPrecompLargeRoot + BeamSearchPrefixLSLargeRoot, then (when a is not NULL)
+// DynamicIcmWithIlsAbsNoNormalLargeRoot with the given ICM/ILS settings, as the streaming
+// encode's large-root branch calls them.
 int mirror_large_root(int d, int m, const int* h_vec, const float* C0, const float* C_small, const float* X, int n,
-                      int H_beam, uint32_t* cluster_id, uint8_t* B_small, char* err, int errlen) {
+                      int H_beam, int icm_iters, int ils_iters, uint32_t* cluster_id, uint8_t* B_small, float* a,
+                      float* cost, char* err, int errlen) {
     try {
         s::CodebookPack pack;
         pack.d = d;
@@ -124,6 +128,14 @@ int mirror_large_root(int d, int m, const int* h_vec, const float* C0, const flo
         s::ColMajorMatrix<s::Code> Bs;
         s::BeamSearchLargeRootTiming timing;
         s::BeamSearchPrefixLSLargeRoot(Xm, pre, s::ColMajorMatrix<float>(), H_beam, &cid, &Bs, &timing);
+        if (a) {
+            s::ColMajorMatrix<float> am;
+            std::vector<float> xn2, cst;
+            s::DynamicIcmWithIlsAbsNoNormalLargeRoot(Xm, pre, s::ColMajorMatrix<float>(), icm_iters, ils_iters, 3,
+                                                    38251450u, cid, &Bs, &am, &xn2, &cst, false, 0);
+            std::memcpy(a, am.data.data(), am.data.size() * sizeof(float));
+            std::memcpy(cost, cst.data(), cst.size() * sizeof(float));
+        }
         std::memcpy(cluster_id, cid.data(), cid.size() * sizeof(std::uint32_t));
         std::memcpy(B_small, Bs.data.data(), Bs.data.size());
         return 0;

@@ -33,7 +33,8 @@ def _lib():
                                   _f32p, ctypes.c_char_p, ctypes.c_int]
     lib.mirror_large_root.restype = ctypes.c_int
     lib.mirror_large_root.argtypes = [ctypes.c_int, ctypes.c_int, _i32p, _f32p, _f32p, _f32p, ctypes.c_int,
-                                      ctypes.c_int, _u32p, _u8p, ctypes.c_char_p, ctypes.c_int]
+                                      ctypes.c_int, ctypes.c_int, ctypes.c_int, _u32p, _u8p, _f32p, _f32p,
+                                      ctypes.c_char_p, ctypes.c_int]
     return lib
 
 
@@ -100,12 +101,18 @@ def test_mirror_large_root_matches_oracle(orc):
     Bs = np.empty((n, m - 1), np.uint8)
     err = ctypes.create_string_buffer(512)
     print(f"mirror_large_root n={n} d={d} h0={h0} K={K} m={m} beam={Hb}", flush=True)
-    rc = _lib().mirror_large_root(d, m, _p(h, _i32p), _p(C0, _f32p), _p(Cs, _f32p), _p(X, _f32p), n, Hb,
-                                  _p(cid, _u32p), _p(Bs, _u8p), err, 512)
+    a = np.empty((n, m), np.float32)
+    cost = np.empty(n, np.float32)
+    rc = _lib().mirror_large_root(d, m, _p(h, _i32p), _p(C0, _f32p), _p(Cs, _f32p), _p(X, _f32p), n, Hb, 1, 2,
+                                  _p(cid, _u32p), _p(Bs, _u8p), _p(a, _f32p), _p(cost, _f32p), err, 512)
     assert rc == 0, err.value.decode()
     norm0, Gs, G0S = orc.build_precomp_large_root(C0, Cs)
     nx2 = orc.xnorm2(X)
     xs = orc.gemm_xc(Cs, X, mode=1)
     cid_o, Bs_o, _ = orc.beam_search_large_root(X, nx2, C0, norm0, xs, Gs, G0S, list(h), Hb)
     assert np.array_equal(cid_o, cid)
-    assert np.array_equal(Bs_o, Bs)
+    B_o, a_o, c_o, _ = orc.icm_ils_large_root(X, C0, norm0, xs, Gs, G0S, orc.invnorm_small(Cs), list(h), cid_o, nx2,
+                                              Bs_o, 1, 2, 3, True, 38251450, 0)
+    assert np.array_equal(B_o, Bs)
+    assert np.array_equal(_bits(a_o), _bits(a))
+    assert np.array_equal(_bits(c_o), _bits(cost))
