@@ -159,8 +159,10 @@ int stlq_mi355_encode_device(stlq_mi355_ctx* ctx, const float* dX, int64_t n,
  * through two buffers on a copy stream (double-buffered hipMemcpyAsync) while the previous chunk
  * encodes on the context stream, and the results are handed to `sink` in chunk order.
  *  input_u8: fill writes uint8 vectors (d bytes each) that the device widens to fp32
- *            (ConvertU8ToF32AndRotatePtr with R = I, kernel_provider_cuda_stream_impl.inc:3730+);
+ *            (ConvertU8ToF32AndRotatePtr, kernel_provider_cuda_stream_impl.inc:3730+);
  *            otherwise fp32 (d floats each).
+ *  R:        d x d column-major rotation applied to every vector before the encode, Xblk = R X
+ *            (encode_base_streaming.cpp:817-833, :1367-1390), on fp32 MFMA; NULL for R = I.
  *  large_root: encode with the large-root codebooks (stlq_mi355_set_large_root): the beam of
  *            BeamSearchPrefixLSLargeRoot with root_mode 0 (top-H_beam roots) or 1 (nearest
  *            root); the chunk output then carries cluster_id, B_small and best_err, and, when
@@ -174,6 +176,7 @@ typedef struct stlq_mi355_stream_params {
     int input_u8;
     int large_root;
     int root_mode;
+    const float* R;
 } stlq_mi355_stream_params;
 
 typedef struct stlq_mi355_chunk_out {
@@ -226,6 +229,14 @@ int stlq_mi355_beam_search_large_root(stlq_mi355_ctx* ctx, const float* X, const
                                       int64_t n, int H_beam, const uint32_t* forced_root,
                                       int root_mode, uint32_t* cluster_id, uint8_t* B_small,
                                       float* best_err);
+
+/* StreamKernelProvider::ConvertU8ToF32AndRotatePtr (include/stlq/core/kernel_provider.h:44-52,
+ * CPU version src/core/kernel_provider_cpu.cpp:48-80): out = R * float(in), where in is a
+ * column-major uint8 tile of `rows` x `cols` with column stride ld_in >= rows, R is rows x rows
+ * column-major (NULL: R = I, out = float(in)), and out is rows x cols column-major. Host
+ * buffers; the product runs on fp32 MFMA with a fused k-ascending accumulation. */
+int stlq_mi355_convert_u8_rotate(stlq_mi355_ctx* ctx, const uint8_t* in, int ld_in, int rows, int cols,
+                                 const float* R, float* out);
 
 /* Large-root refit. Layer 0 of vector i is its root cluster_id[i] (< h0); B_small ((m-1) x n)
  * holds layers 1..m-1. X (d x n) host; xC_small (Hs x n) host or NULL (device MFMA GEMM); nx2

@@ -57,6 +57,7 @@ class StreamParams(ctypes.Structure):
         ("input_u8", ctypes.c_int),
         ("large_root", ctypes.c_int),
         ("root_mode", ctypes.c_int),
+        ("R", ctypes.POINTER(ctypes.c_float)),
     ]
 
 
@@ -110,6 +111,7 @@ SIGNATURES = {
     "stlq_mi355_last_timings": ([_vp, ctypes.POINTER(Timings)], _int),
     "stlq_mi355_set_large_root": ([_vp, _int, _int, _i32p, _f32p, _f32p], _int),
     "stlq_mi355_beam_search_large_root": ([_vp, _f32p, _f32p, _i64, _int, _u32p, _int, _u32p, _u8p, _f32p], _int),
+    "stlq_mi355_convert_u8_rotate": ([_vp, _u8p, _int, _int, _int, _f32p, _f32p], _int),
     "stlq_mi355_solve_ls_all_large_root": ([_vp, _f32p, _f32p, _i64, _u32p, _u8p, _f32p, _i64p], _int),
     "stlq_mi355_compute_costs_large_root": ([_vp, _f32p, _f32p, _i64, _u32p, _u8p, _f32p, _f32p, _f32p], _int),
     "stlq_mi355_icm_ils_large_root": ([_vp, _f32p, _f32p, _f32p, _i64, _u32p, _int, _int, _int, _int, ctypes.c_uint32,

@@ -106,6 +106,7 @@ struct stlq_mi355_ctx {
     // Work buffers (grown on demand, reused across calls).
     DevBuf X, nx2, xC, xC_in, codes, a, cost, best, fails, active, changed, mse, gam0, roots, scores, b0;
     DevBuf ils_codes, ils_a, ils_cost;  // ILS candidate state
+    DevBuf R_in, R_rm;                  // rotation: as given (column-major) and row-major
     DevBuf st_rec[2], st_curH[2];
 
     std::vector<TileEvents> tiles;
@@ -552,6 +553,17 @@ int CheckParams(const stlq_mi355_encode_params* p) {
     return CheckBeam(std::max(1, p->H_beam));
 }
 
+// Uploads a d x d column-major rotation and stores it row-major (R(r, k) at [r*d + k]), the
+// operand layout of GemmXcKernel, so that GemmXc(X, R_rm) = R X per vector.
+int UploadRotation(stlq_mi355_ctx* c, const float* R, int d, hipStream_t s) {
+    const size_t bytes = static_cast<size_t>(d) * d * 4;
+    HIP_TRY(c->R_in.Ensure(bytes));
+    HIP_TRY(c->R_rm.Ensure(bytes));
+    HIP_TRY(hipMemcpyAsync(c->R_in.p, R, bytes, hipMemcpyHostToDevice, s));
+    HIP_TRY(LaunchTranspose(c->R_in.as<float>(), d, d, c->R_rm.as<float>(), s));
+    return STLQ_MI355_OK;
+}
+
 double Mean(const std::vector<float>& v) {
     // MeanMseFromPrecomp accumulates in double and clamps each error at 0 (linkage_tools.cpp:170-221).
     double s = 0.0;
@@ -599,7 +611,8 @@ int stlq_mi355_ctx_destroy(stlq_mi355_ctx* c) {
     DevBuf* bufs[] = {&c->C_all, &c->G_rm, &c->G_cm, &c->gdiag, &c->invnorm, &c->C0, &c->Cs, &c->norm0,
                       &c->G_small, &c->G0S, &c->gdiag_small, &c->X, &c->nx2, &c->xC, &c->xC_in, &c->codes, &c->a,
                       &c->cost, &c->best, &c->fails, &c->active, &c->changed, &c->mse, &c->gam0, &c->roots,
-                      &c->scores, &c->ils_codes, &c->ils_a, &c->ils_cost, &c->b0, &c->invnorm_small};
+                      &c->scores, &c->ils_codes, &c->ils_a, &c->ils_cost, &c->b0, &c->invnorm_small,
+                      &c->R_in, &c->R_rm};
     if (c->g_shared) c->G_cm.p = nullptr;
     for (DevBuf* b : bufs) b->Release();
     for (int b = 0; b < 2; ++b) {
@@ -1059,6 +1072,7 @@ int stlq_mi355_encode_stream(stlq_mi355_ctx* c, int64_t n_total, int64_t chunk, 
     const size_t m = static_cast<size_t>(lr ? c->lr_m : c->m);
     const size_t d = static_cast<size_t>(lr ? c->lr_d : c->d);
     const size_t esz = sp->input_u8 ? 1 : 4;
+    if (sp->R) RC_TRY(UploadRotation(c, sp->R, static_cast<int>(d), c->stream));
     chunk = std::min(chunk, n_total);
     const size_t ch = static_cast<size_t>(chunk);
     const bool want = sp->encode.want_coeffs || sp->encode.icm_iters > 0 || sp->encode.ils_iters > 0;
@@ -1070,7 +1084,7 @@ int stlq_mi355_encode_stream(stlq_mi355_ctx* c, int64_t n_total, int64_t chunk, 
         float* hcost = nullptr;
         uint32_t* hcluster = nullptr;
         float* hbest = nullptr;
-        DevBuf din, dX, dcodes, da, dcost, dcluster, dbest;
+        DevBuf din, dX, dXr, dcodes, da, dcost, dcluster, dbest;
         hipEvent_t copied = nullptr, done = nullptr, c0 = nullptr, c1 = nullptr, k0 = nullptr;
         int64_t first = 0, count = 0;
         bool busy = false;
@@ -1088,7 +1102,8 @@ int stlq_mi355_encode_stream(stlq_mi355_ctx* c, int64_t n_total, int64_t chunk, 
             for (void* p : {sl.hin, static_cast<void*>(sl.hcodes), static_cast<void*>(sl.ha), static_cast<void*>(sl.hcost),
                             static_cast<void*>(sl.hcluster), static_cast<void*>(sl.hbest)})
                 if (p) (void)hipHostFree(p);
-            for (DevBuf* b : {&sl.din, &sl.dX, &sl.dcodes, &sl.da, &sl.dcost, &sl.dcluster, &sl.dbest}) b->Release();
+            for (DevBuf* b : {&sl.din, &sl.dX, &sl.dXr, &sl.dcodes, &sl.da, &sl.dcost, &sl.dcluster, &sl.dbest})
+                b->Release();
             for (hipEvent_t e : {sl.copied, sl.done, sl.c0, sl.c1, sl.k0})
                 if (e) (void)hipEventDestroy(e);
         }
@@ -1100,6 +1115,7 @@ int stlq_mi355_encode_stream(stlq_mi355_ctx* c, int64_t n_total, int64_t chunk, 
         bool ok = hmalloc(&sl.hin, ch * d * esz) && hmalloc(reinterpret_cast<void**>(&sl.hcodes), ch * code_b) &&
                   hip_ok(sl.din.Ensure(ch * d * esz), "hipMalloc") && hip_ok(sl.dcodes.Ensure(ch * code_b), "hipMalloc");
         if (ok && sp->input_u8) ok = hip_ok(sl.dX.Ensure(ch * d * 4), "hipMalloc");
+        if (ok && sp->R) ok = hip_ok(sl.dXr.Ensure(ch * d * 4), "hipMalloc");
         if (ok && want)
             ok = hmalloc(reinterpret_cast<void**>(&sl.ha), ch * m * 4) && hmalloc(reinterpret_cast<void**>(&sl.hcost), ch * 4) &&
                  hip_ok(sl.da.Ensure(ch * m * 4), "hipMalloc") && hip_ok(sl.dcost.Ensure(ch * 4), "hipMalloc");
@@ -1169,6 +1185,12 @@ int stlq_mi355_encode_stream(stlq_mi355_ctx* c, int64_t n_total, int64_t chunk, 
         if (sp->input_u8) {
             if (!hip_ok(LaunchU8ToF32(sl.din.as<uint8_t>(), sl.dX.as<float>(), cnt * d, c->stream), "U8ToF32")) break;
             dX = sl.dX.as<float>();
+        }
+        if (sp->R) {  // Xblk = R X (encode_base_streaming.cpp:817-833)
+            if (!hip_ok(LaunchGemmXc(dX, sl.count, static_cast<int>(d), c->R_rm.as<float>(), static_cast<int>(d),
+                                     sl.dXr.as<float>(), static_cast<int64_t>(d), c->stream), "rotation GEMM"))
+                break;
+            dX = sl.dXr.as<float>();
         }
         // Encode the chunk in workspace-bounded tiles (sequential on the context stream).
         const int64_t tile = lr ? LargeRootTileVectors(c, sl.count, Hb, false)
@@ -1566,6 +1588,30 @@ int LargeRootRefit(stlq_mi355_ctx* c, LrOp op, const float* X, const float* nx2,
 }  // namespace
 
 extern "C" {
+
+int stlq_mi355_convert_u8_rotate(stlq_mi355_ctx* c, const uint8_t* in, int ld_in, int rows, int cols, const float* R,
+                                 float* out) {
+    RC_TRY(CheckCtx(c));
+    if (rows < 0 || cols < 0 || ld_in < rows || (rows > 0 && cols > 0 && (!in || !out)))
+        return Fail(STLQ_MI355_ERR_INVALID, "bad arguments");
+    if (rows == 0 || cols == 0) return STLQ_MI355_OK;
+    const size_t r = static_cast<size_t>(rows), n = static_cast<size_t>(cols);
+    hipStream_t s = c->stream;
+    HIP_TRY(c->codes.Ensure(r * n));
+    HIP_TRY(c->X.Ensure(r * n * 4));
+    HIP_TRY(hipMemcpy2DAsync(c->codes.p, r, in, static_cast<size_t>(ld_in), r, n, hipMemcpyHostToDevice, s));
+    HIP_TRY(LaunchU8ToF32(c->codes.as<uint8_t>(), c->X.as<float>(), r * n, s));
+    const float* res = c->X.as<float>();
+    if (R) {
+        RC_TRY(UploadRotation(c, R, rows, s));
+        HIP_TRY(c->xC.Ensure(r * n * 4));
+        HIP_TRY(LaunchGemmXc(c->X.as<float>(), cols, rows, c->R_rm.as<float>(), rows, c->xC.as<float>(), rows, s));
+        res = c->xC.as<float>();
+    }
+    HIP_TRY(hipMemcpyAsync(out, res, r * n * 4, hipMemcpyDeviceToHost, s));
+    HIP_TRY(hipStreamSynchronize(s));
+    return STLQ_MI355_OK;
+}
 
 int stlq_mi355_solve_ls_all_large_root(stlq_mi355_ctx* c, const float* X, const float* xC_small, int64_t n,
                                        const uint32_t* cluster_id, const uint8_t* B_small, float* a,

@@ -250,7 +250,7 @@ class Context:
 
     # ---- streaming -----------------------------------------------------------------------
     def encode_stream(self, n_total, chunk, cfg: EncodeConfig, fill, sink, input_u8=False, large_root=False,
-                      root_mode=1):
+                      root_mode=1, R=None):
         """Streaming encode. fill(first, count, out) fills `out` ((count, d) float32, or uint8 when
         input_u8). sink(first, count, result) receives a dict of numpy copies: full precomp ->
         codes; large root -> cluster_id, B_small, best_err; both with a and cost when coefficients
@@ -300,7 +300,12 @@ class Context:
 
         f, s = _lib.FILL_FN(_fill), _lib.SINK_FN(_sink)
         st = StreamStats()
-        p = _lib.StreamParams(cfg.to_c(), int(bool(input_u8)), int(bool(large_root)), int(root_mode))
+        Rc = None
+        if R is not None:  # numpy (d, d) matrix R[r, k]; the C ABI takes the reference's column-major array
+            Rc = np.ascontiguousarray(np.asarray(R, dtype=np.float32).T)
+            if Rc.shape != (d, d):
+                raise ValueError(f"R must be {d} x {d}")
+        p = _lib.StreamParams(cfg.to_c(), int(bool(input_u8)), int(bool(large_root)), int(root_mode), _p(Rc, _f32p))
         rc = self.lib.stlq_mi355_encode_stream(self.h, int(n_total), int(chunk), ctypes.byref(p), f, s, None,
                                                ctypes.byref(st))
         if err:
@@ -331,6 +336,16 @@ class Context:
                                                          _p(fr, _u32p), int(root_mode), _p(cid, _u32p), _p(Bs, _u8p),
                                                          _p(err, _f32p)))
         return cid, Bs, err
+
+    def convert_u8_rotate(self, X_u8, R=None):
+        """ConvertU8ToF32AndRotatePtr (kernel_provider.h:44-52) on row-major (n, d) uint8 vectors:
+        returns float32 (n, d) with row i = R @ x_i (R a numpy (d, d) matrix; None = identity)."""
+        X_u8 = np.ascontiguousarray(X_u8, dtype=np.uint8)
+        n, d = X_u8.shape
+        Rc = np.ascontiguousarray(np.asarray(R, dtype=np.float32).T) if R is not None else None
+        out = np.empty((n, d), np.float32)
+        check(self.lib.stlq_mi355_convert_u8_rotate(self.h, _p(X_u8, _u8p), d, d, n, _p(Rc, _f32p), _p(out, _f32p)))
+        return out
 
     def _lr_inputs(self, X, cluster_id, B_small, xC_small):
         X = _c(X, np.float32)

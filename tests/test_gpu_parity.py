@@ -554,3 +554,100 @@ def test_stream_large_root_refit(ctx, orc, icm, ils):
     assert np.array_equal(got["B_small"], B_o)
     assert np.array_equal(_bits(got["a"]), _bits(a_o))
     assert np.array_equal(_bits(got["cost"]), _bits(c_o))
+
+
+def _orthogonal(d, seed):
+    q, r = np.linalg.qr(np.random.default_rng(seed).standard_normal((d, d)))
+    return (q * np.sign(np.diag(r))).astype(np.float32)
+
+
+@pytest.mark.parametrize("d", [96, 100, 128])
+def test_convert_u8_rotate(ctx, orc, d):
+    """ConvertU8ToF32AndRotatePtr (kernel_provider.h:44-52): widening is exact; R X on the MFMA
+    GEMM equals the oracle's fused k-ascending product bit for bit (the reference's BLAS order is
+    unpinned); R = I returns the widened input unchanged; a column stride ld_in > d is honoured."""
+    import ctypes
+
+    from stlq_amd import _lib
+
+    rng = np.random.default_rng(d)
+    Xu8 = rng.integers(0, 256, (3001, d), dtype=np.uint8)
+    Xf = Xu8.astype(np.float32)
+    assert np.array_equal(_bits(ctx.convert_u8_rotate(Xu8)), _bits(Xf))
+    assert np.array_equal(_bits(ctx.convert_u8_rotate(Xu8, np.eye(d, dtype=np.float32))), _bits(Xf))
+    R = _orthogonal(d, d + 1)
+    got = ctx.convert_u8_rotate(Xu8, R)
+    assert np.array_equal(_bits(got), _bits(orc.gemm_xc(R, Xf, mode=1)))
+    ld = d + 7
+    padded = np.zeros((Xu8.shape[0], ld), np.uint8)
+    padded[:, :d] = Xu8
+    out = np.empty_like(Xf)
+    Rc = np.ascontiguousarray(R.T)
+    _lib.check(ctx.lib.stlq_mi355_convert_u8_rotate(ctx.h, padded.ctypes.data_as(ctypes.POINTER(ctypes.c_uint8)), ld, d,
+                                                    Xu8.shape[0], Rc.ctypes.data_as(ctypes.POINTER(ctypes.c_float)),
+                                                    out.ctypes.data_as(ctypes.POINTER(ctypes.c_float))))
+    assert np.array_equal(_bits(out), _bits(got))
+
+
+def test_stream_rotation_full_precomp(ctx, orc):
+    """EncodeBaseStreamingF32 with a rotation (encode_base_streaming.cpp:1367-1390): every chunk is
+    rotated on the device before the encode; identical to the in-memory encode of the oracle-
+    rotated vectors. R = I gives the unrotated stream's results."""
+    X, C = rvq_problem(95, 5000, 64, 4, 64, kind="desc", train_n=2000, iters=3)
+    h = [64] * 4
+    ctx.set_codebooks(C, h)
+    R = _orthogonal(64, 7)
+    cfg = EncodeConfig(H_beam=4, icm_iters=1, ils_iters=1, want_coeffs=True)
+    Xr = orc.gemm_xc(R, X, mode=1)
+    codes, a, cost, _ = ctx.encode(Xr, cfg)
+
+    def run(Rm):
+        got = {"codes": np.zeros_like(codes), "a": np.zeros_like(a), "cost": np.zeros_like(cost)}
+
+        def fill(first, count, out):
+            out[:] = X[first:first + count]
+
+        def sink(first, count, res):
+            for k in got:
+                got[k][first:first + count] = res[k]
+
+        ctx.encode_stream(X.shape[0], 1800, cfg, fill, sink, R=Rm)
+        return got
+
+    g = run(R)
+    assert np.array_equal(g["codes"], codes)
+    assert np.array_equal(_bits(g["a"]), _bits(a))
+    assert np.array_equal(_bits(g["cost"]), _bits(cost))
+    g_id, g_none = run(np.eye(64, dtype=np.float32)), run(None)
+    for k in g_id:  # byte-for-byte equal
+        assert np.array_equal(np.ascontiguousarray(g_id[k]).view(np.uint8), np.ascontiguousarray(g_none[k]).view(np.uint8))
+
+
+def test_stream_rotation_large_root_u8(ctx, orc):
+    """EncodeBaseStreaming's uint8 path with a rotation (encode_base_streaming.cpp:817-833): widen,
+    rotate, large-root beam and refit; identical to the in-memory large-root encode of the
+    oracle-rotated vectors."""
+    m, n = 5, 3000
+    p = _lr_refit_problem(ctx, orc, m, 611, n=n, d=64, h0=1024, K=64)
+    Xu8 = np.clip(np.rint(p["X"]), 0, 255).astype(np.uint8)
+    R = _orthogonal(64, 11)
+    Xr = orc.gemm_xc(R, Xu8.astype(np.float32), mode=1)
+    cid, Bs, err = ctx.beam_search_large_root(Xr, 8, root_mode=1)
+    B_g, a_g, c_g = ctx.icm_ils_large_root(Xr, cid, Bs, 0, 0, 3, True, 38251450)
+    got = {"cluster_id": np.zeros_like(cid), "B_small": np.zeros_like(Bs), "best_err": np.zeros_like(err),
+           "a": np.zeros_like(a_g), "cost": np.zeros_like(c_g)}
+
+    def fill(first, count, out):
+        out[:] = Xu8[first:first + count]
+
+    def sink(first, count, res):
+        for k in got:
+            got[k][first:first + count] = res[k]
+
+    cfg = EncodeConfig(H_beam=8, icm_iters=0, want_coeffs=True)
+    ctx.encode_stream(n, 1100, cfg, fill, sink, input_u8=True, large_root=True, root_mode=1, R=R)
+    assert np.array_equal(got["cluster_id"], cid)
+    assert np.array_equal(got["B_small"], B_g)
+    assert np.array_equal(_bits(got["best_err"]), _bits(err))
+    assert np.array_equal(_bits(got["a"]), _bits(a_g))
+    assert np.array_equal(_bits(got["cost"]), _bits(c_g))
