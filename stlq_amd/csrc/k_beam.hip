@@ -100,31 +100,49 @@ __device__ __forceinline__ float FromOrderBits(uint32_t o) {
     return __uint_as_float((o & 0x80000000u) ? (o & 0x7FFFFFFFu) : ~o);
 }
 
-// Selection state of one vector's streaming top-H (beam_search.cpp:301-333).
-//  Fast path: lane q (< Hb) holds one slot's 64-bit key [OrderBits(err) | 63-slot (6 bits) |
-//    candidate (26 bits)], kept in descending key order. A larger key is the slot RecomputeWorst
-//    (beam_search.cpp:101-113) would pick first: larger error, and among equal errors the lower
-//    slot. Lane 0 is therefore the worst slot, and an insertion is a rank (one 64-bit compare and
-//    a ballot), a one-lane shift of the keys above the rank, and a select.
-//  s_err/s_cand (slot h in lane h) are rebuilt from the keys when the fast path ends (ToSlots).
-//  A NaN or -0 candidate that would enter switches the vector to `slow` for the rest of the
-//  layer: slot arrays with a first-max scan that follows the reference's NaN comparisons.
+// Streaming top-H of one vector (beam_search.cpp:301-333), in two forms.
+//  TopKeys (fast path): lane q (< Hb) holds one slot's 64-bit key [image(err) | 63-slot
+//    (6 bits) | candidate (26 bits)], kept in descending key order. A larger key is the slot
+//    RecomputeWorst (beam_search.cpp:101-113) would pick first: larger error, and among equal
+//    errors the lower slot. Lane 0 is therefore the worst slot, and an insertion is a rank (one
+//    64-bit compare and a ballot), a one-lane shift of the keys above the rank, and a select.
+//    Valid while no eligible candidate is NaN or -0. The error image is OrderBits, or, where
+//    the errors are clamped at zero (layers >= 1: never negative), the float bits themselves,
+//    which order non-negative floats as unsigned integers.
+//  TopSlots (slow path): slot h in lane h with the reference's first-max RecomputeWorst scan and
+//    its NaN comparisons. A layer whose candidates include an eligible NaN or -0 is replayed from
+//    its start on this path.
 constexpr uint32_t kNoCand = (1u << 26) - 1u;
 
-struct TopH {
+template <bool kNonNeg>
+__device__ __forceinline__ uint32_t KeyImage(float e) {
+    return kNonNeg ? __float_as_uint(e) : OrderBits(e);
+}
+template <bool kNonNeg>
+__device__ __forceinline__ float KeyError(uint32_t o) {
+    return kNonNeg ? __uint_as_float(o) : FromOrderBits(o);
+}
+
+template <bool kNonNeg>
+struct TopKeys {
     uint64_t key;
-    uint32_t whi, wlo;  // key of lane 0 (the worst slot) while on the fast path
-    float worst = __builtin_huge_valf();
-    int widx = 0;
-    bool slow = false;
-    float s_err = __builtin_huge_valf();
-    int s_cand = -1;
-    __device__ explicit TopH(int lane)
-        : key((static_cast<uint64_t>(OrderBits(__builtin_huge_valf())) << 32) |
+    uint32_t whi, wlo;  // key of lane 0 (the worst slot)
+    __device__ explicit TopKeys(int lane)
+        : key((static_cast<uint64_t>(KeyImage<kNonNeg>(__builtin_huge_valf())) << 32) |
               (static_cast<uint64_t>(63 - lane) << 26) | kNoCand),
-          whi(OrderBits(__builtin_huge_valf())),
+          whi(KeyImage<kNonNeg>(__builtin_huge_valf())),
           wlo((63u << 26) | kNoCand) {}
 };
+
+struct TopSlots {
+    float s_err = __builtin_huge_valf();
+    int s_cand = -1;
+    float worst = __builtin_huge_valf();
+    int widx = 0;
+};
+
+// Lanes l+1..63.
+__device__ __forceinline__ uint64_t AboveLane(int l) { return l >= 63 ? 0ull : (~0ull << (l + 1)); }
 
 // Lane i receives lane i+1's value across the whole wave (DPP wave_shl:1); lane 63 keeps its own.
 // (bound_ctrl: lane 63 reads 0; callers never take lane 63's value.)
@@ -134,53 +152,33 @@ __device__ __forceinline__ uint64_t WaveShl1(uint64_t v) {
     return (static_cast<uint64_t>(static_cast<uint32_t>(hi)) << 32) | static_cast<uint32_t>(lo);
 }
 
-// Slot-indexed view of the sorted keys: lane h receives the error and candidate of slot h; the
-// worst slot as RecomputeWorst names it.
-__device__ __forceinline__ void ToSlots(TopH& t) {
-    t.worst = FromOrderBits(t.whi);
-    t.widx = 63 - static_cast<int>(t.wlo >> 26);
+// Slot-indexed view of the sorted keys: lane h receives the error and candidate of slot h.
+template <bool kNonNeg>
+__device__ __forceinline__ void ToSlots(const TopKeys<kNonNeg>& t, float& s_err, int& s_cand) {
     const uint32_t lo = static_cast<uint32_t>(t.key);
     const int slot = 63 - static_cast<int>((lo >> 26) & 63u);
     const uint32_t c = lo & kNoCand;
-    const float err = FromOrderBits(static_cast<uint32_t>(t.key >> 32));
-    t.s_err = __int_as_float(__builtin_amdgcn_ds_permute(slot << 2, __float_as_int(err)));
+    const float err = KeyError<kNonNeg>(static_cast<uint32_t>(t.key >> 32));
+    s_err = __int_as_float(__builtin_amdgcn_ds_permute(slot << 2, __float_as_int(err)));
     const int cand = __builtin_amdgcn_ds_permute(slot << 2, static_cast<int>(c));
-    t.s_cand = cand == static_cast<int>(kNoCand) ? -1 : cand;
-}
-
-// Ends the fast path of a layer (no-op after a switch to the slow path).
-__device__ __forceinline__ void Finish(TopH& t) {
-    if (!t.slow) ToSlots(t);
+    s_cand = cand == static_cast<int>(kNoCand) ? -1 : cand;
 }
 
 // Replays the streaming top-H over one chunk of 64 candidates in lane (= scan) order.
 // Candidate `lane` is eligible when ok; it is inserted when !(e >= worst)
 // (beam_search.cpp:320: `if (e >= worst_err) continue;`), into the worst slot.
 // cand_base + lane must stay below 2^26 - 1 (callers check).
-__device__ __forceinline__ void ReplayChunk(bool ok, float e, int cand_base, int Hb, int rows, int lane, TopH& t) {
+//
+// Fast path: returns false, leaving t as it was, when an eligible candidate is NaN or -0 (the
+// caller then replays the layer with ReplaySlow). Otherwise e < worst exactly when
+// image(e) < image(worst). With kNonNeg the errors are +0..+inf, NaN or -0, and NaN and -0 are
+// exactly the bit patterns above +inf's.
+template <bool kNonNeg>
+__device__ __forceinline__ bool ReplayFast(bool ok, float e, int cand_base, int Hb, int lane, TopKeys<kNonNeg>& t) {
     const uint64_t okm = Ballot(ok);
-    if (!okm) return;
-    // NaN (either kind) or -0 among the candidates: leave the key order (NaN always enters)
-    if (!t.slow && (Ballot(__builtin_amdgcn_class(e, 0x23)) & okm) != 0ull) {
-        ToSlots(t);
-        t.slow = true;
-    }
-    if (t.slow) {
-        uint64_t mask = okm & Ballot(!(e >= t.worst));
-        while (mask) {
-            const int l = static_cast<int>(__builtin_ctzll(mask));
-            const float ev = ReadLane(e, l);
-            if (lane == t.widx) {
-                t.s_err = ev;
-                t.s_cand = cand_base + l;
-            }
-            RecomputeWorst(t.s_err, Hb, rows, lane, t.worst, t.widx);
-            mask = (mask & (mask - 1ull)) & Ballot(!(e >= t.worst));
-        }
-        return;
-    }
-    // Without NaN and -0, e < worst exactly when OrderBits(e) < OrderBits(worst).
-    const uint32_t oe = OrderBits(e);
+    const bool bad = kNonNeg ? (__float_as_uint(e) > 0x7F800000u) : __builtin_amdgcn_classf(e, 0x23);
+    if ((Ballot(bad) & okm) != 0ull) return false;
+    const uint32_t oe = KeyImage<kNonNeg>(e);
     uint64_t mask = okm & Ballot(oe < t.whi);
     // lanes 1..Hb-1 of the sorted keys: the ones that stay when lane 0 (the worst) is evicted
     const uint64_t keep = (Hb >= 64 ? ~0ull : ((1ull << Hb) - 1ull)) & ~1ull;
@@ -195,8 +193,54 @@ __device__ __forceinline__ void ReplayChunk(bool ok, float e, int cand_base, int
         t.key = lane < r ? sh : (lane == r ? nk : t.key);
         t.whi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(t.key >> 32), 0));
         t.wlo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(t.key), 0));
-        mask = (mask ^ (1ull << l)) & Ballot(oe < t.whi);
+        mask = okm & AboveLane(l) & Ballot(oe < t.whi);
     }
+    return true;
+}
+
+// Slow path: the reference's scan on slot arrays (NaN enters; RecomputeWorst after each insert).
+// The worst can rise here (to NaN), so the eligible lanes after an insertion are re-tested from
+// all ok lanes behind it, not only from the ones that were eligible before.
+__device__ __forceinline__ void ReplaySlow(bool ok, float e, int cand_base, int Hb, int rows, int lane, TopSlots& t) {
+    const uint64_t okm = Ballot(ok);
+    uint64_t mask = okm & Ballot(!(e >= t.worst));
+    while (mask) {
+        const int l = static_cast<int>(__builtin_ctzll(mask));
+        const float ev = ReadLane(e, l);
+        if (lane == t.widx) {
+            t.s_err = ev;
+            t.s_cand = cand_base + l;
+        }
+        RecomputeWorst(t.s_err, Hb, rows, lane, t.worst, t.widx);
+        mask = okm & AboveLane(l) & Ballot(!(e >= t.worst));
+    }
+}
+
+// Runs `chunks(replay)` with the fast replay and, if it reports a NaN or -0, again from the start
+// with the slow one; returns the slot-indexed (error, candidate) of the final top-H.
+// chunks(replay) must call replay(ok, e, cand_base) for every chunk in scan order, stop and return
+// false as soon as a call returns false, and return true otherwise.
+// The second argument of chunks is std::false_type on the fast pass and std::true_type on the
+// slow one.
+template <bool kNonNeg, class Chunks>
+__device__ __forceinline__ void SelectTopH(int Hb, int lane, Chunks&& chunks, float& s_err, int& s_cand) {
+    TopKeys<kNonNeg> tk(lane);
+    const bool fast = chunks([&](bool ok, float e, int cand_base) { return ReplayFast(ok, e, cand_base, Hb, lane, tk); },
+                             std::false_type());
+    if (fast) {
+        ToSlots(tk, s_err, s_cand);
+        return;
+    }
+    TopSlots ts;
+    const int rows = (Hb + 15) >> 4;
+    chunks(
+        [&](bool ok, float e, int cand_base) {
+            ReplaySlow(ok, e, cand_base, Hb, rows, lane, ts);
+            return true;
+        },
+        std::true_type());
+    s_err = ts.s_err;
+    s_cand = ts.s_cand;
 }
 
 // BestSlot (beam_search.cpp:409-416): first minimum over slots [0, curH) with strict '<'.
@@ -297,26 +341,29 @@ __global__ __launch_bounds__(256) void Layer0Kernel(LayerArgs p) {
     const int64_t i = static_cast<int64_t>(blockIdx.x) * kBeamWavesPerBlock + wave;
     if (i >= p.n) return;
     const int m = p.m, Hb = p.Hb, K = p.K, off0 = p.offL;
-    const int rows = (Hb + 15) >> 4;
     const Rec rc(m);
     const float nx2 = p.nx2[i];
     const float* xCi = p.xC + i * p.ldx;
 
-    TopH top(lane);
     const int nch = (K + kWave - 1) / kWave;
-    for (int j = 0; j < nch; ++j) {
-        const int k = lane + kWave * j;
-        const bool act = k < K;
-        const float alpha = act ? p.gdiag[off0 + k] : 0.0f;
-        const bool ok = act && alpha != 0.0f;
-        const float gamma = act ? xCi[off0 + k] : 0.0f;
-        const float a1 = gamma / alpha;
-        const float e1 = nx2 - gamma * a1;
-        ReplayChunk(ok, e1, kWave * j, Hb, rows, lane, top);
-    }
-    Finish(top);
-    const float s_err = top.s_err;
-    const int s_cand = top.s_cand;
+    float s_err;
+    int s_cand;
+    SelectTopH<false>(
+        Hb, lane,
+        [&](auto&& replay, auto) {
+            for (int j = 0; j < nch; ++j) {
+                const int k = lane + kWave * j;
+                const bool act = k < K;
+                const float alpha = act ? p.gdiag[off0 + k] : 0.0f;
+                const bool ok = act && alpha != 0.0f;
+                const float gamma = act ? xCi[off0 + k] : 0.0f;
+                const float a1 = gamma / alpha;
+                const float e1 = nx2 - gamma * a1;
+                if (!replay(ok, e1, kWave * j)) return false;
+            }
+            return true;
+        },
+        s_err, s_cand);
 
     const int curH = __popcll(__ballot(lane < Hb && s_err < kInfF));  // CountFinite, no max(1,.)
     // Insertion-time write-back of the surviving slot contents (beam_search.cpp:253-258).
@@ -357,7 +404,6 @@ __global__ __launch_bounds__(256) void LayerKernel(LayerArgs p) {
     const int64_t i = static_cast<int64_t>(blockIdx.x) * kBeamWavesPerBlock + wave;
     if (i >= p.n) return;
     const int m = p.m, Hb = p.Hb, K = FULL ? kMaxK : p.K, offL = p.offL;
-    const int rows = (Hb + 15) >> 4;
     const Rec rc(m);
     const int ld = p.gram.ld;
     const float* xCi = p.xC + i * p.ldx;
@@ -375,7 +421,6 @@ __global__ __launch_bounds__(256) void LayerKernel(LayerArgs p) {
         alp[j] = act ? p.gdiag[offL + k] : 0.0f;
     }
 
-    TopH top(lane);
     const int curH = p.in.curH[i];
 
     // Beam slot h's codes (and root) sit in lane h, read with one vector load per word for all
@@ -414,7 +459,9 @@ __global__ __launch_bounds__(256) void LayerKernel(LayerArgs p) {
         }
     };
     // Evaluates slot h's candidates and replays them into the top-H (scan order: slot, then code).
-    auto process = [&](int h, const float (&A)[kMaxChunks][L]) {
+    // Returns false when the replay asks for the slow pass.
+    auto process = [&](int h, const float (&A)[kMaxChunks][L], auto&& replay, auto slow_tag) -> bool {
+        constexpr bool kSlow = decltype(slow_tag)::value;
         const float* rec = recs_in + h * rc.stride;
         const float E_old = rec[0];
         float aold[L];
@@ -453,6 +500,8 @@ __global__ __launch_bounds__(256) void LayerKernel(LayerArgs p) {
         bool safe = true;
         if (LR) {
             eval_all(std::integral_constant<int, 2>(), safe);
+        } else if (kSlow) {  // the rare slow pass: IEEE division only (same quotients)
+            eval_all(std::integral_constant<int, 0>(), safe);
         } else if (diag_fast) {
             eval_all(std::integral_constant<int, 1>(), safe);
             // A numerator left the range where the reciprocal-corrected quotient is exact:
@@ -463,18 +512,26 @@ __global__ __launch_bounds__(256) void LayerKernel(LayerArgs p) {
         }
 #pragma unroll
         for (int j = 0; j < kMaxChunks; ++j) {
-            if (FULL || j < nch) ReplayChunk(okc[j], ech[j], h * K + kWave * j, Hb, rows, lane, top);
+            if (FULL || j < nch) {
+                if (!replay(okc[j], ech[j], h * K + kWave * j)) return false;
+            }
         }
+        return true;
     };
 
-    for (int h = 0; h < curH; ++h) {
-        float A[kMaxChunks][L];
-        load_rows(h, A);
-        process(h, A);
-    }
-    Finish(top);
-    const float s_err = top.s_err;
-    const int s_cand = top.s_cand;
+    float s_err;
+    int s_cand;
+    SelectTopH<true>(  // errors clamped at zero (EvalCand)
+        Hb, lane,
+        [&](auto&& replay, auto slow_tag) {
+            for (int h = 0; h < curH; ++h) {
+                float A[kMaxChunks][L];
+                load_rows(h, A);
+                if (!process(h, A, replay, slow_tag)) return false;
+            }
+            return true;
+        },
+        s_err, s_cand);
 
     // Deferred write-back (beam_search.cpp:337-383) or the all-skipped fallback (:385-400).
     const int newH = __popcll(__ballot(lane < Hb && s_err < kInfF));
@@ -621,7 +678,6 @@ __global__ __launch_bounds__(256) void RootSeedKernel(RootArgs p) {
     const int64_t i = static_cast<int64_t>(blockIdx.x) * kBeamWavesPerBlock + wave;
     if (i >= p.n) return;
     const int m = p.m, Hb = p.Hb, rs = p.root_slots;
-    const int rows = (rs + 15) >> 4;
     const Rec rc(m);
     const float nx2 = p.nx2[i];
     float s_err = kInfF;
@@ -638,21 +694,23 @@ __global__ __launch_bounds__(256) void RootSeedKernel(RootArgs p) {
             }
         }
     } else {
-        TopH top(lane);
         const float* sc = p.scores + i * p.ldx;
-        for (int c0 = 0; c0 < p.h0; c0 += kWave) {
-            const int code = c0 + lane;
-            const bool act = code < p.h0;
-            const float alpha = act ? p.norm0[code] : 0.0f;
-            const bool ok = act && alpha != 0.0f;
-            const float gamma = act ? sc[code] : 0.0f;
-            const float a1 = gamma / alpha;
-            const float e1 = nx2 - gamma * a1;
-            ReplayChunk(ok, e1, c0, rs, rows, lane, top);
-        }
-        Finish(top);
-        s_err = top.s_err;
-        s_cand = top.s_cand;
+        SelectTopH<false>(
+            rs, lane,
+            [&](auto&& replay, auto) {
+                for (int c0 = 0; c0 < p.h0; c0 += kWave) {
+                    const int code = c0 + lane;
+                    const bool act = code < p.h0;
+                    const float alpha = act ? p.norm0[code] : 0.0f;
+                    const bool ok = act && alpha != 0.0f;
+                    const float gamma = act ? sc[code] : 0.0f;
+                    const float a1 = gamma / alpha;
+                    const float e1 = nx2 - gamma * a1;
+                    if (!replay(ok, e1, c0)) return false;
+                }
+                return true;
+            },
+            s_err, s_cand);
     }
     const bool seeded = lane < rs && !(s_err >= kInfF);
     const int curH = max(1, __popcll(__ballot(seeded)));

@@ -92,7 +92,7 @@ def beam_case(seed, n, d, h, kind):
 
 
 DEGENERATE = ["dup_within_layer", "dup_across_layers", "zero_codeword", "zero_layer", "zero_root_layer",
-              "tiny_codebook", "scaled_copies"]
+              "tiny_codebook", "scaled_copies", "nan_codeword"]
 
 
 def degenerate_problem(case):
@@ -123,6 +123,15 @@ def degenerate_problem(case):
     elif case == "scaled_copies":
         C[12 + 3] = 2.0 * C[1]
         C[24 + 6] = -0.5 * C[12 + 8]
+    elif case == "nan_codeword":
+        # Layer-2 code 7 and layer-3 code 2 give NaN candidate errors (NaN and inf Gram entries);
+        # a NaN enters the beam (NaN >= worst is false) and pins RecomputeWorst while finite
+        # candidates keep the beam alive. Zero vectors add exact ties at error 0. (Vectors whose
+        # whole beam turns non-finite reach the all-skipped fallback, which reads the reference's
+        # stale per-thread workspace, so no case here produces them.)
+        C[24 + 7, 1] = np.nan
+        C[36 + 2, 4] = np.inf
+        X[38:45] = 0
     return X, C, h
 
 

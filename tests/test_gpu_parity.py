@@ -90,7 +90,9 @@ def test_beam_degenerate_bit_exact(ctx, orc, case):
         codes_o, err_o = orc.beam_search(nx2, xC, G, h, Hb)
         codes_g, err_g = ctx.beam_search(xC, Hb, nx2=nx2)
         assert np.array_equal(codes_o, codes_g), (case, Hb)
-        assert np.array_equal(_bits(err_o), _bits(err_g)), (case, Hb)
+        # bit for bit, except that a NaN's payload is the platform's (x86 and gfx950 differ)
+        same = (_bits(err_o) == _bits(err_g)) | (np.isnan(err_o) & np.isnan(err_g))
+        assert np.all(same), (case, Hb, np.nonzero(~same)[0][:10])
 
 
 def test_beam_user_precomp_nonsymmetric(ctx, orc):
