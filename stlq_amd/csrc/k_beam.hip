@@ -397,8 +397,17 @@ __global__ __launch_bounds__(256) void Layer0Kernel(LayerArgs p) {
 
 // Layers L >= 1. LR selects the large-root cross-term source and reciprocal solves.
 // FULL: the layer has exactly 256 codewords (no partial chunk).
+// Minimum waves per SIMD requested from the register allocator, per layer: measured on the
+// M=8, K=256, beam-16 encode, where layer 4 runs best at 8 waves and layers 5 and 7 at 7 (the
+// others, and the large-root layers, at the allocator's own choice).
+template <int L, bool LR>
+constexpr int LayerMinWaves() {
+    return LR ? 1 : (L == 4 ? 8 : ((L == 5 || L == 7) ? 7 : 1));
+}
+
 template <int L, bool LR, bool FULL>
-__global__ __launch_bounds__(256) void LayerKernel(LayerArgs p) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LayerMinWaves<L, LR>(), 8))) void LayerKernel(
+    LayerArgs p) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const int64_t i = static_cast<int64_t>(blockIdx.x) * kBeamWavesPerBlock + wave;
