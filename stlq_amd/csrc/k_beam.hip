@@ -397,12 +397,15 @@ __global__ __launch_bounds__(256) void Layer0Kernel(LayerArgs p) {
 
 // Layers L >= 1. LR selects the large-root cross-term source and reciprocal solves.
 // FULL: the layer has exactly 256 codewords (no partial chunk).
-// Minimum waves per SIMD requested from the register allocator, per layer: measured on the
-// M=8, K=256, beam-16 encode, where layer 4 runs best at 8 waves and layers 5 and 7 at 7 (the
-// others, and the large-root layers, at the allocator's own choice).
+// Minimum waves per SIMD requested from the register allocator, per layer (measured):
+//  * layers >= 11 at 4 waves (<= 128 VGPRs): left alone the allocator gives them 2-3 waves, or
+//    1 at layer 16 (> 256 VGPRs); the M=16, beam-8 encode ran 9% faster and the large-root
+//    16-layer beam-32 encode 18% faster;
+//  * on the M=8, K=256, beam-16 encode layer 4 runs best at 8 waves and layers 5 and 7 at 7;
+//  * the other layers at the allocator's own choice.
 template <int L, bool LR>
 constexpr int LayerMinWaves() {
-    return LR ? 1 : (L == 4 ? 8 : ((L == 5 || L == 7) ? 7 : 1));
+    return L >= 11 ? 4 : (LR ? 1 : (L == 4 ? 8 : ((L == 5 || L == 7) ? 7 : 1)));
 }
 
 template <int L, bool LR, bool FULL>
