@@ -25,7 +25,9 @@ struct Staged {
 };
 
 // Loads this thread's share of a 128 x 16 slice (2 rows x 4 consecutive k) of a K-contiguous
-// matrix with `rows` rows and row length d.
+// matrix with `rows` rows and row length d. kInterior: the tile is known to lie inside the matrix
+// and d is a multiple of 16, so every load is an unconditional float4 (no exec-mask branches).
+template <bool kInterior>
 __device__ __forceinline__ void LoadSlice(const float* __restrict__ M, int64_t rows, int d, int64_t r0,
                                           int k0, bool vec4, Staged& st) {
     const int t = threadIdx.x;
@@ -34,7 +36,7 @@ __device__ __forceinline__ void LoadSlice(const float* __restrict__ M, int64_t r
     for (int q = 0; q < 2; ++q) {
         const int64_t row = r0 + (t >> 2) + 64 * q;
         const int k = k0 + 4 * quad;
-        if (row < rows && vec4 && k + 3 < d) {
+        if (kInterior || (row < rows && vec4 && k + 3 < d)) {
             const float4 x = *reinterpret_cast<const float4*>(M + row * d + k);
             st.v[q][0] = x.x;
             st.v[q][1] = x.y;
@@ -59,30 +61,18 @@ __device__ __forceinline__ void StoreSlice(float (*S)[kLdsStride], const Staged&
     }
 }
 
-__global__ __launch_bounds__(256) void GemmXcKernel(const float* __restrict__ X, int64_t n, int d,
-                                                     const float* __restrict__ C, int H,
-                                                     float* __restrict__ xC, int64_t ldx,
-                                                     int tiles_h, int64_t tiles_total,
-                                                     int64_t per_xcd) {
-    __shared__ float As[2][kBM][kLdsStride];
-    __shared__ float Bs[2][kBN][kLdsStride];
-
-    // XCD-aware tile order: workgroups are dispatched round-robin over the 8 XCDs, so block b
-    // runs on XCD b % 8. Give each XCD a contiguous run of tiles so the 128-vector slices of X
-    // that neighbouring codeword tiles share stay in that XCD's L2.
-    const int64_t b = blockIdx.x;
-    const int64_t tile = (b & 7) * per_xcd + (b >> 3);
-    if (tile >= tiles_total) return;
-    const int64_t tx = tile / tiles_h;
-    const int th = static_cast<int>(tile - tx * tiles_h);
-    const int64_t i0 = tx * kBM;
-    const int64_t h0 = static_cast<int64_t>(th) * kBN;
+// One 128 x 128 output tile; kInterior as for LoadSlice (and no bounds checks on the stores).
+template <bool kInterior>
+__device__ __forceinline__ void GemmTile(const float* __restrict__ X, int64_t n, int d, const float* __restrict__ C,
+                                         int H, float* __restrict__ xC, int64_t ldx, int64_t i0, int64_t h0,
+                                         float (*As)[kBM][kLdsStride], float (*Bs)[kBN][kLdsStride]) {
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int wm = wave >> 1, wn = wave & 1;
     const int g = lane >> 4, r16 = lane & 15;
-    const bool vec4 = (d & 3) == 0;
+    // float4 loads need 16-byte aligned rows: d % 4 == 0 and 16-byte aligned bases
+    const bool vec4 = (d & 3) == 0 && ((reinterpret_cast<uintptr_t>(X) | reinterpret_cast<uintptr_t>(C)) & 15u) == 0;
 
     floatx4 acc[4][4];
 #pragma unroll
@@ -92,8 +82,8 @@ __global__ __launch_bounds__(256) void GemmXcKernel(const float* __restrict__ X,
 
     const int nk = (d + kBK - 1) / kBK;
     Staged sa, sb;
-    LoadSlice(X, n, d, i0, 0, vec4, sa);
-    LoadSlice(C, H, d, h0, 0, vec4, sb);
+    LoadSlice<kInterior>(X, n, d, i0, 0, vec4, sa);
+    LoadSlice<kInterior>(C, H, d, h0, 0, vec4, sb);
     StoreSlice(As[0], sa);
     StoreSlice(Bs[0], sb);
     __syncthreads();
@@ -102,8 +92,8 @@ __global__ __launch_bounds__(256) void GemmXcKernel(const float* __restrict__ X,
         const int cur = kt & 1;
         const bool more = kt + 1 < nk;
         if (more) {
-            LoadSlice(X, n, d, i0, (kt + 1) * kBK, vec4, sa);
-            LoadSlice(C, H, d, h0, (kt + 1) * kBK, vec4, sb);
+            LoadSlice<kInterior>(X, n, d, i0, (kt + 1) * kBK, vec4, sa);
+            LoadSlice<kInterior>(C, H, d, h0, (kt + 1) * kBK, vec4, sb);
         }
         floatx4 af[4], bf[4];
 #pragma unroll
@@ -132,14 +122,42 @@ __global__ __launch_bounds__(256) void GemmXcKernel(const float* __restrict__ X,
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int64_t row = i0 + wm * 64 + a * 16 + 4 * g + r;
-            if (row >= n) continue;
+            if (!kInterior && row >= n) continue;
             float* dst = xC + row * ldx;
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
                 const int64_t col = h0 + wn * 64 + c * 16 + r16;
-                if (col < H) dst[col] = acc[a][c][r];
+                if (kInterior || col < H) dst[col] = acc[a][c][r];
             }
         }
+    }
+}
+
+__global__ __launch_bounds__(256) void GemmXcKernel(const float* __restrict__ X, int64_t n, int d,
+                                                     const float* __restrict__ C, int H,
+                                                     float* __restrict__ xC, int64_t ldx,
+                                                     int tiles_h, int64_t tiles_total,
+                                                     int64_t per_xcd) {
+    __shared__ float As[2][kBM][kLdsStride];
+    __shared__ float Bs[2][kBN][kLdsStride];
+    // XCD-aware tile order: workgroups are dispatched round-robin over the 8 XCDs, so block b
+    // runs on XCD b % 8. Give each XCD a contiguous run of tiles so the 128-vector slices of X
+    // that neighbouring codeword tiles share stay in that XCD's L2.
+    const int64_t b = blockIdx.x;
+    const int64_t tile = (b & 7) * per_xcd + (b >> 3);
+    if (tile >= tiles_total) return;
+    const int64_t tx = tile / tiles_h;
+    const int th = static_cast<int>(tile - tx * tiles_h);
+    const int64_t i0 = tx * kBM;
+    const int64_t h0 = static_cast<int64_t>(th) * kBN;
+    // Full tiles with d % 16 == 0 and aligned operands (every tile of the encoder's shapes but the
+    // last row tile) take the branch-free path.
+    const bool interior = i0 + kBM <= n && h0 + kBN <= H && (d % kBK) == 0 &&
+                          ((reinterpret_cast<uintptr_t>(X) | reinterpret_cast<uintptr_t>(C)) & 15u) == 0;
+    if (interior) {
+        GemmTile<true>(X, n, d, C, H, xC, ldx, i0, h0, As, Bs);
+    } else {
+        GemmTile<false>(X, n, d, C, H, xC, ldx, i0, h0, As, Bs);
     }
 }
 
