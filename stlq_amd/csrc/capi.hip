@@ -107,6 +107,7 @@ struct stlq_mi355_ctx {
     DevBuf X, nx2, xC, xC_in, codes, a, cost, best, fails, active, changed, mse, gam0, roots, scores, b0;
     DevBuf ils_codes, ils_a, ils_cost;  // ILS candidate state
     DevBuf R_in, R_rm;                  // rotation: as given (column-major) and row-major
+    DevBuf nearest, nearest_flag;       // large root: nearest root per vector, NaN flags
     DevBuf st_rec[2], st_curH[2];
 
     std::vector<TileEvents> tiles;
@@ -612,7 +613,7 @@ int stlq_mi355_ctx_destroy(stlq_mi355_ctx* c) {
                       &c->G_small, &c->G0S, &c->gdiag_small, &c->X, &c->nx2, &c->xC, &c->xC_in, &c->codes, &c->a,
                       &c->cost, &c->best, &c->fails, &c->active, &c->changed, &c->mse, &c->gam0, &c->roots,
                       &c->scores, &c->ils_codes, &c->ils_a, &c->ils_cost, &c->b0, &c->invnorm_small,
-                      &c->R_in, &c->R_rm};
+                      &c->R_in, &c->R_rm, &c->nearest, &c->nearest_flag};
     if (c->g_shared) c->G_cm.p = nullptr;
     for (DevBuf* b : bufs) b->Release();
     for (int b = 0; b < 2; ++b) {
@@ -1038,7 +1039,7 @@ int stlq_mi355_last_timings(stlq_mi355_ctx* c, stlq_mi355_timings* out) {
 
 namespace {
 int CheckLargeRoot(stlq_mi355_ctx* c, int H_beam, int root_mode);
-int64_t LargeRootTileVectors(stlq_mi355_ctx* c, int64_t n, int Hb, bool forced);
+int64_t LargeRootTileVectors(stlq_mi355_ctx* c, int64_t n, int Hb, bool one_score);
 int LargeRootTile(stlq_mi355_ctx* c, const float* dX, int64_t nt, int Hb, int root_mode, const uint32_t* d_forced,
                   const float* dxC_given, uint32_t* d_cluster, uint8_t* d_codes, float* d_best, hipStream_t s,
                   TileEvents* te, const stlq_mi355_encode_params* refine = nullptr, float* d_a = nullptr,
@@ -1193,7 +1194,7 @@ int stlq_mi355_encode_stream(stlq_mi355_ctx* c, int64_t n_total, int64_t chunk, 
             dX = sl.dXr.as<float>();
         }
         // Encode the chunk in workspace-bounded tiles (sequential on the context stream).
-        const int64_t tile = lr ? LargeRootTileVectors(c, sl.count, Hb, false)
+        const int64_t tile = lr ? LargeRootTileVectors(c, sl.count, Hb, sp->root_mode == 1)
                                 : TileVectors(sl.count, c->d, c->m, c->H, Hb);
         for (int64_t t0 = 0; t0 < sl.count && rc == STLQ_MI355_OK; t0 += tile) {
             const int64_t nt = std::min(tile, sl.count - t0);
@@ -1262,9 +1263,10 @@ int CheckLargeRoot(stlq_mi355_ctx* c, int H_beam, int root_mode) {
     return STLQ_MI355_OK;
 }
 
-int64_t LargeRootTileVectors(stlq_mi355_ctx* c, int64_t n, int Hb, bool forced) {
+// one_score: the root stage keeps one score per vector (forced or nearest root), not h0.
+int64_t LargeRootTileVectors(stlq_mi355_ctx* c, int64_t n, int Hb, bool one_score) {
     const int m = c->lr_m;
-    const int64_t per = 4LL * c->lr_d + 4 + 8LL * std::max(c->Hs, 1) + (forced ? 8 : 4LL * c->h0) +
+    const int64_t per = 4LL * c->lr_d + 4 + 8LL * std::max(c->Hs, 1) + (one_score ? 16 : 4LL * c->h0) +
                         2 * (4LL * Hb * BeamRecordStride(m) + 4) + m + 16 +
                         (5LL * m + 16);  // refit: b0, ICM flags, ILS candidate codes/coefficients/cost
     int64_t t = std::max<int64_t>(EnvWorkspaceBytes() / per, 1024);
@@ -1284,7 +1286,8 @@ int LargeRootTile(stlq_mi355_ctx* c, const float* dX, int64_t nt, int Hb, int ro
     const int m = c->lr_m, Hs = c->Hs, h0 = c->h0, d = c->lr_d;
     HIP_TRY(c->nx2.Ensure(static_cast<size_t>(nt) * 4));
     HIP_TRY(c->xC.Ensure(static_cast<size_t>(nt) * std::max(Hs, 1) * 4));
-    HIP_TRY(c->scores.Ensure(static_cast<size_t>(nt) * (d_forced ? 1 : h0) * 4));
+    const bool one_score = d_forced || root_mode == 1;  // the seed reads one score per vector
+    HIP_TRY(c->scores.Ensure(static_cast<size_t>(nt) * (one_score ? 1 : h0) * 4));
     RC_TRY(EnsureState(c, nt, m, Hb));
     auto rec = [&](int k) -> hipError_t {
         if (!te) return hipSuccess;
@@ -1317,6 +1320,23 @@ int LargeRootTile(stlq_mi355_ctx* c, const float* dX, int64_t nt, int Hb, int ro
         HIP_TRY(LaunchGatherRootDot(dX, d, c->C0.as<float>(), d_forced, nt, c->scores.as<float>(), s));
         ra.ldx = 1;
         ra.forced = d_forced;
+        ra.root_slots = 1;
+    } else if (root_mode == 1) {
+        // Nearest root: the root-score GEMM with a first-minimum epilogue (no n x h0 score matrix),
+        // vectors that met a NaN error redone by the exact scan, then the chosen root seeded as a
+        // forced root (the same records as the one-slot scan of the scores).
+        HIP_TRY(c->nearest.Ensure(static_cast<size_t>(nt) * 4));
+        HIP_TRY(c->nearest_flag.Ensure(static_cast<size_t>(nt)));
+        uint32_t* dn = c->nearest.as<uint32_t>();
+        uint8_t* df = c->nearest_flag.as<uint8_t>();
+        HIP_TRY(LaunchNearestRoot(dX, nt, d, c->C0.as<float>(), h0, c->norm0.as<float>(), c->nx2.as<float>(), dn, df,
+                                  s));
+        if (te) ++te->gemm_launches;
+        HIP_TRY(LaunchNearestRootFixup(dX, d, c->C0.as<float>(), h0, c->norm0.as<float>(), c->nx2.as<float>(), df, nt,
+                                       dn, s));
+        HIP_TRY(LaunchGatherRootDot(dX, d, c->C0.as<float>(), dn, nt, c->scores.as<float>(), s));
+        ra.ldx = 1;
+        ra.forced = dn;
         ra.root_slots = 1;
     } else {
         HIP_TRY(LaunchGemmXc(dX, nt, d, c->C0.as<float>(), h0, c->scores.as<float>(), h0, s));
@@ -1450,7 +1470,7 @@ int stlq_mi355_beam_search_large_root(stlq_mi355_ctx* c, const float* X, const f
                                                         std::to_string(i) + " >= h0");
     }
     c->ResetTimings();
-    const int64_t tile = LargeRootTileVectors(c, n, Hb, forced_root != nullptr);
+    const int64_t tile = LargeRootTileVectors(c, n, Hb, forced_root != nullptr || root_mode == 1);
     HIP_TRY(c->X.Ensure(static_cast<size_t>(tile) * d * 4));
     HIP_TRY(c->roots.Ensure(static_cast<size_t>(tile) * 4 * 2));
     HIP_TRY(c->codes.Ensure(static_cast<size_t>(tile) * std::max(m - 1, 1)));

@@ -85,6 +85,15 @@ hipError_t LaunchGemmXc(const float* X, int64_t n, int d, const float* C, int H,
 hipError_t LaunchBeamLayer0(const LayerArgs& a, hipStream_t s);
 hipError_t LaunchBeamLayer(int L, bool large_root, const LayerArgs& a, hipStream_t s);
 hipError_t LaunchRootSeed(const RootArgs& a, hipStream_t s);
+// No root for the vector (every root skipped or worse than +inf): the forced-root paths seed
+// nothing, as the root scan does.
+constexpr uint32_t kNoRoot = 0xFFFFFFFFu;
+// Nearest root per vector from fused MFMA root scores (no score matrix); flag = 1 where a NaN
+// error was met (those vectors are redone by LaunchNearestRootFixup).
+hipError_t LaunchNearestRoot(const float* X, int64_t n, int d, const float* C0, int h0, const float* norm0,
+                             const float* nx2, uint32_t* root_out, uint8_t* flag, hipStream_t s);
+hipError_t LaunchNearestRootFixup(const float* X, int d, const float* C0, int h0, const float* norm0,
+                                  const float* nx2, const uint8_t* flag, int64_t n, uint32_t* root_out, hipStream_t s);
 hipError_t LaunchGatherRootDot(const float* X, int d, const float* C0, const uint32_t* roots, int64_t n, float* out,
                                hipStream_t s);
 

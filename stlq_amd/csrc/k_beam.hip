@@ -695,7 +695,7 @@ __global__ __launch_bounds__(256) void RootSeedKernel(RootArgs p) {
     float s_err = kInfF;
     int s_cand = -1;
     if (p.forced) {
-        if (lane == 0) {
+        if (lane == 0 && p.forced[i] != kNoRoot) {
             const int code = static_cast<int>(p.forced[i]);
             const float alpha = p.norm0[code];
             if (alpha != 0.0f) {
@@ -762,11 +762,59 @@ __global__ __launch_bounds__(256) void GatherRootDotKernel(const float* __restri
                                                            float* __restrict__ out) {
     const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (i >= n) return;
+    if (roots[i] == kNoRoot) {
+        out[i] = 0.0f;
+        return;
+    }
     const float* x = X + i * d;
     const float* c = C0 + static_cast<int64_t>(roots[i]) * d;
     float s = 0.0f;
     for (int r = 0; r < d; ++r) s = __builtin_fmaf(c[r], x[r], s);
     out[i] = s;
+}
+
+// The vectors NearestRootKernel flagged (a NaN error met): the root scan of RootSeedKernel with
+// one slot, in ascending code order with the reference's NaN rules, on root scores computed here
+// as fused k-ordered dot products (GatherRootDotKernel's order, the MFMA GEMM's bits). A grid of
+// waves strides over the vectors; unflagged ones cost one byte read.
+__global__ __launch_bounds__(256) void NearestRootFixupKernel(const float* __restrict__ X, int d,
+                                                              const float* __restrict__ C0, int h0,
+                                                              const float* __restrict__ norm0,
+                                                              const float* __restrict__ nx2,
+                                                              const uint8_t* __restrict__ flag, int64_t n,
+                                                              uint32_t* __restrict__ root_out) {
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kBeamWavesPerBlock;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBeamWavesPerBlock + wave; i < n; i += stride) {
+        if (!flag[i]) continue;
+        const float* x = X + i * d;
+        const float xn = nx2[i];
+        float s_err;
+        int s_cand;
+        SelectTopH<false>(
+            1, lane,
+            [&](auto&& replay, auto) {
+                for (int c0 = 0; c0 < h0; c0 += kWave) {
+                    const int code = c0 + lane;
+                    const bool act = code < h0;
+                    const float alpha = act ? norm0[code] : 0.0f;
+                    const bool ok = act && alpha != 0.0f;
+                    float gamma = 0.0f;
+                    if (act) {
+                        const float* c = C0 + static_cast<int64_t>(code) * d;
+                        for (int r = 0; r < d; ++r) gamma = __builtin_fmaf(c[r], x[r], gamma);
+                    }
+                    const float a1 = gamma / alpha;
+                    const float e1 = xn - gamma * a1;
+                    if (!replay(ok, e1, c0)) return false;
+                }
+                return true;
+            },
+            s_err, s_cand);
+        (void)s_err;
+        if (lane == 0) root_out[i] = s_cand >= 0 ? static_cast<uint32_t>(s_cand) : kNoRoot;
+    }
 }
 
 template <int L>
@@ -792,6 +840,16 @@ hipError_t LaunchRootSeed(const RootArgs& a, hipStream_t s) {
     if (a.n <= 0) return hipSuccess;
     const unsigned blocks = static_cast<unsigned>((a.n + kBeamWavesPerBlock - 1) / kBeamWavesPerBlock);
     hipLaunchKernelGGL(RootSeedKernel, dim3(blocks), dim3(kWave * kBeamWavesPerBlock), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t LaunchNearestRootFixup(const float* X, int d, const float* C0, int h0, const float* norm0,
+                                  const float* nx2, const uint8_t* flag, int64_t n, uint32_t* root_out, hipStream_t s) {
+    if (n <= 0 || h0 <= 0) return hipSuccess;
+    const int64_t waves = std::min<int64_t>(n, 8192);
+    const unsigned blocks = static_cast<unsigned>((waves + kBeamWavesPerBlock - 1) / kBeamWavesPerBlock);
+    hipLaunchKernelGGL(NearestRootFixupKernel, dim3(blocks), dim3(kBeamWavesPerBlock * kWave), 0, s, X, d, C0, h0,
+                       norm0, nx2, flag, n, root_out);
     return hipGetLastError();
 }
 

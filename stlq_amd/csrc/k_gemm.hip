@@ -61,11 +61,13 @@ __device__ __forceinline__ void StoreSlice(float (*S)[kLdsStride], const Staged&
     }
 }
 
-// One 128 x 128 output tile; kInterior as for LoadSlice (and no bounds checks on the stores).
+// One 128 x 128 tile of X C^T into acc; kInterior as for LoadSlice. D block (a, c) of acc: lane
+// holds rows wm*64 + 16a + 4g + r (r = 0..3) of column wn*64 + 16c + r16. Ends with a barrier,
+// so the LDS buffers are free for the next tile.
 template <bool kInterior>
-__device__ __forceinline__ void GemmTile(const float* __restrict__ X, int64_t n, int d, const float* __restrict__ C,
-                                         int H, float* __restrict__ xC, int64_t ldx, int64_t i0, int64_t h0,
-                                         float (*As)[kBM][kLdsStride], float (*Bs)[kBN][kLdsStride]) {
+__device__ __forceinline__ void GemmAcc(const float* __restrict__ X, int64_t n, int d, const float* __restrict__ C,
+                                        int H, int64_t i0, int64_t h0, float (*As)[kBM][kLdsStride],
+                                        float (*Bs)[kBN][kLdsStride], floatx4 (&acc)[4][4]) {
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -74,7 +76,6 @@ __device__ __forceinline__ void GemmTile(const float* __restrict__ X, int64_t n,
     // float4 loads need 16-byte aligned rows: d % 4 == 0 and 16-byte aligned bases
     const bool vec4 = (d & 3) == 0 && ((reinterpret_cast<uintptr_t>(X) | reinterpret_cast<uintptr_t>(C)) & 15u) == 0;
 
-    floatx4 acc[4][4];
 #pragma unroll
     for (int a = 0; a < 4; ++a)
 #pragma unroll
@@ -115,8 +116,19 @@ __device__ __forceinline__ void GemmTile(const float* __restrict__ X, int64_t n,
         }
         __syncthreads();
     }
+}
 
-    // D block (a, c): lane holds rows 4g..4g+3 of column r16.
+// One 128 x 128 output tile of xC; kInterior as for LoadSlice (and no bounds checks on the stores).
+template <bool kInterior>
+__device__ __forceinline__ void GemmTile(const float* __restrict__ X, int64_t n, int d, const float* __restrict__ C,
+                                         int H, float* __restrict__ xC, int64_t ldx, int64_t i0, int64_t h0,
+                                         float (*As)[kBM][kLdsStride], float (*Bs)[kBN][kLdsStride]) {
+    floatx4 acc[4][4];
+    GemmAcc<kInterior>(X, n, d, C, H, i0, h0, As, Bs, acc);
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int g = lane >> 4, r16 = lane & 15;
 #pragma unroll
     for (int a = 0; a < 4; ++a) {
 #pragma unroll
@@ -161,7 +173,131 @@ __global__ __launch_bounds__(256) void GemmXcKernel(const float* __restrict__ X,
     }
 }
 
+// Nearest root of the large-root beam (beam_search.cpp:639-709 with one root slot, the forced
+// nearest root): per vector, the first root code in ascending order with the smallest
+// e1 = ||x||^2 - g*(g/alpha), g = <x, C0[:,code]>, alpha = ||C0[:,code]||^2 != 0, where a later
+// code replaces the current one only when strictly smaller (so ties keep the lower code, and +0
+// and -0 tie). The root scores come from the same MFMA tiles as GemmXcKernel (identical g bits),
+// but each block sweeps every root tile for its 128 vectors and keeps a running per-row minimum
+// in registers instead of writing the n x h0 score matrix.
+// A NaN e1 has no such reduction (the reference lets it in and then accepts the next candidate
+// whatever it is), so a vector that meets one is flagged for NearestRootFixupKernel.
+// root_out: code or kNoRoot; flag: 1 where a NaN was met.
+template <bool kInteriorRows>
+__global__ __launch_bounds__(256) void NearestRootKernel(const float* __restrict__ X, int64_t n, int d,
+                                                         const float* __restrict__ C0, int h0,
+                                                         const float* __restrict__ norm0,
+                                                         const float* __restrict__ nx2, uint32_t* __restrict__ root_out,
+                                                         uint8_t* __restrict__ flag) {
+    __shared__ float As[2][kBM][kLdsStride];
+    __shared__ float Bs[2][kBN][kLdsStride];
+    __shared__ float red_e[2][kBM];
+    __shared__ uint32_t red_c[2][kBM];
+    __shared__ uint32_t red_f[2][kBM];
+    const int64_t i0 = static_cast<int64_t>(blockIdx.x) * kBM;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int g = lane >> 4, r16 = lane & 15;
+
+    float be[4][4], xn[4][4];
+    uint32_t bc[4][4];
+    uint32_t nanm = 0;  // bit 4a+r: a NaN e1 met on that row
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int64_t row = i0 + wm * 64 + a * 16 + 4 * g + r;
+            be[a][r] = __builtin_huge_valf();
+            bc[a][r] = kNoRoot;
+            xn[a][r] = (kInteriorRows || row < n) ? nx2[row] : 0.0f;
+        }
+    const int tiles = (h0 + kBN - 1) / kBN;
+    const bool aligned = (d % kBK) == 0 && ((reinterpret_cast<uintptr_t>(X) | reinterpret_cast<uintptr_t>(C0)) & 15u) == 0;
+    for (int th = 0; th < tiles; ++th) {
+        const int64_t hb = static_cast<int64_t>(th) * kBN;
+        const bool interior = kInteriorRows && aligned && hb + kBN <= h0;
+        floatx4 acc[4][4];
+        if (interior) {
+            GemmAcc<true>(X, n, d, C0, h0, i0, hb, As, Bs, acc);
+        } else {
+            GemmAcc<false>(X, n, d, C0, h0, i0, hb, As, Bs, acc);
+        }
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int col = static_cast<int>(hb) + wn * 64 + c * 16 + r16;
+            const float alpha = col < h0 ? norm0[col] : 0.0f;
+            if (alpha == 0.0f) continue;  // beam_search.cpp: alpha == 0 roots are skipped
+#pragma unroll
+            for (int a = 0; a < 4; ++a)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float gam = acc[a][c][r];
+                    const float a1 = gam / alpha;
+                    const float e1 = xn[a][r] - gam * a1;
+                    if (__builtin_isnan(e1)) nanm |= 1u << (4 * a + r);
+                    if (e1 < be[a][r]) {
+                        be[a][r] = e1;
+                        bc[a][r] = static_cast<uint32_t>(col);
+                    }
+                }
+        }
+    }
+    // first minimum over the 16 lanes that share these rows (codes differ, so ties go to the
+    // lower code), then over the two column waves through LDS
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            float e = be[a][r];
+            uint32_t cd = bc[a][r];
+            uint32_t f = (nanm >> (4 * a + r)) & 1u;
+#pragma unroll
+            for (int sh = 1; sh < 16; sh <<= 1) {
+                const float e2 = __shfl_xor(e, sh, 16);
+                const uint32_t c2 = __shfl_xor(cd, sh, 16);
+                f |= __shfl_xor(f, sh, 16);
+                if (e2 < e || (e2 == e && c2 < cd)) {
+                    e = e2;
+                    cd = c2;
+                }
+            }
+            if (r16 == 0) {
+                const int lr = wm * 64 + a * 16 + 4 * g + r;
+                red_e[wn][lr] = e;
+                red_c[wn][lr] = cd;
+                red_f[wn][lr] = f;
+            }
+        }
+    __syncthreads();
+    const int t = threadIdx.x;
+    if (t < kBM && (kInteriorRows || i0 + t < n)) {
+        float e = red_e[0][t];
+        uint32_t cd = red_c[0][t];
+        const float e2 = red_e[1][t];
+        const uint32_t c2 = red_c[1][t];
+        if (e2 < e || (e2 == e && c2 < cd)) cd = c2;
+        root_out[i0 + t] = cd;
+        flag[i0 + t] = static_cast<uint8_t>(red_f[0][t] | red_f[1][t]);
+    }
+}
+
 }  // namespace
+
+hipError_t LaunchNearestRoot(const float* X, int64_t n, int d, const float* C0, int h0, const float* norm0,
+                             const float* nx2, uint32_t* root_out, uint8_t* flag, hipStream_t s) {
+    if (n <= 0 || h0 <= 0) return hipSuccess;
+    const int64_t full = n / kBM;
+    if (full > 0)
+        hipLaunchKernelGGL(NearestRootKernel<true>, dim3(static_cast<unsigned>(full)), dim3(256), 0, s, X, n, d, C0,
+                           h0, norm0, nx2, root_out, flag);
+    if (full * kBM < n) {
+        // the partial last row tile: blockIdx 0 of this launch is tile `full`
+        hipLaunchKernelGGL(NearestRootKernel<false>, dim3(1), dim3(256), 0, s, X + full * kBM * d, n - full * kBM, d,
+                           C0, h0, norm0, nx2 + full * kBM, root_out + full * kBM, flag + full * kBM);
+    }
+    return hipGetLastError();
+}
 
 hipError_t LaunchGemmXc(const float* X, int64_t n, int d, const float* C, int H, float* xC, int64_t ldx,
                         hipStream_t s) {

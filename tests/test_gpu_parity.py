@@ -653,3 +653,32 @@ def test_stream_rotation_large_root_u8(ctx, orc):
     assert np.array_equal(_bits(got["best_err"]), _bits(err))
     assert np.array_equal(_bits(got["a"]), _bits(a_g))
     assert np.array_equal(_bits(got["cost"]), _bits(c_g))
+
+
+@pytest.mark.parametrize("nan_roots", [0, 3])
+def test_large_root_nearest_nan_roots(ctx, orc, nan_roots):
+    """Nearest-root mode with root codewords that give NaN errors for every vector: the fused
+    first-minimum GEMM flags those vectors and the exact scan redoes them (a NaN enters the
+    one-slot scan and the next candidate replaces it), matching the oracle's streaming scan."""
+    from stlq_amd import workloads
+
+    n, d, h0, K = 700, 32, 700, 64
+    mix = workloads.Mixture("gauss", d, 128, 97)
+    rng = np.random.default_rng(97)
+    C0 = mix.sample(5_000_000, h0)
+    Cs = workloads.residual_codebooks(mix.sample(1_000_000, 2000) - C0[rng.integers(0, h0, 2000)], 3, K, 3, 98)
+    for r in rng.choice(h0, nan_roots, replace=False):
+        C0[r, 5] = np.nan
+    X = mix.sample(0, n)
+    h = [h0] + [K] * 3
+    print(f"lr nearest nan_roots={nan_roots} n={n} h0={h0}", flush=True)
+    ctx.set_large_root(C0, Cs, h)
+    cid_g, Bs_g, err_g = ctx.beam_search_large_root(X, 8, root_mode=1)
+    norm0, Gs, G0S = orc.build_precomp_large_root(C0, Cs)
+    nx2 = orc.xnorm2(X)
+    xs = orc.gemm_xc(Cs, X, mode=1)
+    cid_o, Bs_o, err_o = orc.beam_search_large_root(X, nx2, C0, norm0, xs, Gs, G0S, h, 8, root_mode=1)
+    assert np.array_equal(cid_o, cid_g), np.nonzero(cid_o != cid_g)[0][:10]
+    assert np.array_equal(Bs_o, Bs_g)
+    same = (_bits(err_o) == _bits(err_g)) | (np.isnan(err_o) & np.isnan(err_g))
+    assert np.all(same)
