@@ -14,13 +14,11 @@ constexpr int kMaxBeam = 64;  // slot state lives in one wave64 lane per slot
 constexpr int kWave = 64;
 constexpr int kBeamWavesPerBlock = 4;  // one vector per wave, four vectors per workgroup
 
-// Packed upper-triangular index of R(r, c), r <= c < m (row-major rows of decreasing length).
-__host__ __device__ inline int TriIdx(int m, int r, int c) { return r * m - (r * (r - 1)) / 2 + (c - r); }
-__host__ __device__ inline int TriSize(int m) { return m * (m + 1) / 2; }
 __host__ __device__ inline int CodeStride(int m) { return (m + 3) & ~3; }
 
 // Beam state of one tile of vectors, slot-major (vector i, slot s at i*Hb + s). Each slot is
-// one record of BeamRecordStride(m) dwords: [err, coef[m], packed R (TriSize(m)),
+// one record of BeamRecordStride(m) dwords: [err, the Cholesky factor R column by column with
+// each column followed by the reciprocal of its diagonal (m(m+3)/2), coef[m],
 // codes (CodeStride(m) bytes), root id, padding to 16 bytes].
 struct BeamState {
     float* rec = nullptr;        // [n*Hb*BeamRecordStride(m)]
