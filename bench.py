@@ -129,7 +129,7 @@ def main():
 
     gemm_ms = beam_ms = total_ms = icm_ms = 0.0
     layer_ms = np.zeros(20)
-    launches = 0
+    launches = reruns = 0
     ctx.synchronize()
     t_start = time.perf_counter()
     for k in range(args.steps):
@@ -141,6 +141,7 @@ def main():
         total_ms += t.total_ms
         layer_ms += np.array(t.layer_ms[:20])
         launches += t.gemm_launches
+        reruns += t.beam_reruns
     ctx.synchronize()
     wall = time.perf_counter() - t_start
     log(f"timed {args.steps} steps in {wall:.3f}s")
@@ -173,13 +174,17 @@ def main():
         "gemm_ms": gemm_ms / steps,
         "beam_ms": beam_ms / steps,
         "beam_layer_ms": [round(x / steps, 3) for x in layer_ms[:M]],
+        # vectors the best-first beam pass flagged and re-ran in the reference order (per step)
+        "beam_reruns": reruns / steps,
         "icm_ms": icm_ms / steps,
         "device_total_ms": total_ms / steps,
     }
 
-    traffic, traffic_src = (_profiled_traffic(f"LayerKernel<{last}, false, true>") if args.config == "C2"
+    # the timed layer kernel: full codebook, best-first pass (the default beam order)
+    prof_kernel = f"LayerKernel<{last}, false, true, true>"
+    traffic, traffic_src = (_profiled_traffic(prof_kernel) if args.config == "C2"
                             else (None, None))
-    valu, salu, valu_src = (_profiled_valu(f"LayerKernel<{last}, false, true>") if args.config == "C2"
+    valu, salu, valu_src = (_profiled_valu(prof_kernel) if args.config == "C2"
                             else (None, None, None))
     metric = ("vectors encoded/sec (d=128,M=8,K=256,B=16)" if args.config == "C2" else
               f"vectors encoded/sec (d={d},M={M},K={K},B={B}" + (f",ICM={w.icm_iters})" if w.icm_iters else ")"))

@@ -68,6 +68,8 @@ typedef struct stlq_mi355_timings {
     int gemm_launches;
     int beam_launches;
     double layer_ms[STLQ_MI355_MAX_M]; /* beam layer l (one launch per tile) */
+    int64_t beam_reruns; /* vectors the full-precomp beam re-ran in the reference's slot order
+                            (ties the best-first pass cannot settle); included in beam_ms */
 } stlq_mi355_timings;
 
 const char* stlq_mi355_last_error(void);

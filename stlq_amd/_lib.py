@@ -48,6 +48,7 @@ class Timings(ctypes.Structure):
         ("gemm_launches", ctypes.c_int),
         ("beam_launches", ctypes.c_int),
         ("layer_ms", ctypes.c_double * 20),
+        ("beam_reruns", ctypes.c_int64),
     ]
 
 

@@ -109,6 +109,11 @@ struct stlq_mi355_ctx {
     DevBuf R_in, R_rm;                  // rotation: as given (column-major) and row-major
     DevBuf nearest, nearest_flag;       // large root: nearest root per vector, NaN flags
     DevBuf st_rec[2], st_curH[2];
+    // Best-first beam pass: per-vector flags, the list of flagged vectors, and two counters
+    // (this tile's count, and the total since the timings were last reset).
+    DevBuf bf_flags, bf_list, bf_count;
+    bool bf_reset = true;  // clear the total at the next best-first pass
+    bool bf_used = false;  // a best-first pass ran since the timings were reset
 
     std::vector<TileEvents> tiles;
     std::vector<hipEvent_t> event_pool;
@@ -127,6 +132,8 @@ struct stlq_mi355_ctx {
         tiles.clear();
         event_next = 0;
         overlapped = false;
+        bf_reset = true;
+        bf_used = false;
     }
 };
 
@@ -166,7 +173,7 @@ int ValidateLayers(int d, int m, const int* h_vec, int first_max) {
 // Per-vector device bytes of one encode tile.
 int64_t PerVectorBytes(int d, int m, int H, int Hb) {
     const int64_t state = static_cast<int64_t>(Hb) * 4 * BeamRecordStride(m);
-    return 4LL * d + 4 + 4LL * H + m + 4LL * m + 4 + 4 + 2 + 8 + 2 * (state + 4);
+    return 4LL * d + 4 + 4LL * H + m + 4LL * m + 4 + 4 + 2 + 8 + 5 + 2 * (state + 4);  // 5: best-first flag + list
 }
 
 int64_t TileVectors(int64_t n, int d, int m, int H, int Hb) {
@@ -193,10 +200,34 @@ BeamState StateOf(stlq_mi355_ctx* c, int b) {
     return s;
 }
 
+// Scan order of the full-precomp beam: best-first pass plus a reference-order re-run of the
+// vectors it flags (the default), or the reference order throughout (STLQ_MI355_BEAM_ORDER=reference).
+bool BestFirstBeam() {
+    const char* v = std::getenv("STLQ_MI355_BEAM_ORDER");
+    return !(v && std::strcmp(v, "reference") == 0);
+}
+
 // Full-precomp beam over one tile: layer 0 then layers 1..m-1 (BeamSearchPrefixLS).
+//
+// By default the layers first run best-first (LayerArgs::flags): parents in ascending error
+// order, which admits far fewer candidates into the top-H on the way (about 80 instead of 115 per
+// vector and layer at C2) and gives the reference's top-H sets, records and final pick except
+// where candidates tie at the top-H boundary or for the final minimum (or an error is NaN or -0).
+// Every such vector is flagged and then re-run on its own in the reference's slot order, so the
+// results are the reference's in every case.
 int RunBeam(stlq_mi355_ctx* c, const float* dxC, int64_t ldx, const float* dnx2, int64_t n, int Hb,
             uint8_t* dcodes, float* dbest, hipStream_t s, int* launches, TileEvents* te = nullptr) {
     RC_TRY(EnsureState(c, n, c->m, Hb));
+    const bool best = c->m >= 2 && BestFirstBeam();
+    if (best) {
+        HIP_TRY(c->bf_flags.Ensure(static_cast<size_t>(n)));
+        HIP_TRY(c->bf_list.Ensure(static_cast<size_t>(n) * 4));
+        HIP_TRY(c->bf_count.Ensure(8));
+        HIP_TRY(LaunchFill8(c->bf_flags.as<uint8_t>(), 0, n, s));
+        HIP_TRY(LaunchFill8(c->bf_count.as<uint8_t>(), 0, c->bf_reset ? 8 : 4, s));
+        c->bf_reset = false;
+        c->bf_used = true;
+    }
     auto mark = [&](int k) -> hipError_t {
         if (!te) return hipSuccess;
         te->lay[k] = c->NextEvent();
@@ -217,24 +248,40 @@ int RunBeam(stlq_mi355_ctx* c, const float* dxC, int64_t ldx, const float* dnx2,
     a.Hb = Hb;
     a.codes_out = dcodes;
     a.best_err = dbest;
-    int cur = 0;
-    a.out = StateOf(c, cur);
-    a.K = c->h_vec[0];
-    a.offL = c->off[0];
-    a.is_last = (c->m == 1);
-    HIP_TRY(LaunchBeamLayer0(a, s));
-    HIP_TRY(mark(1));
-    int nl = 1;
-    for (int L = 1; L < c->m; ++L) {
-        a.in = StateOf(c, cur);
-        a.out = StateOf(c, cur ^ 1);
-        a.K = c->h_vec[L];
-        a.offL = c->off[L];
-        a.is_last = (L == c->m - 1);
-        HIP_TRY(LaunchBeamLayer(L, false, a, s));
-        HIP_TRY(mark(L + 1));
-        cur ^= 1;
+    a.flags = best ? c->bf_flags.as<uint8_t>() : nullptr;
+    int nl = 0;
+    auto layers = [&](bool timed) -> int {
+        int cur = 0;
+        a.out = StateOf(c, cur);
+        a.K = c->h_vec[0];
+        a.offL = c->off[0];
+        a.is_last = (c->m == 1);
+        HIP_TRY(LaunchBeamLayer0(a, s));
+        if (timed) HIP_TRY(mark(1));
         ++nl;
+        for (int L = 1; L < c->m; ++L) {
+            a.in = StateOf(c, cur);
+            a.out = StateOf(c, cur ^ 1);
+            a.K = c->h_vec[L];
+            a.offL = c->off[L];
+            a.is_last = (L == c->m - 1);
+            HIP_TRY(LaunchBeamLayer(L, false, a, s));
+            if (timed) HIP_TRY(mark(L + 1));
+            cur ^= 1;
+            ++nl;
+        }
+        return STLQ_MI355_OK;
+    };
+    RC_TRY(layers(true));
+    if (best) {
+        // Re-run the flagged vectors in the reference order: one wave per listed vector, the
+        // grid sized for all n (waves past the list's length exit at once).
+        int* counts = c->bf_count.as<int>();
+        HIP_TRY(LaunchCollectFlagged(c->bf_flags.as<uint8_t>(), n, c->bf_list.as<int>(), counts, s));
+        a.flags = nullptr;
+        a.list = c->bf_list.as<int>();
+        a.list_n = counts;
+        RC_TRY(layers(false));
     }
     if (launches) *launches += nl;
     return STLQ_MI355_OK;
@@ -613,7 +660,8 @@ int stlq_mi355_ctx_destroy(stlq_mi355_ctx* c) {
                       &c->G_small, &c->G0S, &c->gdiag_small, &c->X, &c->nx2, &c->xC, &c->xC_in, &c->codes, &c->a,
                       &c->cost, &c->best, &c->fails, &c->active, &c->changed, &c->mse, &c->gam0, &c->roots,
                       &c->scores, &c->ils_codes, &c->ils_a, &c->ils_cost, &c->b0, &c->invnorm_small,
-                      &c->R_in, &c->R_rm, &c->nearest, &c->nearest_flag};
+                      &c->R_in, &c->R_rm, &c->nearest, &c->nearest_flag, &c->bf_flags, &c->bf_list,
+                      &c->bf_count};
     if (c->g_shared) c->G_cm.p = nullptr;
     for (DevBuf* b : bufs) b->Release();
     for (int b = 0; b < 2; ++b) {
@@ -1026,6 +1074,11 @@ int stlq_mi355_last_timings(stlq_mi355_ctx* c, stlq_mi355_timings* out) {
             HIP_TRY(hipEventElapsedTime(&lm, te.lay[l], te.lay[l + 1]));
             out->layer_ms[l] += lm;
         }
+    }
+    if (c->bf_used && !c->tiles.empty()) {
+        int counts[2] = {0, 0};
+        HIP_TRY(hipMemcpy(counts, c->bf_count.p, sizeof(counts), hipMemcpyDeviceToHost));
+        out->beam_reruns = counts[1];
     }
     if (c->overlapped && !c->tiles.empty()) {
         float env = 0.0f;

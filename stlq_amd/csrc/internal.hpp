@@ -51,6 +51,16 @@ struct LayerArgs {
     float* best_err = nullptr;
     uint32_t* cluster_out = nullptr;
     int is_last = 0;
+    // Best-first pass (full precomp): parents are scanned in ascending error order instead of
+    // the reference's slot order, which keeps the reference's top-H sets whenever no two
+    // candidates tie at the top-H boundary. flags[i] = 1 marks a vector where that could fail
+    // (a boundary tie, a tie for the final minimum, a NaN or -0 error); those vectors are
+    // re-run in the reference order. null: the reference order.
+    uint8_t* flags = nullptr;
+    // Re-run over a list: wave w encodes vector list[w] for w < *list_n, with its beam state at
+    // index w. null: wave w encodes vector w.
+    const int* list = nullptr;
+    const int* list_n = nullptr;
 };
 
 struct RootArgs {
@@ -82,6 +92,9 @@ hipError_t LaunchGemmXc(const float* X, int64_t n, int d, const float* C, int H,
 
 hipError_t LaunchBeamLayer0(const LayerArgs& a, hipStream_t s);
 hipError_t LaunchBeamLayer(int L, bool large_root, const LayerArgs& a, hipStream_t s);
+// Indices of the vectors with flags[i] != 0 into list; counts[0] and counts[1] grow by their
+// number (both must be cleared beforehand as the caller needs).
+hipError_t LaunchCollectFlagged(const uint8_t* flags, int64_t n, int* list, int* counts, hipStream_t s);
 hipError_t LaunchRootSeed(const RootArgs& a, hipStream_t s);
 // No root for the vector (every root skipped or worse than +inf): the forced-root paths seed
 // nothing, as the root scan does.

@@ -173,17 +173,30 @@ __device__ __forceinline__ void ToSlots(const TopKeys<kNonNeg>& t, float& s_err,
 // caller then replays the layer with ReplaySlow). Otherwise e < worst exactly when
 // image(e) < image(worst). With kNonNeg the errors are +0..+inf, NaN or -0, and NaN and -0 are
 // exactly the bit patterns above +inf's.
-template <bool kNonNeg>
-__device__ __forceinline__ bool ReplayFast(bool ok, float e, int cand_base, int Hb, int lane, TopKeys<kNonNeg>& t) {
+// Best-first pass bookkeeping: the smallest key image among eligible candidates that did not
+// enter (rej, per lane) or were evicted (ev).
+struct OutTrack {
+    uint32_t rej = 0xFFFFFFFFu;
+    uint32_t ev = 0xFFFFFFFFu;
+};
+
+template <bool kNonNeg, bool kTrack>
+__device__ __forceinline__ bool ReplayFast(bool ok, float e, int cand_base, int Hb, int lane, TopKeys<kNonNeg>& t,
+                                           OutTrack& ot) {
     const uint64_t okm = Ballot(ok);
     const bool bad = kNonNeg ? (__float_as_uint(e) > 0x7F800000u) : __builtin_amdgcn_classf(e, 0x23);
     if ((Ballot(bad) & okm) != 0ull) return false;
     const uint32_t oe = KeyImage<kNonNeg>(e);
     uint64_t mask = okm & Ballot(oe < t.whi);
+    uint64_t entered = 0;
     // lanes 1..Hb-1 of the sorted keys: the ones that stay when lane 0 (the worst) is evicted
     const uint64_t keep = (Hb >= 64 ? ~0ull : ((1ull << Hb) - 1ull)) & ~1ull;
     while (mask) {
         const int l = static_cast<int>(__builtin_ctzll(mask));
+        if (kTrack) {
+            entered |= 1ull << l;
+            ot.ev = ot.ev < t.whi ? ot.ev : t.whi;
+        }
         // the new pair takes the evicted slot: the slot field of lane 0's key
         const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(oe), l));
         const uint32_t lo = (t.wlo & 0xFC000000u) | static_cast<uint32_t>(cand_base + l);
@@ -195,7 +208,43 @@ __device__ __forceinline__ bool ReplayFast(bool ok, float e, int cand_base, int 
         t.wlo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(t.key), 0));
         mask = okm & AboveLane(l) & Ballot(oe < t.whi);
     }
+    if (kTrack) {
+        const uint32_t img = __builtin_amdgcn_inverse_ballot_w64(okm & ~entered) ? oe : 0xFFFFFFFFu;
+        ot.rej = img < ot.rej ? img : ot.rej;
+    }
     return true;
+}
+
+template <int CTRL>
+__device__ __forceinline__ uint32_t DppU(uint32_t v) {
+    return static_cast<uint32_t>(
+        __builtin_amdgcn_update_dpp(static_cast<int>(v), static_cast<int>(v), CTRL, 0xF, 0xF, false));
+}
+
+// Wave-uniform minimum: DPP within each 16-lane row (as RowMin), then the four row results.
+__device__ __forceinline__ uint32_t WaveMinU32(uint32_t v) {
+    v = min(v, DppU<0xB1>(v));
+    v = min(v, DppU<0x4E>(v));
+    v = min(v, DppU<0x141>(v));
+    v = min(v, DppU<0x140>(v));
+    const uint32_t a = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 0));
+    const uint32_t b = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 16));
+    const uint32_t c = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 32));
+    const uint32_t d = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 48));
+    return min(min(a, b), min(c, d));
+}
+
+// Rank-indexed view of the sorted keys: lane q receives the q-th smallest key's error and
+// candidate (placeholders last).
+template <bool kNonNeg>
+__device__ __forceinline__ void ToRanks(const TopKeys<kNonNeg>& t, int Hb, int lane, float& s_err, int& s_cand) {
+    const uint32_t lo = static_cast<uint32_t>(t.key);
+    const uint32_t c = lo & kNoCand;
+    const float err = KeyError<kNonNeg>(static_cast<uint32_t>(t.key >> 32));
+    const int tgt = lane < Hb ? Hb - 1 - lane : lane;
+    s_err = __int_as_float(__builtin_amdgcn_ds_permute(tgt << 2, __float_as_int(err)));
+    const int cand = __builtin_amdgcn_ds_permute(tgt << 2, static_cast<int>(c));
+    s_cand = cand == static_cast<int>(kNoCand) ? -1 : cand;
 }
 
 // Slow path: the reference's scan on slot arrays (NaN enters; RecomputeWorst after each insert).
@@ -222,25 +271,48 @@ __device__ __forceinline__ void ReplaySlow(bool ok, float e, int cand_base, int 
 // false as soon as a call returns false, and return true otherwise.
 // The second argument of chunks is std::false_type on the fast pass and std::true_type on the
 // slow one.
-template <bool kNonNeg, class Chunks>
-__device__ __forceinline__ void SelectTopH(int Hb, int lane, Chunks&& chunks, float& s_err, int& s_cand) {
+//
+// kRank: the fast pass's result comes out rank-indexed (lane q the q-th smallest key).
+// kBest (the best-first pass; implies kRank): no slow pass, and `flag` is set when the result
+// may differ from the reference's: an eligible NaN or -0, or an eligible candidate left out (or
+// evicted) with the same error as the final worst of a full top-H. Without such a tie the top-H
+// set does not depend on the scan order: every candidate with an error below the final worst
+// enters when it is scanned and is never evicted, whatever came before it.
+template <bool kNonNeg, bool kBest, bool kRank, class Chunks>
+__device__ __forceinline__ void SelectTopH(int Hb, int lane, Chunks&& chunks, float& s_err, int& s_cand, bool& flag) {
     TopKeys<kNonNeg> tk(lane);
-    const bool fast = chunks([&](bool ok, float e, int cand_base) { return ReplayFast(ok, e, cand_base, Hb, lane, tk); },
-                             std::false_type());
-    if (fast) {
-        ToSlots(tk, s_err, s_cand);
-        return;
+    OutTrack ot;
+    const bool fast = chunks(
+        [&](bool ok, float e, int cand_base) { return ReplayFast<kNonNeg, kBest>(ok, e, cand_base, Hb, lane, tk, ot); },
+        std::false_type());
+    if constexpr (kBest) {
+        if (!fast) {
+            flag = true;
+            s_err = kInfF;
+            s_cand = -1;
+            return;
+        }
+        const uint32_t rej = WaveMinU32(ot.rej);
+        const uint32_t out_min = rej < ot.ev ? rej : ot.ev;
+        if (tk.whi < KeyImage<kNonNeg>(kInfF) && out_min == tk.whi) flag = true;
+        ToRanks(tk, Hb, lane, s_err, s_cand);
+    } else {
+        if (fast) {
+            if (kRank) ToRanks(tk, Hb, lane, s_err, s_cand);
+            else ToSlots(tk, s_err, s_cand);
+            return;
+        }
+        TopSlots ts;
+        const int rows = (Hb + 15) >> 4;
+        chunks(
+            [&](bool ok, float e, int cand_base) {
+                ReplaySlow(ok, e, cand_base, Hb, rows, lane, ts);
+                return true;
+            },
+            std::true_type());
+        s_err = ts.s_err;
+        s_cand = ts.s_cand;
     }
-    TopSlots ts;
-    const int rows = (Hb + 15) >> 4;
-    chunks(
-        [&](bool ok, float e, int cand_base) {
-            ReplaySlow(ok, e, cand_base, Hb, rows, lane, ts);
-            return true;
-        },
-        std::true_type());
-    s_err = ts.s_err;
-    s_cand = ts.s_cand;
 }
 
 // BestSlot (beam_search.cpp:409-416): first minimum over slots [0, curH) with strict '<'.
@@ -349,12 +421,33 @@ __device__ __forceinline__ void EvalCand(RFn R, const float (&rinv)[L], const fl
     e = ee < 0.0f ? 0.0f : ee;
 }
 
-// Layer 0 of the full-precomp beam (beam_search.cpp:240-263).
+// Vector index i and beam-state index w of this wave (see LayerArgs::list); false when the wave
+// has no vector.
+__device__ __forceinline__ bool WaveItem(const LayerArgs& p, int wave, int64_t& i, int64_t& w) {
+    w = static_cast<int64_t>(blockIdx.x) * kBeamWavesPerBlock + wave;
+    if (p.list) {
+        if (w >= *p.list_n) return false;
+        i = p.list[w];
+        return true;
+    }
+    i = w;
+    return w < p.n;
+}
+
+// Best-first pass, last layer: the final pick is the first minimum over slots, so a tie for the
+// minimum makes it depend on the slot order. `err` is rank-indexed (lane 0 the smallest).
+__device__ __forceinline__ bool FinalTie(float err, int curH) {
+    return curH >= 2 && ReadLane(err, 0) == ReadLane(err, 1);
+}
+
+// Layer 0 of the full-precomp beam (beam_search.cpp:240-263). BEST: the best-first pass
+// (LayerArgs::flags); its records come out rank-indexed.
+template <bool BEST>
 __global__ __launch_bounds__(256) void Layer0Kernel(LayerArgs p) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * kBeamWavesPerBlock + wave;
-    if (i >= p.n) return;
+    int64_t i, w;
+    if (!WaveItem(p, wave, i, w)) return;
     const int m = p.m, Hb = p.Hb, K = p.K, off0 = p.offL;
     const Rec rc(m);
     const float nx2 = p.nx2[i];
@@ -363,7 +456,8 @@ __global__ __launch_bounds__(256) void Layer0Kernel(LayerArgs p) {
     const int nch = (K + kWave - 1) / kWave;
     float s_err;
     int s_cand;
-    SelectTopH<false>(
+    bool flagged = false;
+    SelectTopH<false, false, BEST>(
         Hb, lane,
         [&](auto&& replay, auto) {
             for (int j = 0; j < nch; ++j) {
@@ -378,9 +472,14 @@ __global__ __launch_bounds__(256) void Layer0Kernel(LayerArgs p) {
             }
             return true;
         },
-        s_err, s_cand);
+        s_err, s_cand, flagged);
 
     const int curH = __popcll(__ballot(lane < Hb && s_err < kInfF));  // CountFinite, no max(1,.)
+    // (Layer 0 scans in the reference order, so only the slot order of its result can differ.)
+    if (BEST && p.is_last && FinalTie(s_err, curH)) {
+        if (lane == 0) p.flags[i] = 1;
+        return;
+    }
     // Insertion-time write-back of the surviving slot contents (beam_search.cpp:253-258).
     uint8_t c0 = 0;
     float a0 = 0.0f, r00 = 0.0f;
@@ -392,7 +491,7 @@ __global__ __launch_bounds__(256) void Layer0Kernel(LayerArgs p) {
         r00 = sqrtf(alpha);
     }
     if (lane < Hb) {
-        float* rec = p.out.rec + (i * Hb + lane) * rc.stride;
+        float* rec = p.out.rec + (w * Hb + lane) * rc.stride;
         rec[0] = s_err;
         rec[rc.coef] = a0;
         rec[Rec::R(0, 0)] = r00;
@@ -400,7 +499,7 @@ __global__ __launch_bounds__(256) void Layer0Kernel(LayerArgs p) {
         reinterpret_cast<uint32_t*>(rec + rc.code)[0] = c0;
         reinterpret_cast<uint32_t*>(rec)[rc.root] = 0u;
     }
-    if (lane == 0) p.out.curH[i] = curH;
+    if (lane == 0) p.out.curH[w] = curH;
     if (p.is_last) {
         const int best = BestSlot(s_err, curH, lane);
         if (lane == best) {
@@ -416,11 +515,12 @@ __global__ __launch_bounds__(256) void Layer0Kernel(LayerArgs p) {
 //  * layers >= 11 at 4 waves (<= 128 VGPRs): left alone the allocator gives them 2-3 waves, or
 //    1 at layer 16 (> 256 VGPRs); the M=16, beam-8 encode ran 9% faster and the large-root
 //    16-layer beam-32 encode 18% faster;
-//  * on the M=8, K=256, beam-16 encode layers 4 and 6 run best at 8 waves and layer 7 at 7;
+//  * on the M=8, K=256, beam-16 encode layers 4 and 6 run best at 8 waves and layer 7 at 7, and
+//    layer 3 of the best-first pass at 8 (left alone it takes 65 VGPRs, one over);
 //  * the other layers at the allocator's own choice.
-template <int L, bool LR>
+template <int L, bool LR, bool BEST>
 constexpr int LayerMinWaves() {
-    return L >= 11 ? 4 : (LR ? 1 : ((L == 4 || L == 6) ? 8 : (L == 7 ? 7 : 1)));
+    return L >= 11 ? 4 : (LR ? 1 : ((L == 4 || L == 6 || (BEST && L == 3)) ? 8 : (L == 7 ? 7 : 1)));
 }
 
 // Layers up to kVStateMaxL read the slot state into VGPRs (see process() in LayerKernel): on the
@@ -428,20 +528,23 @@ constexpr int LayerMinWaves() {
 // extra VGPRs cost occupancy.
 constexpr int kVStateMaxL = 3;
 
-template <int L, bool LR, bool FULL>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LayerMinWaves<L, LR>(), 8))) void LayerKernel(
+// BEST: the best-first pass (LayerArgs::flags). Its input records are rank-indexed, so slots are
+// scanned in ascending error order, and so are its output records. A vector flagged by an earlier
+// layer arrives with an empty beam.
+template <int L, bool LR, bool FULL, bool BEST>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LayerMinWaves<L, LR, BEST>(), 8))) void LayerKernel(
     LayerArgs p) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * kBeamWavesPerBlock + wave;
-    if (i >= p.n) return;
+    int64_t i, w;
+    if (!WaveItem(p, wave, i, w)) return;
     const int m = p.m, Hb = p.Hb, K = FULL ? kMaxK : p.K, offL = p.offL;
     const Rec rc(m);
     const int ld = p.gram.ld;
     const float* xCi = p.xC + i * p.ldx;
     const int nch = FULL ? kMaxChunks : (K + kWave - 1) / kWave;
-    const float* __restrict__ recs_in = p.in.rec + i * Hb * rc.stride;
-    float* __restrict__ recs_out = p.out.rec + i * Hb * rc.stride;
+    const float* __restrict__ recs_in = p.in.rec + w * Hb * rc.stride;
+    float* __restrict__ recs_out = p.out.rec + w * Hb * rc.stride;
     const float* __restrict__ G = p.gram.G + offL + lane;
     const int vz = VZero();
 
@@ -454,7 +557,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LayerMinWav
         alp[j] = act ? p.gdiag[offL + k] : 0.0f;
     }
 
-    const int curH = p.in.curH[i];
+    const int curH = p.in.curH[w];
 
     // Beam slot h's codes (and root) sit in lane h, read with one vector load per word for all
     // slots at once, so a slot's G rows can be addressed without waiting for its record.
@@ -559,7 +662,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LayerMinWav
 
     float s_err;
     int s_cand;
-    SelectTopH<true>(  // errors clamped at zero (EvalCand)
+    bool flagged = false;
+    SelectTopH<true, BEST, BEST>(  // errors clamped at zero (EvalCand)
         Hb, lane,
         [&](auto&& replay, auto slow_tag) {
             for (int h = 0; h < curH; ++h) {
@@ -569,7 +673,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LayerMinWav
             }
             return true;
         },
-        s_err, s_cand);
+        s_err, s_cand, flagged);
+    if (BEST && flagged) {
+        // No records: the next layers see an empty beam (curH = 0), do no work for this vector
+        // and keep it well-formed until its re-run.
+        if (lane == 0) {
+            p.flags[i] = 1;
+            p.out.curH[w] = 0;
+        }
+        return;
+    }
 
     // Deferred write-back (beam_search.cpp:337-383) or the all-skipped fallback (:385-400).
     const int newH = __popcll(__ballot(lane < Hb && s_err < kInfF));
@@ -685,8 +798,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LayerMinWav
         }
         reinterpret_cast<uint32_t*>(ro)[rc.root] = nroot;
     }
-    if (lane == 0) p.out.curH[i] = outH;
+    if (lane == 0) p.out.curH[w] = outH;
 
+    if (BEST && p.is_last && FinalTie(out_err, outH)) {
+        if (lane == 0) p.flags[i] = 1;
+        return;
+    }
     if (p.is_last) {
         const int best = BestSlot(out_err, outH, lane);
         if (lane == best) {
@@ -733,7 +850,8 @@ __global__ __launch_bounds__(256) void RootSeedKernel(RootArgs p) {
         }
     } else {
         const float* sc = p.scores + i * p.ldx;
-        SelectTopH<false>(
+        bool unused_flag = false;
+        SelectTopH<false, false, false>(
             rs, lane,
             [&](auto&& replay, auto) {
                 for (int c0 = 0; c0 < p.h0; c0 += kWave) {
@@ -748,7 +866,7 @@ __global__ __launch_bounds__(256) void RootSeedKernel(RootArgs p) {
                 }
                 return true;
             },
-            s_err, s_cand);
+            s_err, s_cand, unused_flag);
     }
     const bool seeded = lane < rs && !(s_err >= kInfF);
     const int curH = max(1, __popcll(__ballot(seeded)));
@@ -818,7 +936,8 @@ __global__ __launch_bounds__(256) void NearestRootFixupKernel(const float* __res
         const float xn = nx2[i];
         float s_err;
         int s_cand;
-        SelectTopH<false>(
+        bool unused_flag = false;
+        SelectTopH<false, false, false>(
             1, lane,
             [&](auto&& replay, auto) {
                 for (int c0 = 0; c0 < h0; c0 += kWave) {
@@ -837,7 +956,7 @@ __global__ __launch_bounds__(256) void NearestRootFixupKernel(const float* __res
                 }
                 return true;
             },
-            s_err, s_cand);
+            s_err, s_cand, unused_flag);
         (void)s_err;
         if (lane == 0) root_out[i] = s_cand >= 0 ? static_cast<uint32_t>(s_cand) : kNoRoot;
     }
@@ -848,12 +967,16 @@ hipError_t LaunchL(bool lr, const LayerArgs& a, hipStream_t s) {
     const unsigned blocks = static_cast<unsigned>((a.n + kBeamWavesPerBlock - 1) / kBeamWavesPerBlock);
     const dim3 block(kWave * kBeamWavesPerBlock);
     const bool full = a.K == kMaxK;
-    if (lr) {
-        if (full) hipLaunchKernelGGL((LayerKernel<L, true, true>), dim3(blocks), block, 0, s, a);
-        else hipLaunchKernelGGL((LayerKernel<L, true, false>), dim3(blocks), block, 0, s, a);
+    if (lr) {  // the large-root beam always runs in the reference order
+        if (a.flags) return hipErrorInvalidValue;
+        if (full) hipLaunchKernelGGL((LayerKernel<L, true, true, false>), dim3(blocks), block, 0, s, a);
+        else hipLaunchKernelGGL((LayerKernel<L, true, false, false>), dim3(blocks), block, 0, s, a);
+    } else if (a.flags) {
+        if (full) hipLaunchKernelGGL((LayerKernel<L, false, true, true>), dim3(blocks), block, 0, s, a);
+        else hipLaunchKernelGGL((LayerKernel<L, false, false, true>), dim3(blocks), block, 0, s, a);
     } else {
-        if (full) hipLaunchKernelGGL((LayerKernel<L, false, true>), dim3(blocks), block, 0, s, a);
-        else hipLaunchKernelGGL((LayerKernel<L, false, false>), dim3(blocks), block, 0, s, a);
+        if (full) hipLaunchKernelGGL((LayerKernel<L, false, true, false>), dim3(blocks), block, 0, s, a);
+        else hipLaunchKernelGGL((LayerKernel<L, false, false, false>), dim3(blocks), block, 0, s, a);
     }
     return hipGetLastError();
 }
@@ -861,6 +984,35 @@ hipError_t LaunchL(bool lr, const LayerArgs& a, hipStream_t s) {
 }  // namespace
 
 int BeamRecordStride(int m) { return Rec(m).stride; }
+
+namespace {
+
+// Appends the index of every flagged vector to list (in no particular order) and adds the count
+// to counts[0] and counts[1]. One atomic add per wave that holds a flagged vector.
+__global__ __launch_bounds__(256) void CollectFlaggedKernel(const uint8_t* __restrict__ flags, int64_t n,
+                                                            int* __restrict__ list, int* __restrict__ counts) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int lane = threadIdx.x & 63;
+    const bool f = i < n && flags[i] != 0;
+    const uint64_t mask = Ballot(f);
+    if (mask == 0ull) return;
+    int base = 0;
+    if (lane == 0) {
+        base = atomicAdd(&counts[0], __popcll(mask));
+        atomicAdd(&counts[1], __popcll(mask));
+    }
+    base = __shfl(base, 0);
+    if (f) list[base + __popcll(mask & ((1ull << lane) - 1ull))] = static_cast<int>(i);
+}
+
+}  // namespace
+
+hipError_t LaunchCollectFlagged(const uint8_t* flags, int64_t n, int* list, int* counts, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(CollectFlaggedKernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s, flags, n,
+                       list, counts);
+    return hipGetLastError();
+}
 
 hipError_t LaunchRootSeed(const RootArgs& a, hipStream_t s) {
     if (a.n <= 0) return hipSuccess;
@@ -890,7 +1042,8 @@ hipError_t LaunchGatherRootDot(const float* X, int d, const float* C0, const uin
 hipError_t LaunchBeamLayer0(const LayerArgs& a, hipStream_t s) {
     if (a.n <= 0) return hipSuccess;
     const unsigned blocks = static_cast<unsigned>((a.n + kBeamWavesPerBlock - 1) / kBeamWavesPerBlock);
-    hipLaunchKernelGGL(Layer0Kernel, dim3(blocks), dim3(kWave * kBeamWavesPerBlock), 0, s, a);
+    if (a.flags) hipLaunchKernelGGL(Layer0Kernel<true>, dim3(blocks), dim3(kWave * kBeamWavesPerBlock), 0, s, a);
+    else hipLaunchKernelGGL(Layer0Kernel<false>, dim3(blocks), dim3(kWave * kBeamWavesPerBlock), 0, s, a);
     return hipGetLastError();
 }
 

@@ -95,6 +95,55 @@ def test_beam_degenerate_bit_exact(ctx, orc, case):
         assert np.all(same), (case, Hb, np.nonzero(~same)[0][:10])
 
 
+def _beam_both_orders(ctx, xC, Hb, nx2, monkeypatch):
+    """Beam codes, errors and re-run count with the default best-first pass, then in the
+    reference order throughout."""
+    monkeypatch.delenv("STLQ_MI355_BEAM_ORDER", raising=False)
+    codes_b, err_b = ctx.beam_search(xC, Hb, nx2=nx2)
+    reruns = ctx.last_timings().beam_reruns
+    monkeypatch.setenv("STLQ_MI355_BEAM_ORDER", "reference")
+    codes_r, err_r = ctx.beam_search(xC, Hb, nx2=nx2)
+    assert ctx.last_timings().beam_reruns == 0
+    monkeypatch.delenv("STLQ_MI355_BEAM_ORDER")
+    return codes_b, err_b, codes_r, err_r, reruns
+
+
+def test_best_first_beam_equals_reference_order(ctx, orc, monkeypatch):
+    """The best-first pass plus the re-run of its flagged vectors returns the reference order's
+    codes and errors bit for bit, and on descriptor-like data re-runs only a small fraction."""
+    X, C = rvq_problem(31, 20000, 128, 8, 256, kind="desc", train_n=4000, iters=4)
+    h = [256] * 8
+    G, inv = _set(ctx, C, h)
+    nx2 = orc.xnorm2(X)
+    xC = ctx.gemm_xc(X)
+    for Hb in (4, 16):
+        codes_b, err_b, codes_r, err_r, reruns = _beam_both_orders(ctx, xC, Hb, nx2, monkeypatch)
+        assert np.array_equal(codes_b, codes_r), Hb
+        assert np.array_equal(_bits(err_b), _bits(err_r)), Hb
+        assert reruns <= 0.01 * X.shape[0], (Hb, reruns)
+    codes_o, err_o = orc.beam_search(nx2, xC, G, h, 16)
+    assert np.array_equal(codes_b, codes_o)
+
+
+@pytest.mark.parametrize("case", ["dup_within_layer", "dup_across_layers", "scaled_copies", "nan_codeword"])
+def test_best_first_beam_reruns_ties(ctx, orc, monkeypatch, case):
+    """Ties at the top-H boundary (duplicate or zero codewords) and NaN errors send vectors to the
+    reference-order re-run; the results stay the reference's."""
+    X, C, h = degenerate_problem(case)
+    G, inv = _set(ctx, C, h)
+    nx2 = orc.xnorm2(X)
+    xC = orc.gemm_xc(C, X)
+    for Hb in (2, 5, 16):
+        codes_b, err_b, codes_r, err_r, reruns = _beam_both_orders(ctx, xC, Hb, nx2, monkeypatch)
+        assert np.array_equal(codes_b, codes_r), (case, Hb)
+        same = (_bits(err_b) == _bits(err_r)) | (np.isnan(err_b) & np.isnan(err_r))
+        assert np.all(same), (case, Hb)
+        codes_o, _ = orc.beam_search(nx2, xC, G, h, Hb)
+        assert np.array_equal(codes_b, codes_o), (case, Hb)
+        if case == "nan_codeword":  # every vector meets a NaN candidate at layer 2
+            assert reruns == X.shape[0], (case, Hb, reruns)
+
+
 def test_beam_user_precomp_nonsymmetric(ctx, orc):
     """set_precomp with a caller's G: every read uses the reference's G(row, col) element."""
     X, C = random_problem(22, 500, 16, [20, 20, 20], x_scale=2.0)
