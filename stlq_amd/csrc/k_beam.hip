@@ -787,14 +787,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LayerMinWav
         ro[0] = out_err;
         uint32_t* cw = reinterpret_cast<uint32_t*>(ro + rc.code);
 #pragma unroll
-        for (int w = 0; w <= L / 4; ++w) {
+        for (int q = 0; q <= L / 4; ++q) {
             uint32_t word = 0;
 #pragma unroll
             for (int b = 0; b < 4; ++b) {
-                const int t = 4 * w + b;
+                const int t = 4 * q + b;
                 if (t <= L) word |= static_cast<uint32_t>(ncode[t]) << (8 * b);
             }
-            cw[w] = word;
+            cw[q] = word;
         }
         reinterpret_cast<uint32_t*>(ro)[rc.root] = nroot;
     }
