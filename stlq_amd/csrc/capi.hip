@@ -114,6 +114,7 @@ struct stlq_mi355_ctx {
     DevBuf bf_flags, bf_list, bf_count;
     bool bf_reset = true;  // clear the total at the next best-first pass
     bool bf_used = false;  // a best-first pass ran since the timings were reset
+    int* bf_host = nullptr;  // pinned copy of bf_count, refreshed after every best-first pass
 
     std::vector<TileEvents> tiles;
     std::vector<hipEvent_t> event_pool;
@@ -223,6 +224,7 @@ int RunBeam(stlq_mi355_ctx* c, const float* dxC, int64_t ldx, const float* dnx2,
         HIP_TRY(c->bf_flags.Ensure(static_cast<size_t>(n)));
         HIP_TRY(c->bf_list.Ensure(static_cast<size_t>(n) * 4));
         HIP_TRY(c->bf_count.Ensure(8));
+        if (!c->bf_host) HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&c->bf_host), 8, hipHostMallocDefault));
         HIP_TRY(LaunchFill8(c->bf_flags.as<uint8_t>(), 0, n, s));
         HIP_TRY(LaunchFill8(c->bf_count.as<uint8_t>(), 0, c->bf_reset ? 8 : 4, s));
         c->bf_reset = false;
@@ -282,6 +284,8 @@ int RunBeam(stlq_mi355_ctx* c, const float* dxC, int64_t ldx, const float* dnx2,
         a.list = c->bf_list.as<int>();
         a.list_n = counts;
         RC_TRY(layers(false));
+        // for stlq_mi355_last_timings, without a synchronous copy there
+        HIP_TRY(hipMemcpyAsync(c->bf_host, counts, 8, hipMemcpyDeviceToHost, s));
     }
     if (launches) *launches += nl;
     return STLQ_MI355_OK;
@@ -669,6 +673,7 @@ int stlq_mi355_ctx_destroy(stlq_mi355_ctx* c) {
         c->st_curH[b].Release();
     }
     for (hipEvent_t e : c->event_pool) (void)hipEventDestroy(e);
+    if (c->bf_host) (void)hipHostFree(c->bf_host);
     (void)hipStreamDestroy(c->stream);
     (void)hipStreamDestroy(c->copy_stream);
     (void)hipStreamDestroy(c->aux_stream);
@@ -1075,11 +1080,7 @@ int stlq_mi355_last_timings(stlq_mi355_ctx* c, stlq_mi355_timings* out) {
             out->layer_ms[l] += lm;
         }
     }
-    if (c->bf_used && !c->tiles.empty()) {
-        int counts[2] = {0, 0};
-        HIP_TRY(hipMemcpy(counts, c->bf_count.p, sizeof(counts), hipMemcpyDeviceToHost));
-        out->beam_reruns = counts[1];
-    }
+    if (c->bf_used && c->bf_host && !c->tiles.empty()) out->beam_reruns = c->bf_host[1];  // tiles synchronized above
     if (c->overlapped && !c->tiles.empty()) {
         float env = 0.0f;
         HIP_TRY(hipEventElapsedTime(&env, c->tiles.front().e[0], c->tiles.back().e[6]));
