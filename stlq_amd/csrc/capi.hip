@@ -108,6 +108,7 @@ struct stlq_mi355_ctx {
     DevBuf ils_codes, ils_a, ils_cost;  // ILS candidate state
     DevBuf R_in, R_rm;                  // rotation: as given (column-major) and row-major
     DevBuf nearest, nearest_flag;       // large root: nearest root per vector, NaN flags
+    DevBuf icm_pend;                    // ICM: the layer's proposed code per vector
     DevBuf st_rec[2], st_curH[2];
     // Best-first beam pass: per-vector flags, the list of flagged vectors, and two counters
     // (this tile's count, and the total since the timings were last reset).
@@ -174,7 +175,8 @@ int ValidateLayers(int d, int m, const int* h_vec, int first_max) {
 // Per-vector device bytes of one encode tile.
 int64_t PerVectorBytes(int d, int m, int H, int Hb) {
     const int64_t state = static_cast<int64_t>(Hb) * 4 * BeamRecordStride(m);
-    return 4LL * d + 4 + 4LL * H + m + 4LL * m + 4 + 4 + 2 + 8 + 5 + 2 * (state + 4);  // 5: best-first flag + list
+    // ... + 5: best-first flag + list; + 4: ICM proposal
+    return 4LL * d + 4 + 4LL * H + m + 4LL * m + 4 + 4 + 2 + 8 + 5 + 4 + 2 * (state + 4);
 }
 
 int64_t TileVectors(int64_t n, int d, int m, int H, int Hb) {
@@ -383,8 +385,10 @@ int RunIcmOrders(stlq_mi355_ctx* c, const IcmProblem& P, int iters, int use_abs,
     if (iters <= 0) return STLQ_MI355_OK;
     HIP_TRY(c->active.Ensure(static_cast<size_t>(n)));
     HIP_TRY(c->changed.Ensure(static_cast<size_t>(n)));
+    HIP_TRY(c->icm_pend.Ensure(static_cast<size_t>(n) * 4));
     HIP_TRY(LaunchFill8(c->active.as<uint8_t>(), 1, n, s));
     IcmArgs q;
+    q.pend = c->icm_pend.as<int>();
     q.ls = ls;
     q.codes_rw = dcodes;
     q.G_cm = P.G_cm;
@@ -665,7 +669,7 @@ int stlq_mi355_ctx_destroy(stlq_mi355_ctx* c) {
                       &c->cost, &c->best, &c->fails, &c->active, &c->changed, &c->mse, &c->gam0, &c->roots,
                       &c->scores, &c->ils_codes, &c->ils_a, &c->ils_cost, &c->b0, &c->invnorm_small,
                       &c->R_in, &c->R_rm, &c->nearest, &c->nearest_flag, &c->bf_flags, &c->bf_list,
-                      &c->bf_count};
+                      &c->bf_count, &c->icm_pend};
     if (c->g_shared) c->G_cm.p = nullptr;
     for (DevBuf* b : bufs) b->Release();
     for (int b = 0; b < 2; ++b) {
@@ -1322,7 +1326,7 @@ int64_t LargeRootTileVectors(stlq_mi355_ctx* c, int64_t n, int Hb, bool one_scor
     const int m = c->lr_m;
     const int64_t per = 4LL * c->lr_d + 4 + 8LL * std::max(c->Hs, 1) + (one_score ? 16 : 4LL * c->h0) +
                         2 * (4LL * Hb * BeamRecordStride(m) + 4) + m + 16 +
-                        (5LL * m + 16);  // refit: b0, ICM flags, ILS candidate codes/coefficients/cost
+                        (5LL * m + 20);  // refit: b0, ICM flags and proposals, ILS candidate codes/coefficients/cost
     int64_t t = std::max<int64_t>(EnvWorkspaceBytes() / per, 1024);
     return std::min<int64_t>(t, std::max<int64_t>(n, 1));
 }

@@ -141,6 +141,7 @@ struct IcmArgs {
     uint8_t* active = nullptr;       // [n]
     uint8_t* changed = nullptr;      // [n]
     int* fails = nullptr;
+    int* pend = nullptr;             // [n] the layer's proposed code, or -1 (scoring -> re-solve)
     int j = 0;                       // layer updated by this launch
     int use_abs = 1;
     int hj = 0;

@@ -223,7 +223,8 @@ __device__ __forceinline__ float WaveMax(float v) {
 // t = lane + 64*jj of layer j:
 //   val(t) = (xC(start+t) - sum_{l != j} a_l G(start+t, flat_l)) * invnorm(start+t)
 // (subtractions in ascending l), pick the first maximum of val (or |val|), and if it differs
-// from the current code, re-solve LS and accept iff new_cost + 1e-6 < cost. For a large root
+// from the current code, propose it in pend[i]; IcmSolveBody then re-solves LS and accepts iff
+// new_cost + 1e-6 < cost. For a large root
 // (RunIcmLargeRoot, icm.cpp:437-611) layer 0's term is a0*G0S(root, start+t), the G and
 // invnorm arrays are the small layers' (G_small is symmetric, so its rows serve as columns),
 // and b0 is the vector's cached <C0[:,root], x>.
@@ -242,7 +243,6 @@ __device__ __forceinline__ void IcmLayerBody(const IcmArgs& q) {
     float* ai = p.a + i * M;
     const float* xCi = p.xC + i * p.ldx;
     const uint32_t root = LR ? p.root[i] : 0u;
-    const float b0 = LR ? p.b0[i] : 0.0f;
     int flat[M];
     float a[M];
     Flats<M, LR>(p, ci, flat);
@@ -277,9 +277,30 @@ __device__ __forceinline__ void IcmLayerBody(const IcmArgs& q) {
         }
     }
     const int best_code = (best_val > -kInfF) ? best_t : old_code;
-    if (best_code == old_code) return;
-    if (lane != 0) return;
+    if (lane == 0) q.pend[i] = best_code == old_code ? -1 : best_code;
+}
 
+// The LS re-solve and acceptance of one ICM layer update (icm.cpp:300-328), one thread per
+// vector: the scoring above proposed code pend[i] (or nothing). A thread per vector instead of
+// lane 0 of the scoring wave keeps 64 times more of these latency-bound solves in flight.
+template <int M, bool LR>
+__device__ __forceinline__ void IcmSolveBody(const IcmArgs& q) {
+    const LsArgs& p = q.ls;
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= p.n) return;
+    if (!q.active[i]) return;
+    const int best_code = q.pend[i];
+    if (best_code < 0) return;
+    const int j = q.j;
+    const int start = p.off[j];
+    uint8_t* ci = q.codes_rw + i * p.cstride;
+    const int jc = LR ? j - 1 : j;
+    float* ai = p.a + i * M;
+    const float* xCi = p.xC + i * p.ldx;
+    const uint32_t root = LR ? p.root[i] : 0u;
+    const float b0 = LR ? p.b0[i] : 0.0f;
+    int flat[M];
+    Flats<M, LR>(p, ci, flat);
     int nflat[M];
 #pragma unroll
     for (int l = 0; l < M; ++l) nflat[l] = (l == j) ? start + best_code : flat[l];
@@ -302,6 +323,10 @@ template <int M>
 __global__ __launch_bounds__(256) void IcmLayerKernel(IcmArgs q) { IcmLayerBody<M, false>(q); }
 template <int M>
 __global__ __launch_bounds__(256) void IcmLayerLargeRootKernel(IcmArgs q) { IcmLayerBody<M, true>(q); }
+template <int M>
+__global__ __launch_bounds__(256) void IcmSolveKernel(IcmArgs q) { IcmSolveBody<M, false>(q); }
+template <int M>
+__global__ __launch_bounds__(256) void IcmSolveLargeRootKernel(IcmArgs q) { IcmSolveBody<M, true>(q); }
 
 __global__ void DeactivateKernel(uint8_t* active, const uint8_t* changed, int64_t n) {
     const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -419,10 +444,13 @@ hipError_t LaunchCosts(const LsArgs& a, hipStream_t s) {
 hipError_t LaunchIcmLayer(const IcmArgs& a, hipStream_t s) {
     if (a.ls.n <= 0) return hipSuccess;
     const dim3 grid(static_cast<unsigned>((a.ls.n + 3) / 4)), block(256);
+    const dim3 grid_solve(static_cast<unsigned>((a.ls.n + 255) / 256));
     if (a.ls.root) {
         STLQ_SWITCH_M(IcmLayerLargeRootKernel, a.ls.m, grid, block, s, a);
+        STLQ_SWITCH_M(IcmSolveLargeRootKernel, a.ls.m, grid_solve, block, s, a);
     } else {
         STLQ_SWITCH_M(IcmLayerKernel, a.ls.m, grid, block, s, a);
+        STLQ_SWITCH_M(IcmSolveKernel, a.ls.m, grid_solve, block, s, a);
     }
     return hipGetLastError();
 }
