@@ -235,7 +235,9 @@ __device__ __forceinline__ void IcmLayerBody(const IcmArgs& q) {
     const int lane = threadIdx.x & 63;
     const int64_t i = static_cast<int64_t>(blockIdx.x) * 4 + wave;
     if (i >= p.n) return;
-    if (!q.active[i]) return;
+    // The vector's flag, codes and coefficients are read together, before the flag is tested,
+    // so an active vector waits for one memory round trip here, not two.
+    const bool active = q.active[i] != 0;
     const int j = q.j, hj = q.hj;
     const int start = p.off[j];
     uint8_t* ci = q.codes_rw + i * p.cstride;
@@ -249,31 +251,44 @@ __device__ __forceinline__ void IcmLayerBody(const IcmArgs& q) {
 #pragma unroll
     for (int l = 0; l < M; ++l) a[l] = ai[l];
     const int old_code = ci[jc];
+    if (!active) return;
     const float* g0 = LR ? p.G0S_rm + static_cast<int64_t>(root) * p.H : nullptr;
 
-    float best_val = -kInfF;
-    int best_t = 0x7fffffff;
-    for (int t0 = 0; t0 < hj; t0 += 64) {
-        const int t = t0 + lane;
-        float score = -kInfF;
+    // All (at most four) chunks of 64 codes are scored before any reduction, so their loads are
+    // in flight together.
+    constexpr int kChunks = 4;  // layers hold at most 256 codewords
+    float score[kChunks];
+#pragma unroll
+    for (int c = 0; c < kChunks; ++c) {
+        const int t = 64 * c + lane;
+        score[c] = -kInfF;
         if (t < hj) {
             float tmp = xCi[start + t];
             if constexpr (LR) tmp = tmp - a[0] * g0[start + t];
+            // Layer j's own term is loaded and multiplied but not subtracted (x - (+0) == x), so
+            // all M loads are unconditional and in flight together.
 #pragma unroll
             for (int l = LR ? 1 : 0; l < M; ++l) {
-                if (l == j) continue;
-                tmp = tmp - a[l] * q.G_cm[static_cast<int64_t>(flat[l]) * p.H + start + t];
+                const float prod = a[l] * q.G_cm[static_cast<int64_t>(flat[l]) * p.H + start + t];
+                tmp = tmp - (l == j ? 0.0f : prod);
             }
             const float val = tmp * q.invnorm[start + t];
-            score = q.use_abs ? fabsf(val) : val;
-            if (__builtin_isnan(score)) score = -kInfF;  // NaN never wins a strict '>' scan
+            const float sc = q.use_abs ? fabsf(val) : val;
+            score[c] = __builtin_isnan(sc) ? -kInfF : sc;  // NaN never wins a strict '>' scan
         }
-        // first maximum over this chunk, then over chunks in order (strict '>' keeps the earlier)
-        const float mx = WaveMax(score);
-        if (mx > best_val) {
-            const uint64_t eq = __ballot(t < hj && score == mx);
-            best_val = mx;
-            best_t = t0 + static_cast<int>(__builtin_ctzll(eq));
+    }
+    // The scan's first maximum (strict '>' in ascending code order): the wave maximum, then the
+    // lowest code that attains it.
+    float lane_max = score[0];
+#pragma unroll
+    for (int c = 1; c < kChunks; ++c) lane_max = fmaxf(lane_max, score[c]);
+    const float best_val = WaveMax(lane_max);
+    int best_t = 0x7fffffff;
+    if (best_val > -kInfF) {
+#pragma unroll
+        for (int c = kChunks - 1; c >= 0; --c) {
+            const uint64_t eq = __ballot(64 * c + lane < hj && score[c] == best_val);
+            if (eq) best_t = 64 * c + static_cast<int>(__builtin_ctzll(eq));
         }
     }
     const int best_code = (best_val > -kInfF) ? best_t : old_code;
