@@ -228,12 +228,43 @@ __global__ __launch_bounds__(256) void NearestRootKernel(const float* __restrict
             const int col = static_cast<int>(hb) + wn * 64 + c * 16 + r16;
             const float alpha = col < h0 ? norm0[col] : 0.0f;
             if (alpha == 0.0f) continue;  // beam_search.cpp: alpha == 0 roots are skipped
+            // a1 = RN(gam / alpha) without a division per element: gam/alpha = (gam*sc)/(alpha*sc)
+            // with sc a power of two and alpha*sc = ap in [1, 2), so q0 = sp*yp,
+            // q = fma(-fma(ap, q0, -sp), yp, q0) with yp = RN(1/ap) is the correctly rounded
+            // quotient whenever sp = gam*sc is exact and |sp| lies in [2^-100, 2^100] (the identity
+            // tests/division_check.c verifies, as for the beam's quotients). Any lane outside that
+            // range sends the column back to IEEE division.
+            int ex;
+            const float mant = frexpf(alpha, &ex);
+            const bool colfast = alpha >= 0x1p-60f && alpha <= 0x1p60f;
+            const float ap = 2.0f * mant;
+            const float sc = colfast ? ldexpf(1.0f, 1 - ex) : 0.0f;  // 0: always the IEEE path
+            const float yp = 1.0f / ap;
+            float a1v[4][4];
+            float lo = __builtin_huge_valf(), hi = 0.0f;
+#pragma unroll
+            for (int a = 0; a < 4; ++a)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float sp = acc[a][c][r] * sc;
+                    const float q0 = sp * yp;
+                    const float rr = __builtin_fmaf(ap, q0, -sp);
+                    a1v[a][r] = __builtin_fmaf(-rr, yp, q0);
+                    lo = __builtin_fminf(lo, __builtin_fabsf(sp));
+                    hi = __builtin_fmaxf(hi, __builtin_fabsf(sp));
+                }
+            if (__builtin_amdgcn_ballot_w64(!(lo >= 0x1p-100f && hi <= 0x1p100f)) != 0ull) {
+#pragma unroll
+                for (int a = 0; a < 4; ++a)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) a1v[a][r] = acc[a][c][r] / alpha;
+            }
 #pragma unroll
             for (int a = 0; a < 4; ++a)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const float gam = acc[a][c][r];
-                    const float a1 = gam / alpha;
+                    const float a1 = a1v[a][r];
                     const float e1 = xn[a][r] - gam * a1;
                     if (__builtin_isnan(e1)) nanm |= 1u << (4 * a + r);
                     if (e1 < be[a][r]) {
