@@ -512,16 +512,16 @@ __global__ __launch_bounds__(256) void Layer0Kernel(LayerArgs p) {
 // Layers L >= 1. LR selects the large-root cross-term source and reciprocal solves.
 // FULL: the layer has exactly 256 codewords (no partial chunk).
 // Minimum waves per SIMD requested from the register allocator, per layer (measured):
-//  * layers >= 11 at 4 waves (<= 128 VGPRs): left alone the allocator gives them 2-3 waves, or
-//    1 at layer 16 (> 256 VGPRs); the M=16, beam-8 encode ran 9% faster and the large-root
-//    16-layer beam-32 encode 18% faster;
+//  * layers >= 11 at 4 waves (<= 128 VGPRs), 5 for the large root: left alone the allocator
+//    gives them 2-3 waves, or 1 at layer 16 (> 256 VGPRs); the M=16, beam-8 encode ran 9% faster
+//    and the large-root 16-layer beam-32 encode 18% faster (5 waves there: another 1%);
 //  * on the M=8, K=256, beam-16 encode layers 4 and 6 run best at 8 waves and layer 7 at 7 (6 in
 //    the best-first pass, where 80 VGPRs remove its spills), and layer 3 of the best-first pass
 //    at 8 (left alone it takes 65 VGPRs, one over);
 //  * the other layers at the allocator's own choice.
 template <int L, bool LR, bool BEST>
 constexpr int LayerMinWaves() {
-    return L >= 11 ? 4
+    return L >= 11 ? (LR ? 5 : 4)
                    : (LR ? 1 : ((L == 4 || L == 6 || (BEST && L == 3)) ? 8 : (L == 7 ? (BEST ? 6 : 7) : 1)));
 }
 
