@@ -80,6 +80,9 @@ BEAM_CASES = [
     ("m16_K256_b8_decay", 18, 120, 64, [256] * 16, 8, "decay"),
     ("m1_K200_b3", 19, 500, 16, [200], 3, "gauss"),
     ("m6_K65_b33", 20, 300, 30, [65, 130, 200, 3, 256, 64], 33, "gauss"),
+    # the deepest prefixes (kMaxM = 20: layers up to 19, past the scalar-register budget)
+    ("m20_K256_b8_decay", 21, 80, 64, [256] * 20, 8, "decay"),
+    ("m20_K24_b33", 22, 200, 24, [24] * 20, 33, "gauss"),
 ]
 
 

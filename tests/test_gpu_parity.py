@@ -167,7 +167,7 @@ def test_beam_user_precomp_nonsymmetric(ctx, orc):
     assert np.array_equal(_bits(a_i), _bits(a_j))
 
 
-@pytest.mark.parametrize("m", [1, 3, 4, 5, 8, 10, 16])
+@pytest.mark.parametrize("m", [1, 3, 4, 5, 8, 10, 16, 20])
 def test_ls_and_costs_bit_exact(ctx, orc, m):
     h = [32] * m
     X, C = random_problem(30 + m, 1500, 24, h, x_scale=2.0)
@@ -186,7 +186,8 @@ def test_ls_and_costs_bit_exact(ctx, orc, m):
 
 
 @pytest.mark.parametrize("use_abs", [True, False])
-@pytest.mark.parametrize("m,K,d,iters", [(8, 256, 96, 2), (5, 64, 32, 4), (10, 32, 40, 3)])
+@pytest.mark.parametrize("m,K,d,iters", [(8, 256, 96, 2), (5, 64, 32, 4), (10, 32, 40, 3), (16, 64, 48, 1),
+                                         (20, 24, 24, 2)])
 def test_icm_bit_exact(ctx, orc, use_abs, m, K, d, iters):
     h = [K] * m
     X, C = rvq_problem(40 + m, 1200, d, m, K, kind="sphere" if d == 96 else "gauss", train_n=max(2000, 4 * K), iters=4)
@@ -441,6 +442,7 @@ LARGE_ROOT_CASES = [
     ("lr_forced", 72, 600, 32, 1000, [256, 256, 256], 32, "forced"),
     ("lr_c5_shape", 73, 300, 128, 4096, [256] * 6, 32, "nearest"),
     ("lr_m1", 74, 400, 16, 500, [], 4, "topH"),
+    ("lr_m20", 75, 200, 32, 700, [64] * 19, 16, "nearest"),
 ]
 
 
@@ -538,7 +540,7 @@ def _lr_refit_problem(ctx, orc, m, seed, n=2000, d=32, h0=1500, K=64):
     return p
 
 
-@pytest.mark.parametrize("m", [2, 5, 8, 11])
+@pytest.mark.parametrize("m", [2, 5, 8, 11, 17, 20])
 def test_large_root_ls_costs_bit_exact(ctx, orc, m):
     """SolveLeastSquaresAllLargeRoot + ComputeCostsLargeRoot on the device: b0 = <C0[:,root], x> in
     the omp-simd order, the root row of the system from norm0/G0S, the reference's cost order."""
@@ -557,7 +559,8 @@ def test_large_root_ls_costs_bit_exact(ctx, orc, m):
 
 
 @pytest.mark.parametrize("m,icm,ils,pk,off,use_abs", [(5, 2, 0, 3, 0, True), (5, 1, 3, 2, 777, False),
-                                                      (8, 2, 2, 3, 10_000, True), (3, 0, 3, 3, 5, True)])
+                                                      (8, 2, 2, 3, 10_000, True), (3, 0, 3, 3, 5, True),
+                                                      (17, 1, 1, 3, 0, True), (20, 2, 0, 2, 0, False)])
 def test_large_root_icm_ils_bit_exact(ctx, orc, m, icm, ils, pk, off, use_abs):
     """DynamicIcmWithIls*NoNormalLargeRoot on the device: roots fixed, ICM over layers 1..m-1
     with the root's G0S row, ILS rounds keyed by the global id; codes, a and cost identical."""
