@@ -217,6 +217,14 @@ __global__ __launch_bounds__(256) void NearestRootKernel(const float* __restrict
     for (int th = 0; th < tiles; ++th) {
         const int64_t hb = static_cast<int64_t>(th) * kBN;
         const bool interior = kInteriorRows && aligned && hb + kBN <= h0;
+        // The tile's ||c0||^2 values are read before its k-loop, so they have arrived by the time
+        // the epilogue needs them.
+        float alpha_c[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int col = static_cast<int>(hb) + wn * 64 + c * 16 + r16;
+            alpha_c[c] = col < h0 ? norm0[col] : 0.0f;
+        }
         floatx4 acc[4][4];
         if (interior) {
             GemmAcc<true>(X, n, d, C0, h0, i0, hb, As, Bs, acc);
@@ -226,7 +234,7 @@ __global__ __launch_bounds__(256) void NearestRootKernel(const float* __restrict
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
             const int col = static_cast<int>(hb) + wn * 64 + c * 16 + r16;
-            const float alpha = col < h0 ? norm0[col] : 0.0f;
+            const float alpha = alpha_c[c];
             if (alpha == 0.0f) continue;  // beam_search.cpp: alpha == 0 roots are skipped
             // a1 = RN(gam / alpha) without a division per element: gam/alpha = (gam*sc)/(alpha*sc)
             // with sc a power of two and alpha*sc = ap in [1, 2), so q0 = sp*yp,
