@@ -155,6 +155,21 @@ int stlq_mi355_encode_device(stlq_mi355_ctx* ctx, const float* dX, int64_t n,
                              const stlq_mi355_encode_params* params, uint8_t* dcodes,
                              float* da, float* dcost, void* stream);
 
+/* No counterpart in the reference. For callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc): the same encode as
+ * stlq_mi355_encode_device (same arguments, same results bit for bit), with every work buffer
+ * (||x||^2, xC, beam records, best-first flags and counters, LS/ICM/ILS state) taken from a
+ * 256 MiB static device array held by each device for the life of the process. The call
+ * allocates no device or pinned memory and records no events (stlq_mi355_last_timings then
+ * reports nothing). n must fit that scratch in one tile: about 16k vectors at d=128, M=8,
+ * K=256, beam 16; a larger n fails with STLQ_MI355_ERR_UNSUPPORTED and a message naming the
+ * capacity for the shape. Every call on a device shares that device's scratch, so calls that
+ * overlap in time on one device (two contexts, two streams, two threads) race; calls that are
+ * ordered on one stream are safe. */
+int stlq_mi355_encode_device_noalloc(stlq_mi355_ctx* ctx, const float* dX, int64_t n,
+                                     const stlq_mi355_encode_params* params, uint8_t* dcodes,
+                                     float* da, float* dcost, void* stream);
+
 /* Streaming encode (EncodeBaseStreaming / EncodeBaseStreamingF32,
  * src/quantizer/encode_base_streaming.cpp:1913 and :4544-4579, tile loop :2534-2620): vectors
  * are produced by `fill` into pinned host chunks of `chunk` vectors, copied to the device

@@ -107,6 +107,7 @@ SIGNATURES = {
                             _u8p, _f32p, _f32p], _int),
     "stlq_mi355_encode": ([_vp, _f32p, _i64, ctypes.POINTER(EncodeParams), _u8p, _f32p, _f32p, _f64p, _f64p], _int),
     "stlq_mi355_encode_device": ([_vp, _vp, _i64, ctypes.POINTER(EncodeParams), _vp, _vp, _vp, _vp], _int),
+    "stlq_mi355_encode_device_noalloc": ([_vp, _vp, _i64, ctypes.POINTER(EncodeParams), _vp, _vp, _vp, _vp], _int),
     "stlq_mi355_encode_stream": ([_vp, _i64, _i64, ctypes.POINTER(StreamParams), FILL_FN, SINK_FN, _vp,
                                   ctypes.POINTER(StreamStats)], _int),
     "stlq_mi355_last_timings": ([_vp, ctypes.POINTER(Timings)], _int),

@@ -8,6 +8,7 @@
 #include <chrono>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <numeric>
 #include <random>
 #include <string>
@@ -40,8 +41,11 @@ int Fail(int code, const std::string& msg) {
 struct DevBuf {
     void* p = nullptr;
     size_t bytes = 0;
+    // A range of the static no-allocation scratch lent for one call: never freed or regrown.
+    bool borrowed = false;
     hipError_t Ensure(size_t want) {
         if (want <= bytes && p) return hipSuccess;
+        if (borrowed) return hipErrorOutOfMemory;
         if (p) {
             hipError_t e = hipFree(p);
             if (e != hipSuccess) return e;
@@ -54,9 +58,10 @@ struct DevBuf {
         return e;
     }
     void Release() {
-        if (p) (void)hipFree(p);
+        if (p && !borrowed) (void)hipFree(p);
         p = nullptr;
         bytes = 0;
+        borrowed = false;
     }
     template <class T>
     T* as() const {
@@ -80,6 +85,37 @@ int64_t EnvWorkspaceBytes() {
     double gb = s ? std::atof(s) : 24.0;
     if (!(gb > 0.0)) gb = 24.0;
     return static_cast<int64_t>(gb * 1024.0 * 1024.0 * 1024.0);
+}
+
+// Static device scratch of stlq_mi355_encode_device_noalloc: every work buffer of that entry
+// point (||x||^2, xC, beam records, flags, counters, ICM/ILS state) is a range of this array, so
+// the call allocates nothing. Each device holds its own copy for the life of the process; host
+// code reaches it only through the address hipGetSymbolAddress returns for that device
+// (ScratchAddress), never through the symbol itself.
+constexpr size_t kScratchBytes = size_t{256} << 20;
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+}  // namespace
+
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace {
+
+// The device address of `scratch` on `device` (which must be current), looked up once per device.
+hipError_t ScratchAddress(int device, void** out) {
+    *out = nullptr;
+    if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[device]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        g_scratch_ptr[device] = p;
+    }
+    *out = g_scratch_ptr[device];
+    return hipSuccess;
 }
 
 }  // namespace
@@ -116,6 +152,9 @@ struct stlq_mi355_ctx {
     bool bf_reset = true;  // clear the total at the next best-first pass
     bool bf_used = false;  // a best-first pass ran since the timings were reset
     int* bf_host = nullptr;  // pinned copy of bf_count, refreshed after every best-first pass
+
+    void* scratch = nullptr;  // this device's address of the static no-allocation scratch
+    bool noalloc = false;     // inside stlq_mi355_encode_device_noalloc: no pinned copies, no events
 
     std::vector<TileEvents> tiles;
     std::vector<hipEvent_t> event_pool;
@@ -226,11 +265,12 @@ int RunBeam(stlq_mi355_ctx* c, const float* dxC, int64_t ldx, const float* dnx2,
         HIP_TRY(c->bf_flags.Ensure(static_cast<size_t>(n)));
         HIP_TRY(c->bf_list.Ensure(static_cast<size_t>(n) * 4));
         HIP_TRY(c->bf_count.Ensure(8));
-        if (!c->bf_host) HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&c->bf_host), 8, hipHostMallocDefault));
+        if (!c->bf_host && !c->noalloc)
+            HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&c->bf_host), 8, hipHostMallocDefault));
         HIP_TRY(LaunchFill8(c->bf_flags.as<uint8_t>(), 0, n, s));
-        HIP_TRY(LaunchFill8(c->bf_count.as<uint8_t>(), 0, c->bf_reset ? 8 : 4, s));
-        c->bf_reset = false;
-        c->bf_used = true;
+        HIP_TRY(LaunchFill8(c->bf_count.as<uint8_t>(), 0, (c->bf_reset || c->noalloc) ? 8 : 4, s));
+        c->bf_reset = c->noalloc;  // (the no-allocation call's counters are its own)
+        c->bf_used = !c->noalloc;
     }
     auto mark = [&](int k) -> hipError_t {
         if (!te) return hipSuccess;
@@ -287,7 +327,7 @@ int RunBeam(stlq_mi355_ctx* c, const float* dxC, int64_t ldx, const float* dnx2,
         a.list_n = counts;
         RC_TRY(layers(false));
         // for stlq_mi355_last_timings, without a synchronous copy there
-        HIP_TRY(hipMemcpyAsync(c->bf_host, counts, 8, hipMemcpyDeviceToHost, s));
+        if (!c->noalloc) HIP_TRY(hipMemcpyAsync(c->bf_host, counts, 8, hipMemcpyDeviceToHost, s));
     }
     if (launches) *launches += nl;
     return STLQ_MI355_OK;
@@ -653,6 +693,12 @@ int stlq_mi355_ctx_create(int device, stlq_mi355_ctx** out) {
     if (c->fails.Ensure(256) != hipSuccess) {
         delete c;
         return Fail(STLQ_MI355_ERR_HIP, "allocation failed");
+    }
+    // Once per device, with the device current: the address of the no-allocation scratch.
+    const hipError_t se = ScratchAddress(device, &c->scratch);
+    if (se != hipSuccess) {
+        stlq_mi355_ctx_destroy(c);
+        return Fail(STLQ_MI355_ERR_HIP, std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(se));
     }
     *out = c;
     return STLQ_MI355_OK;
@@ -1053,6 +1099,129 @@ int stlq_mi355_encode_device(stlq_mi355_ctx* c, const float* dX, int64_t n, cons
         RC_TRY(EncodeTile(c, dX + t0 * c->d, nt, *params, o, s, true, true, static_cast<uint64_t>(t0)));
     }
     return STLQ_MI355_OK;
+}
+
+}  // extern "C"
+
+namespace {
+
+// The work buffers one full-precomp encode tile of n vectors asks for (EncodeTile without the
+// sub-tile overlap, BeamAndRefit, RunBeam, RunIcmIls), with their sizes: the no-allocation entry
+// point lends each of them a 256-byte-aligned range of the static scratch.
+constexpr int kMaxLease = 24;
+struct LeaseItem {
+    DevBuf* buf;
+    size_t bytes;
+};
+
+int NoAllocPlan(stlq_mi355_ctx* c, int64_t n, const stlq_mi355_encode_params& P, bool has_a, bool has_cost,
+                LeaseItem (&items)[kMaxLease], int* count, size_t* total) {
+    const size_t N = static_cast<size_t>(n), m = static_cast<size_t>(c->m), H = static_cast<size_t>(c->H);
+    const size_t Hb = static_cast<size_t>(std::max(1, P.H_beam));
+    const size_t rec = N * Hb * 4 * static_cast<size_t>(BeamRecordStride(c->m));
+    const bool refine = P.icm_iters > 0 || P.ils_iters > 0;
+    const bool need_ls = P.want_coeffs || refine;
+    int k = 0;
+    auto add = [&](DevBuf& b, size_t bytes) { items[k++] = LeaseItem{&b, std::max<size_t>(bytes, 1)}; };
+    add(c->nx2, N * 4);
+    add(c->xC, N * H * 4);
+    for (int b = 0; b < 2; ++b) {
+        add(c->st_rec[b], rec);
+        add(c->st_curH[b], N * 4);
+    }
+    add(c->bf_flags, N);
+    add(c->bf_list, N * 4);
+    add(c->bf_count, 8);
+    add(c->fails, 4);
+    if (need_ls && !has_a) add(c->a, N * m * 4);
+    if (need_ls && !has_cost) add(c->cost, N * 4);
+    if (P.icm_iters > 0) {
+        add(c->active, N);
+        add(c->changed, N);
+        add(c->icm_pend, N * 4);
+    }
+    if (P.ils_iters > 0 && P.perturb_k > 0 && c->m > 1) {
+        add(c->ils_codes, N * m);
+        add(c->ils_a, N * m * 4);
+        add(c->ils_cost, N * 4);
+    }
+    size_t t = 0;
+    for (int i = 0; i < k; ++i) t += (items[i].bytes + 255) & ~size_t{255};
+    *count = k;
+    *total = t;
+    return STLQ_MI355_OK;
+}
+
+// Lends the planned ranges of the scratch to the context's buffers for one call and gives the
+// context its own buffers back afterwards.
+class ScratchLease {
+   public:
+    ScratchLease(stlq_mi355_ctx* c, const LeaseItem* items, int count) : c_(c), count_(count) {
+        char* base = static_cast<char*>(c->scratch);
+        size_t off = 0;
+        for (int i = 0; i < count; ++i) {
+            saved_[i] = *items[i].buf;
+            bufs_[i] = items[i].buf;
+            DevBuf lent;
+            lent.p = base + off;
+            lent.bytes = items[i].bytes;
+            lent.borrowed = true;
+            *items[i].buf = lent;
+            off += (items[i].bytes + 255) & ~size_t{255};
+        }
+        c->noalloc = true;
+    }
+    ~ScratchLease() {
+        for (int i = 0; i < count_; ++i) *bufs_[i] = saved_[i];
+        c_->noalloc = false;
+    }
+
+   private:
+    stlq_mi355_ctx* c_;
+    int count_;
+    DevBuf* bufs_[kMaxLease] = {};
+    DevBuf saved_[kMaxLease];
+};
+
+}  // namespace
+
+extern "C" {
+
+int stlq_mi355_encode_device_noalloc(stlq_mi355_ctx* c, const float* dX, int64_t n,
+                                     const stlq_mi355_encode_params* params, uint8_t* dcodes, float* da,
+                                     float* dcost, void* stream) {
+    RC_TRY(CheckPre(c));
+    RC_TRY(CheckParams(params));
+    if (n < 0 || (n > 0 && (!dX || !dcodes))) return Fail(STLQ_MI355_ERR_INVALID, "bad arguments");
+    if (!c->scratch) return Fail(STLQ_MI355_ERR_STATE, "no-allocation scratch unavailable on this device");
+    if (n == 0) return STLQ_MI355_OK;
+    LeaseItem items[kMaxLease];
+    int count = 0;
+    size_t total = 0;
+    RC_TRY(NoAllocPlan(c, n, *params, da != nullptr, dcost != nullptr, items, &count, &total));
+    if (total > kScratchBytes) {
+        // capacity for this shape: the largest tile whose plan fits the scratch
+        int64_t lo = 0, hi = n;
+        while (lo < hi) {
+            const int64_t mid = lo + (hi - lo + 1) / 2;
+            LeaseItem tmp[kMaxLease];
+            int cnt = 0;
+            size_t tot = 0;
+            RC_TRY(NoAllocPlan(c, mid, *params, da != nullptr, dcost != nullptr, tmp, &cnt, &tot));
+            if (tot <= kScratchBytes) lo = mid;
+            else hi = mid - 1;
+        }
+        return Fail(STLQ_MI355_ERR_UNSUPPORTED,
+                    "n = " + std::to_string(n) + " exceeds the no-allocation capacity of " + std::to_string(lo) +
+                        " vectors for this shape (" + std::to_string(kScratchBytes >> 20) + " MiB device scratch); "
+                        "use stlq_mi355_encode_device or smaller batches");
+    }
+    c->ResetTimings();
+    hipStream_t s = stream ? static_cast<hipStream_t>(stream) : c->stream;
+    ScratchLease lease(c, items, count);
+    HIP_TRY(LaunchFill8(c->fails.as<uint8_t>(), 0, 4, s));  // the scratch keeps the previous call's bytes
+    EncodeOut o{dcodes, da, dcost, nullptr};
+    return EncodeTile(c, dX, n, *params, o, s, /*record=*/false, /*allow_overlap=*/false, 0);
 }
 
 int stlq_mi355_last_timings(stlq_mi355_ctx* c, stlq_mi355_timings* out) {

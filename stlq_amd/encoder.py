@@ -242,6 +242,14 @@ class Context:
                                                 ctypes.c_void_p(dcost) if dcost else None,
                                                 ctypes.c_void_p(stream) if stream else None))
 
+    def encode_device_noalloc(self, dX, n, cfg: EncodeConfig, dcodes, da=None, dcost=None, stream=None):
+        """encode_device without any device allocation (static per-device scratch; one tile)."""
+        p = cfg.to_c()
+        check(self.lib.stlq_mi355_encode_device_noalloc(self.h, ctypes.c_void_p(dX), int(n), ctypes.byref(p),
+                                                        ctypes.c_void_p(dcodes), ctypes.c_void_p(da) if da else None,
+                                                        ctypes.c_void_p(dcost) if dcost else None,
+                                                        ctypes.c_void_p(stream) if stream else None))
+
     def device_info(self):
         buf = ctypes.create_string_buffer(128)
         cu = ctypes.c_int(0)
