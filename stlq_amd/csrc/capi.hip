@@ -3,6 +3,7 @@
 #include "stlq_mi355.h"
 #include "stlq_mi355_tools.h"
 #include "internal.hpp"
+#include "prune_bound.hpp"
 
 #include <algorithm>
 #include <chrono>
@@ -132,12 +133,18 @@ struct stlq_mi355_ctx {
     int h_vec[kMaxM] = {}, off[kMaxM] = {};
     DevBuf C_all, G_rm, G_cm, gdiag, invnorm;
     bool g_shared = true;  // G_cm aliases G_rm (symmetric G built on the device)
+    // Beam candidate pruning (prune_bound.hpp): the codewords' scalings sw, isw and the row-scaled
+    // Gram Gs; allowed when max |G| <= 2^30.
+    DevBuf Gs, sw, isw, absmax;
+    bool prune_full = false;
 
     // Large-root precomp (BuildPrecompLargeRoot).
     bool has_lr = false;
     int lr_d = 0, lr_m = 0, h0 = 0, Hs = 0;
     int lr_h[kMaxM] = {}, soff[kMaxM] = {};
     DevBuf C0, Cs, norm0, G_small, G0S, gdiag_small, invnorm_small;
+    DevBuf Gs_small, sw_small, isw_small, sw0, isw0;  // the same for the small layers and the roots
+    bool prune_lr = false;      // max |G_small|, |G0S| <= 2^30
 
     // Work buffers (grown on demand, reused across calls).
     DevBuf X, nx2, xC, xC_in, codes, a, cost, best, fails, active, changed, mse, gam0, roots, scores, b0;
@@ -179,6 +186,25 @@ struct stlq_mi355_ctx {
 };
 
 namespace {
+
+// Candidate pruning in the beam (on unless STLQ_MI355_PRUNE=0). It never changes a result: a
+// pruned candidate is one the reference's rule rejects.
+bool PruneEnv() {
+    const char* v = std::getenv("STLQ_MI355_PRUNE");
+    return !(v && std::strcmp(v, "0") == 0);
+}
+
+// Whether max |x| over the n floats at x (device) lies within the pruning envelope (2^30).
+int GramInEnvelope(stlq_mi355_ctx* c, const float* const* mats, const int64_t* counts, int nm, bool* ok) {
+    HIP_TRY(c->absmax.Ensure(4));
+    HIP_TRY(LaunchFill8(c->absmax.as<uint8_t>(), 0, 4, c->stream));
+    for (int i = 0; i < nm; ++i) HIP_TRY(LaunchAbsMaxBits(mats[i], counts[i], c->absmax.as<unsigned>(), c->stream));
+    unsigned bits = 0xFFFFFFFFu;
+    HIP_TRY(hipMemcpyAsync(&bits, c->absmax.p, 4, hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    *ok = bits <= prune::kGAbsMaxBits;
+    return STLQ_MI355_OK;
+}
 
 int CheckCtx(stlq_mi355_ctx* ctx) {
     if (!ctx) return Fail(STLQ_MI355_ERR_INVALID, "null context");
@@ -287,6 +313,10 @@ int RunBeam(stlq_mi355_ctx* c, const float* dxC, int64_t ldx, const float* dnx2,
     a.ldx = ldx;
     a.nx2 = dnx2;
     a.gdiag = c->gdiag.as<float>();
+    a.Gs = c->Gs.as<float>();
+    a.sw = c->sw.as<float>();
+    a.isw = c->isw.as<float>();
+    a.prune = (c->prune_full && PruneEnv()) ? 1 : 0;
     a.n = n;
     a.m = c->m;
     a.Hb = Hb;
@@ -715,7 +745,8 @@ int stlq_mi355_ctx_destroy(stlq_mi355_ctx* c) {
                       &c->cost, &c->best, &c->fails, &c->active, &c->changed, &c->mse, &c->gam0, &c->roots,
                       &c->scores, &c->ils_codes, &c->ils_a, &c->ils_cost, &c->b0, &c->invnorm_small,
                       &c->R_in, &c->R_rm, &c->nearest, &c->nearest_flag, &c->bf_flags, &c->bf_list,
-                      &c->bf_count, &c->icm_pend};
+                      &c->bf_count, &c->icm_pend, &c->Gs, &c->sw, &c->isw, &c->absmax, &c->Gs_small,
+                      &c->sw_small, &c->isw_small, &c->sw0, &c->isw0};
     if (c->g_shared) c->G_cm.p = nullptr;
     for (DevBuf* b : bufs) b->Release();
     for (int b = 0; b < 2; ++b) {
@@ -729,6 +760,20 @@ int stlq_mi355_ctx_destroy(stlq_mi355_ctx* c) {
     (void)hipStreamDestroy(c->aux_stream);
     delete c;
     return STLQ_MI355_OK;
+}
+
+// The pruning scalings, the row-scaled Gram and the pruning envelope of the full precomp
+// (synchronizes the stream).
+static int SetPruneFull(stlq_mi355_ctx* c) {
+    const size_t H = static_cast<size_t>(c->H);
+    HIP_TRY(c->sw.Ensure(H * 4));
+    HIP_TRY(c->isw.Ensure(H * 4));
+    HIP_TRY(c->Gs.Ensure(H * H * 4));
+    HIP_TRY(LaunchPruneScale(c->gdiag.as<float>(), c->H, c->sw.as<float>(), c->isw.as<float>(), c->stream));
+    HIP_TRY(LaunchRowScale(c->G_rm.as<float>(), c->H, c->H, c->sw.as<float>(), c->Gs.as<float>(), c->stream));
+    const float* mats[1] = {c->G_rm.as<float>()};
+    const int64_t counts[1] = {static_cast<int64_t>(H * H)};
+    return GramInEnvelope(c, mats, counts, 1, &c->prune_full);
 }
 
 static int SetPrecompCommon(stlq_mi355_ctx* c, int d, int m, const int* h_vec, const float* C_all) {
@@ -763,7 +808,7 @@ int stlq_mi355_set_codebooks(stlq_mi355_ctx* c, int d, int m, const int* h_vec, 
     HIP_TRY(LaunchGram(c->C_all.as<float>(), d, c->H, c->G_rm.as<float>(), c->stream));
     HIP_TRY(LaunchNorms(c->C_all.as<float>(), d, c->H, false, nullptr, c->invnorm.as<float>(), c->stream));
     HIP_TRY(LaunchDiag(c->G_rm.as<float>(), c->H, c->gdiag.as<float>(), c->stream));
-    HIP_TRY(hipStreamSynchronize(c->stream));
+    RC_TRY(SetPruneFull(c));
     c->has_pre = true;
     return STLQ_MI355_OK;
 }
@@ -782,7 +827,7 @@ int stlq_mi355_set_precomp(stlq_mi355_ctx* c, int d, int m, const int* h_vec, co
     HIP_TRY(LaunchTranspose(c->G_cm.as<float>(), c->H, c->H, c->G_rm.as<float>(), c->stream));
     HIP_TRY(hipMemcpyAsync(c->invnorm.p, invnorm, H * 4, hipMemcpyHostToDevice, c->stream));
     HIP_TRY(LaunchDiag(c->G_rm.as<float>(), c->H, c->gdiag.as<float>(), c->stream));
-    HIP_TRY(hipStreamSynchronize(c->stream));
+    RC_TRY(SetPruneFull(c));
     c->has_pre = true;
     return STLQ_MI355_OK;
 }
@@ -1534,6 +1579,8 @@ int LargeRootTile(stlq_mi355_ctx* c, const float* dX, int64_t nt, int Hb, int ro
     RootArgs ra;
     ra.nx2 = c->nx2.as<float>();
     ra.norm0 = c->norm0.as<float>();
+    ra.sw0 = c->sw0.as<float>();
+    ra.isw0 = c->isw0.as<float>();
     ra.out = StateOf(c, 0);
     ra.n = nt;
     ra.m = m;
@@ -1588,6 +1635,12 @@ int LargeRootTile(stlq_mi355_ctx* c, const float* dX, int64_t nt, int Hb, int ro
     a.ldx = Hs;
     a.nx2 = c->nx2.as<float>();
     a.gdiag = c->gdiag_small.as<float>();
+    a.Gs = c->Gs_small.as<float>();
+    a.sw = c->sw_small.as<float>();
+    a.isw = c->isw_small.as<float>();
+    a.sw0 = c->sw0.as<float>();
+    a.isw0 = c->isw0.as<float>();
+    a.prune = (c->prune_lr && PruneEnv()) ? 1 : 0;
     a.n = nt;
     a.m = m;
     a.Hb = Hb;
@@ -1675,6 +1728,25 @@ int stlq_mi355_set_large_root(stlq_mi355_ctx* c, int d, int m, const int* h_vec,
         HIP_TRY(LaunchDiag(c->G_small.as<float>(), c->Hs, c->gdiag_small.as<float>(), c->stream));
         // precomp_large_root.cpp:101-114: invnorm_small_flat from the omp-simd Norm2
         HIP_TRY(LaunchNorms(c->Cs.as<float>(), d, c->Hs, true, nullptr, c->invnorm_small.as<float>(), c->stream));
+    }
+    // Beam candidate pruning: the roots' and small codewords' scalings, the row-scaled small Gram,
+    // and the envelope.
+    HIP_TRY(c->sw0.Ensure(h0 * 4));
+    HIP_TRY(c->isw0.Ensure(h0 * 4));
+    HIP_TRY(c->sw_small.Ensure(Hs * 4));
+    HIP_TRY(c->isw_small.Ensure(Hs * 4));
+    HIP_TRY(c->Gs_small.Ensure(Hs * Hs * 4));
+    HIP_TRY(LaunchPruneScale(c->norm0.as<float>(), c->h0, c->sw0.as<float>(), c->isw0.as<float>(), c->stream));
+    if (c->Hs > 0) {
+        HIP_TRY(LaunchPruneScale(c->gdiag_small.as<float>(), c->Hs, c->sw_small.as<float>(), c->isw_small.as<float>(),
+                                 c->stream));
+        HIP_TRY(LaunchRowScale(c->G_small.as<float>(), c->Hs, c->Hs, c->sw_small.as<float>(), c->Gs_small.as<float>(),
+                               c->stream));
+        const float* mats[2] = {c->G_small.as<float>(), c->G0S.as<float>()};
+        const int64_t counts[2] = {static_cast<int64_t>(c->Hs) * c->Hs, static_cast<int64_t>(h0) * c->Hs};
+        RC_TRY(GramInEnvelope(c, mats, counts, 2, &c->prune_lr));
+    } else {
+        c->prune_lr = false;
     }
     HIP_TRY(hipStreamSynchronize(c->stream));
     c->has_lr = true;

@@ -19,7 +19,8 @@ __host__ __device__ inline int CodeStride(int m) { return (m + 3) & ~3; }
 // Beam state of one tile of vectors, slot-major (vector i, slot s at i*Hb + s). Each slot is
 // one record of BeamRecordStride(m) dwords: [err, the Cholesky factor R column by column with
 // each column followed by the reciprocal of its diagonal (m(m+3)/2), coef[m],
-// codes (CodeStride(m) bytes), root id, padding to 16 bytes].
+// codes (CodeStride(m) bytes), root id, the two pruning constants kap and phi, padding to
+// 16 bytes].
 struct BeamState {
     float* rec = nullptr;        // [n*Hb*BeamRecordStride(m)]
     int* curH = nullptr;         // [n]
@@ -43,6 +44,16 @@ struct LayerArgs {
     int64_t ldx = 0;
     const float* nx2 = nullptr;   // [n]
     const float* gdiag = nullptr; // G diagonal over the same flat index space
+    // Candidate pruning (prune_bound.hpp), over the same flat index space as gdiag:
+    // isw[f] = RN(sqrt(gdiag[f])), sw[f] = RN(1/isw[f]), Gs = G with row f scaled by sw[f]
+    // (row-major, same ld; the large root's prefix 0 is scaled by sw0[root] on the fly);
+    // sw0/isw0 the same for the roots of a large root. prune = 0 turns it off.
+    const float* Gs = nullptr;
+    const float* sw = nullptr;
+    const float* isw = nullptr;
+    const float* sw0 = nullptr;
+    const float* isw0 = nullptr;
+    int prune = 0;
     BeamState in, out;
     int64_t n = 0;
     int m = 0, Hb = 0, K = 0, offL = 0;
@@ -68,6 +79,8 @@ struct RootArgs {
     int64_t ldx = 0;
     const float* nx2 = nullptr;
     const float* norm0 = nullptr;   // [h0]
+    const float* sw0 = nullptr;     // [h0] pruning scalings of the roots (LayerArgs::sw0, isw0)
+    const float* isw0 = nullptr;
     const uint32_t* forced = nullptr;
     BeamState out;
     int64_t n = 0;
@@ -85,6 +98,12 @@ hipError_t LaunchNorms(const float* C, int d, int H, bool lane4, float* norm2, f
 hipError_t LaunchRootDot(const float* X, int d, const float* C0, const uint32_t* root, int64_t n, float* out,
                          hipStream_t s);
 hipError_t LaunchDiag(const float* G_rm, int H, float* diag, hipStream_t s);
+// Pruning scalings of n codewords from their squared norms g: isw = RN(sqrt(g)), sw = RN(1/isw).
+hipError_t LaunchPruneScale(const float* g, int64_t n, float* sw, float* isw, hipStream_t s);
+// Gs(r, c) = G(r, c) * sw[r] for a row-major rows x cols matrix (row stride cols).
+hipError_t LaunchRowScale(const float* G, int64_t rows, int cols, const float* sw, float* Gs, hipStream_t s);
+// *out = max over i of the bits of |x[i]| (NaN above +inf); *out must be cleared beforehand.
+hipError_t LaunchAbsMaxBits(const float* x, int64_t n, unsigned* out, hipStream_t s);
 hipError_t LaunchTranspose(const float* in, int rows, int cols, float* out, hipStream_t s);
 hipError_t LaunchXNorm2(const float* X, int d, int64_t n, float* out, hipStream_t s);
 hipError_t LaunchGemmXc(const float* X, int64_t n, int d, const float* C, int H, float* xC, int64_t ldx,

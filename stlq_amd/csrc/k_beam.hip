@@ -23,6 +23,7 @@
 #include <type_traits>
 
 #include "internal.hpp"
+#include "prune_bound.hpp"
 
 namespace stlq_mi355 {
 namespace {
@@ -164,10 +165,11 @@ __device__ __forceinline__ void ToSlots(const TopKeys<kNonNeg>& t, float& s_err,
     s_cand = cand == static_cast<int>(kNoCand) ? -1 : cand;
 }
 
-// Replays the streaming top-H over one chunk of 64 candidates in lane (= scan) order.
+// Replays the streaming top-H over one group of 64 candidates in lane (= scan) order; lane l
+// carries candidate id `cand` (ids ascend with the lane among the eligible lanes).
 // Candidate `lane` is eligible when ok; it is inserted when !(e >= worst)
 // (beam_search.cpp:320: `if (e >= worst_err) continue;`), into the worst slot.
-// cand_base + lane must stay below 2^26 - 1 (callers check).
+// cand must stay below 2^26 - 1 (callers check).
 //
 // Fast path: returns false, leaving t as it was, when an eligible candidate is NaN or -0 (the
 // caller then replays the layer with ReplaySlow). Otherwise e < worst exactly when
@@ -181,7 +183,7 @@ struct OutTrack {
 };
 
 template <bool kNonNeg, bool kTrack>
-__device__ __forceinline__ bool ReplayFast(bool ok, float e, int cand_base, int Hb, int lane, TopKeys<kNonNeg>& t,
+__device__ __forceinline__ bool ReplayFast(bool ok, float e, int cand, int Hb, int lane, TopKeys<kNonNeg>& t,
                                            OutTrack& ot) {
     const uint64_t okm = Ballot(ok);
     const bool bad = kNonNeg ? (__float_as_uint(e) > 0x7F800000u) : __builtin_amdgcn_classf(e, 0x23);
@@ -199,7 +201,7 @@ __device__ __forceinline__ bool ReplayFast(bool ok, float e, int cand_base, int 
         }
         // the new pair takes the evicted slot: the slot field of lane 0's key
         const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(oe), l));
-        const uint32_t lo = (t.wlo & 0xFC000000u) | static_cast<uint32_t>(cand_base + l);
+        const uint32_t lo = (t.wlo & 0xFC000000u) | static_cast<uint32_t>(__builtin_amdgcn_readlane(cand, l));
         const uint64_t nk = (static_cast<uint64_t>(hi) << 32) | lo;
         const int r = __popcll(Ballot(t.key > nk) & keep);
         const uint64_t sh = WaveShl1(t.key);
@@ -250,15 +252,16 @@ __device__ __forceinline__ void ToRanks(const TopKeys<kNonNeg>& t, int Hb, int l
 // Slow path: the reference's scan on slot arrays (NaN enters; RecomputeWorst after each insert).
 // The worst can rise here (to NaN), so the eligible lanes after an insertion are re-tested from
 // all ok lanes behind it, not only from the ones that were eligible before.
-__device__ __forceinline__ void ReplaySlow(bool ok, float e, int cand_base, int Hb, int rows, int lane, TopSlots& t) {
+__device__ __forceinline__ void ReplaySlow(bool ok, float e, int cand, int Hb, int rows, int lane, TopSlots& t) {
     const uint64_t okm = Ballot(ok);
     uint64_t mask = okm & Ballot(!(e >= t.worst));
     while (mask) {
         const int l = static_cast<int>(__builtin_ctzll(mask));
         const float ev = ReadLane(e, l);
+        const int cl = __builtin_amdgcn_readlane(cand, l);
         if (lane == t.widx) {
             t.s_err = ev;
-            t.s_cand = cand_base + l;
+            t.s_cand = cl;
         }
         RecomputeWorst(t.s_err, Hb, rows, lane, t.worst, t.widx);
         mask = okm & AboveLane(l) & Ballot(!(e >= t.worst));
@@ -267,10 +270,11 @@ __device__ __forceinline__ void ReplaySlow(bool ok, float e, int cand_base, int 
 
 // Runs `chunks(replay)` with the fast replay and, if it reports a NaN or -0, again from the start
 // with the slow one; returns the slot-indexed (error, candidate) of the final top-H.
-// chunks(replay) must call replay(ok, e, cand_base) for every chunk in scan order, stop and return
-// false as soon as a call returns false, and return true otherwise.
+// chunks(replay, tag, worst) must call replay(ok, e, cand) for every group of candidates in scan
+// order, stop and return false as soon as a call returns false, and return true otherwise.
 // The second argument of chunks is std::false_type on the fast pass and std::true_type on the
-// slow one.
+// slow one; the third returns the current worst error (+inf while a slot is empty), which only
+// falls during the fast pass.
 //
 // kRank: the fast pass's result comes out rank-indexed (lane q the q-th smallest key).
 // kBest (the best-first pass; implies kRank): no slow pass, and `flag` is set when the result
@@ -283,8 +287,8 @@ __device__ __forceinline__ void SelectTopH(int Hb, int lane, Chunks&& chunks, fl
     TopKeys<kNonNeg> tk(lane);
     OutTrack ot;
     const bool fast = chunks(
-        [&](bool ok, float e, int cand_base) { return ReplayFast<kNonNeg, kBest>(ok, e, cand_base, Hb, lane, tk, ot); },
-        std::false_type());
+        [&](bool ok, float e, int cand) { return ReplayFast<kNonNeg, kBest>(ok, e, cand, Hb, lane, tk, ot); },
+        std::false_type(), [&]() { return KeyError<kNonNeg>(tk.whi); });
     if constexpr (kBest) {
         if (!fast) {
             flag = true;
@@ -305,11 +309,11 @@ __device__ __forceinline__ void SelectTopH(int Hb, int lane, Chunks&& chunks, fl
         TopSlots ts;
         const int rows = (Hb + 15) >> 4;
         chunks(
-            [&](bool ok, float e, int cand_base) {
-                ReplaySlow(ok, e, cand_base, Hb, rows, lane, ts);
+            [&](bool ok, float e, int cand) {
+                ReplaySlow(ok, e, cand, Hb, rows, lane, ts);
                 return true;
             },
-            std::true_type());
+            std::true_type(), [&]() { return ts.worst; });
         s_err = ts.s_err;
         s_cand = ts.s_cand;
     }
@@ -328,17 +332,28 @@ __device__ __forceinline__ int BestSlot(float err, int curH, int lane) {
 }
 
 // Record layout of one beam slot (dword offsets); stride dwords per slot:
-// [err, R column by column, coef[m], codes, root id, padding to 16 bytes]. Column c of the
-// Cholesky factor holds R(0..c, c) followed by RN(1/R(c,c)) (formed once when the slot is made),
-// so the first L columns sit at offsets that depend on L only and a layer-L kernel reads them
-// with immediate offsets.
+// [err, R column by column, coef[m], codes, root id, kap, phi, kb, cq, padding to 16 bytes].
+// Column c of the Cholesky factor holds R(0..c, c) followed by RN(1/R(c,c)) (formed once when the
+// slot is made), so the first L columns sit at offsets that depend on L only and a layer-L kernel
+// reads them with immediate offsets. kap, phi, kb and cq are the slot's pruning constants
+// (prune_bound.hpp).
 struct Rec {
-    int coef, code, root, stride;
+    int coef, code, root, kap, phi, kb, cq, stride;
     __host__ __device__ explicit Rec(int m) {
         coef = 1 + m * (m + 3) / 2;
         code = coef + m;
         root = code + CodeStride(m) / 4;
-        stride = (root + 1 + 3) & ~3;
+        kap = root + 1;
+        phi = root + 2;
+        kb = root + 3;
+        cq = root + 4;
+        stride = (root + 5 + 3) & ~3;
+    }
+    __device__ void PutBounds(float* rec, const prune::SlotBounds& b) const {
+        rec[kap] = b.kap;
+        rec[phi] = b.phi;
+        rec[kb] = b.kb;
+        rec[cq] = b.cq;
     }
     __host__ __device__ static constexpr int R(int r, int c) { return 1 + c * (c + 3) / 2 + r; }
     __host__ __device__ static constexpr int Rinv(int c) { return 1 + c * (c + 3) / 2 + c + 1; }
@@ -459,7 +474,7 @@ __global__ __launch_bounds__(256) void Layer0Kernel(LayerArgs p) {
     bool flagged = false;
     SelectTopH<false, false, BEST>(
         Hb, lane,
-        [&](auto&& replay, auto) {
+        [&](auto&& replay, auto, auto) {
             for (int j = 0; j < nch; ++j) {
                 const int k = lane + kWave * j;
                 const bool act = k < K;
@@ -468,7 +483,7 @@ __global__ __launch_bounds__(256) void Layer0Kernel(LayerArgs p) {
                 const float gamma = act ? xCi[off0 + k] : 0.0f;
                 const float a1 = gamma / alpha;
                 const float e1 = nx2 - gamma * a1;
-                if (!replay(ok, e1, kWave * j)) return false;
+                if (!replay(ok, e1, kWave * j + lane)) return false;
             }
             return true;
         },
@@ -483,12 +498,14 @@ __global__ __launch_bounds__(256) void Layer0Kernel(LayerArgs p) {
     // Insertion-time write-back of the surviving slot contents (beam_search.cpp:253-258).
     uint8_t c0 = 0;
     float a0 = 0.0f, r00 = 0.0f;
+    prune::SlotBounds bd = prune::NoBounds();
     if (lane < Hb && s_cand >= 0) {
         const float alpha = p.gdiag[off0 + s_cand];
         const float gamma = xCi[off0 + s_cand];
         c0 = static_cast<uint8_t>(s_cand);
         a0 = gamma / alpha;
         r00 = sqrtf(alpha);
+        bd = prune::FirstBounds(r00, p.sw[off0 + s_cand], a0, p.isw[off0 + s_cand]);
     }
     if (lane < Hb) {
         float* rec = p.out.rec + (w * Hb + lane) * rc.stride;
@@ -498,6 +515,7 @@ __global__ __launch_bounds__(256) void Layer0Kernel(LayerArgs p) {
         rec[Rec::Rinv(0)] = 1.0f / r00;
         reinterpret_cast<uint32_t*>(rec + rc.code)[0] = c0;
         reinterpret_cast<uint32_t*>(rec)[rc.root] = 0u;
+        rc.PutBounds(rec, bd);
     }
     if (lane == 0) p.out.curH[w] = curH;
     if (p.is_last) {
@@ -521,8 +539,7 @@ __global__ __launch_bounds__(256) void Layer0Kernel(LayerArgs p) {
 //  * the other layers at the allocator's own choice.
 template <int L, bool LR, bool BEST>
 constexpr int LayerMinWaves() {
-    return L >= 11 ? (LR ? 5 : 4)
-                   : (LR ? 1 : ((L == 4 || L == 6 || (BEST && L == 3)) ? 8 : (L == 7 ? (BEST ? 6 : 7) : 1)));
+    return L >= 11 ? (LR ? 5 : 4) : 1;
 }
 
 // Layers up to kVStateMaxL read the slot state into VGPRs (see process() in LayerKernel): on the
@@ -530,11 +547,538 @@ constexpr int LayerMinWaves() {
 // extra VGPRs cost occupancy.
 constexpr int kVStateMaxL = 3;
 
+// Layers kQueueMinL..kQueueMaxL scan through a queue (LayerKernel, scan_queue): the survivors of the
+// pruning bound from every parent go into one FIFO and are evaluated 64 at a time, each lane with
+// its own parent's factor in VGPRs. Deeper layers evaluate each parent's survivors apart, with the
+// factor in SGPRs, whose VGPR cost would otherwise grow as L^2.
+constexpr int kQueueMinL = 3;
+constexpr int kQueueMaxL = 8;
+constexpr int kQueueCap = 128;  // ring capacity: at most 63 carried over plus one chunk of 64
+
 // BEST: the best-first pass (LayerArgs::flags). Its input records are rank-indexed, so slots are
 // scanned in ascending error order, and so are its output records. A vector flagged by an earlier
 // layer arrives with an empty beam.
 template <int L, bool LR, bool FULL, bool BEST>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LayerMinWaves<L, LR, BEST>(), 8))) void LayerKernel(
+    LayerArgs p) {
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    int64_t i, w;
+    if (!WaveItem(p, wave, i, w)) return;
+    const int m = p.m, Hb = p.Hb, K = FULL ? kMaxK : p.K, offL = p.offL;
+    const Rec rc(m);
+    const int ld = p.gram.ld;
+    const float* xCi = p.xC + i * p.ldx;
+    const int nch = FULL ? kMaxChunks : (K + kWave - 1) / kWave;
+    const float* __restrict__ recs_in = p.in.rec + w * Hb * rc.stride;
+    float* __restrict__ recs_out = p.out.rec + w * Hb * rc.stride;
+    const int vz = VZero();
+
+
+    // Per codeword of the layer: gamma = <x, c_k> and fl(alpha (1 - 2^-20)) for the pruning bound.
+    float gam[kMaxChunks], alc[kMaxChunks];
+#pragma unroll
+    for (int j = 0; j < kMaxChunks; ++j) {
+        const int k = lane + kWave * j;
+        const bool act = FULL || (j < nch && k < K);
+        gam[j] = act ? xCi[offL + k] : 0.0f;
+        alc[j] = (act ? p.gdiag[offL + k] : 0.0f) * prune::kAlphaScale;
+    }
+
+    const int curH = p.in.curH[w];
+
+    // Beam slot h's codes (and root) sit in lane h, read with one vector load per word for all
+    // slots at once, so a slot's G rows can be addressed without waiting for its record.
+    constexpr int kCodeWords = (L + 3) / 4;
+    uint32_t cw[kCodeWords];
+    uint32_t rootw = 0;
+    {
+        const uint32_t* rl = reinterpret_cast<const uint32_t*>(recs_in + (lane < curH ? lane : 0) * rc.stride);
+#pragma unroll
+        for (int w = 0; w < kCodeWords; ++w) cw[w] = rl[rc.code + w];
+        if (LR) rootw = rl[rc.root];
+    }
+    // Per wave: the layer's codewords that go to the exact evaluation, in scan order.
+    __shared__ int s_pack[kBeamWavesPerBlock][kMaxK];
+    int* __restrict__ pack = s_pack[wave];
+    const bool prune_on = p.prune != 0;
+
+    // Evaluates slot h's candidates and replays them into the top-H (scan order: slot, then code).
+    // Returns false when the replay asks for the slow pass.
+    //
+    // Pruning (prune_bound.hpp): once every slot of the top-H holds a candidate, a candidate whose
+    // bound shows e > worst is one the reference rejects; the others are listed in `pack` in
+    // ascending code order and evaluated exactly, 64 per group. While a slot is still empty the
+    // chunks are listed one at a time without a bound, so the worst can become finite after each.
+    auto process = [&](int h, auto&& replay, auto slow_tag, auto&& worst_now) -> bool {
+        constexpr bool kSlow = decltype(slow_tag)::value;
+        const float* rec = recs_in + h * rc.stride;
+        const float E_old = rec[0];
+        // Rows of the slot's prefix codewords from this layer's first column: G for the exact
+        // evaluation, Gs (rows scaled by sw) for the bound. The large root's prefix 0 reads
+        // G0S(root, .), scaled by sw0[root] in the bound.
+        const float* rowb[L];
+        const float* rows[L];
+        float ahat[L];  // a_t * isw_t
+        uint32_t root = 0;
+#pragma unroll
+        for (int t = 0; t < L; ++t) {
+            float isw_t;
+            if (LR && t == 0) {
+                root = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(rootw), h));
+                rowb[t] = p.gram.G0S + static_cast<int64_t>(root) * ld + offL;
+                rows[t] = rowb[t];
+                isw_t = p.isw0[root];
+            } else {
+                const uint32_t word = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(cw[t >> 2]), h));
+                const int f = p.gram.off[t] + static_cast<int>((word >> (8 * (t & 3))) & 0xFFu);
+                rowb[t] = p.gram.G + static_cast<int64_t>(f) * ld + offL;
+                rows[t] = p.Gs + static_cast<int64_t>(f) * ld + offL;
+                isw_t = p.isw[f];
+            }
+            ahat[t] = rec[rc.coef + t] * isw_t;
+        }
+        const float sw0 = LR ? p.sw0[root] : 1.0f;
+        const float kb = rec[rc.kb], cq = rec[rc.cq];
+
+        int next = 0;  // first chunk not yet listed
+        while (next < nch) {
+            float gp = 0.0f;
+            const float W = worst_now();
+            const bool bounded = !kSlow && prune_on && kb < kInfF && prune::ParentGap(E_old, W, gp);
+            const bool filling = !kSlow && prune_on && !(W < kInfF);
+            const int last = (bounded || !filling) ? nch : next + 1;
+            int total = 0;
+            // One chunk at a time (no unrolling): the bound stage then holds one chunk's L values.
+#pragma unroll 1
+            for (int j = next; j < last; ++j) {
+                const int k = lane + kWave * j;
+                const bool act = FULL || k < K;
+                bool keep = act;
+                if (bounded) {
+                    // eta~ = sum_t b_t ahat_t and b2 = sum_t b_t^2 by fma, b_t = Gs(f_t, k)
+                    float et = 0.0f, b2 = 0.0f;
+#pragma unroll
+                    for (int t = 0; t < L; ++t) {
+                        float bt = act ? rows[t][static_cast<uint32_t>(k)] : 0.0f;
+                        if (LR && t == 0) bt = bt * sw0;
+                        et = t == 0 ? bt * ahat[t] : __builtin_fmaf(bt, ahat[t], et);
+                        b2 = t == 0 ? bt * bt : __builtin_fmaf(bt, bt, b2);
+                    }
+                    const float alc = (act ? p.gdiag[offL + k] : 0.0f) * prune::kAlphaScale;
+                    const float gm = act ? xCi[offL + k] : 0.0f;
+                    keep = act && !prune::Prunable(alc, b2, gm - et, kb, cq, gp);
+                }
+                const uint64_t km = Ballot(keep);
+                if (keep) pack[total + __popcll(km & ((1ull << lane) - 1ull))] = k;
+                total += __popcll(km);
+            }
+            next = last;
+            if (total == 0) continue;
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            // The slot's R, 1/diag and coefficients (wave-uniform) for the exact evaluation. Up to
+            // kVStateMaxL they are read into VGPRs, so the solves' products have two VGPR
+            // sources; beyond it they stay in SGPRs, where they cost no occupancy.
+            const float* recv = kVStateMaxL >= L ? rec + vz : rec;
+            float aold[L];
+            float Rv[L][L];
+            float Ri[L];
+#pragma unroll
+            for (int t = 0; t < L; ++t) aold[t] = recv[rc.coef + t];
+            bool diag_ok = true;
+#pragma unroll
+            for (int r = 0; r < L; ++r) {
+#pragma unroll
+                for (int c = r; c < L; ++c) Rv[r][c] = recv[Rec::R(r, c)];
+                Ri[r] = recv[Rec::Rinv(r)];
+                diag_ok = diag_ok && DiagFastOk(Rv[r][r]);
+            }
+            const bool diag_fast = !LR && Ballot(!diag_ok) == 0ull;
+            auto Rf = [&](int r, int c) { return Rv[r][c]; };
+            for (int b = 0; b < total; b += kWave) {
+                const int idx = b + lane;
+                const bool act = idx < total;
+                const uint32_t k = static_cast<uint32_t>(act ? pack[idx] : 0);
+                float A[L];
+#pragma unroll
+                for (int t = 0; t < L; ++t) A[t] = rowb[t][k];
+                const float alpha = p.gdiag[offL + k];
+                const float gamma = xCi[offL + k];
+                float y[L], v[L], denom, a_last, e;
+                bool ok, safe = true;
+                if (LR) {
+                    EvalCand<L, 2>(Rf, Ri, A, aold, E_old, alpha, gamma, y, v, e, denom, a_last, ok, safe);
+                } else {
+                    // Markstein quotients where they are exact (every numerator in range), IEEE
+                    // division otherwise (the rare slow pass, a diagonal out of range, or a
+                    // numerator that left the range: the group is evaluated again).
+                    bool ieee = kSlow || !diag_fast;
+                    if (!ieee) {
+                        EvalCand<L, 1>(Rf, Ri, A, aold, E_old, alpha, gamma, y, v, e, denom, a_last, ok, safe);
+                        ieee = Ballot(!safe) != 0ull;
+                    }
+                    if (ieee) EvalCand<L, 0>(Rf, Ri, A, aold, E_old, alpha, gamma, y, v, e, denom, a_last, ok, safe);
+                }
+                if (!replay(ok && act, e, h * K + static_cast<int>(k))) return false;
+            }
+        }
+        return true;
+    };
+
+    // The queue scan (layers up to kQueueMaxL, fast pass with pruning): candidates are bound-
+    // tested chunk by chunk in scan order against the worst of that moment, the survivors
+    // (parent h, codeword k) are appended to a per-wave FIFO in scan order, and every full 64 of
+    // them (then the rest) are evaluated exactly and replayed. The worst only falls between a
+    // test and the evaluation, so a pruned candidate stays one the reference rejects.
+    __shared__ int s_queue[kBeamWavesPerBlock][kQueueCap];
+    int* __restrict__ queue = s_queue[wave];
+    auto scan_queue = [&](auto&& replay, auto&& worst_now) -> bool {
+        int qhead = 0, qlen = 0;
+        // Exact evaluation of the first n queued candidates, one per lane, each with its own
+        // parent's state.
+        auto flush = [&](int n) -> bool {
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            const bool act = lane < n;
+            const int ent = act ? queue[(qhead + lane) & (kQueueCap - 1)] : 0;
+            const int hl = ent >> 8;
+            const uint32_t k = static_cast<uint32_t>(ent & 0xFF);
+            const float* rl = recs_in + hl * rc.stride;
+            float Rv[L][L], Ri[L], aold[L], A[L];
+            bool diag_ok = true;
+#pragma unroll
+            for (int r = 0; r < L; ++r) {
+#pragma unroll
+                for (int c = r; c < L; ++c) Rv[r][c] = rl[Rec::R(r, c)];
+                Ri[r] = rl[Rec::Rinv(r)];
+                aold[r] = rl[rc.coef + r];
+                diag_ok = diag_ok && DiagFastOk(Rv[r][r]);
+            }
+            const float E_old = rl[0];
+            const uint32_t rootl =
+                LR ? static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(hl << 2, static_cast<int>(rootw))) : 0u;
+            // the parent's codes from its lane (lane h holds slot h's code words)
+            uint32_t cwl[kCodeWords];
+#pragma unroll
+            for (int q = 0; q < kCodeWords; ++q)
+                cwl[q] = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(hl << 2, static_cast<int>(cw[q])));
+#pragma unroll
+            for (int t = 0; t < L; ++t) {
+                const int code = static_cast<int>((cwl[t >> 2] >> (8 * (t & 3))) & 0xFFu);
+                const float* row = (LR && t == 0) ? p.gram.G0S + static_cast<int64_t>(rootl) * ld + offL
+                                                  : p.gram.G + static_cast<int64_t>(p.gram.off[t] + code) * ld + offL;
+                A[t] = row[k];
+            }
+            const float alpha = p.gdiag[offL + k];
+            const float gamma = xCi[offL + k];
+            auto Rf = [&](int r, int c) { return Rv[r][c]; };
+            float y[L], v[L], denom, a_last, e;
+            bool ok, safe = true;
+            if (LR) {
+                EvalCand<L, 2>(Rf, Ri, A, aold, E_old, alpha, gamma, y, v, e, denom, a_last, ok, safe);
+            } else {
+                bool ieee = Ballot(act && !diag_ok) != 0ull;
+                if (!ieee) {
+                    EvalCand<L, 1>(Rf, Ri, A, aold, E_old, alpha, gamma, y, v, e, denom, a_last, ok, safe);
+                    ieee = Ballot(act && !safe) != 0ull;
+                }
+                if (ieee) EvalCand<L, 0>(Rf, Ri, A, aold, E_old, alpha, gamma, y, v, e, denom, a_last, ok, safe);
+            }
+            qhead = (qhead + n) & (kQueueCap - 1);
+            qlen -= n;
+            return replay(ok && act, e, hl * K + static_cast<int>(k));
+        };
+        for (int h = 0; h < curH; ++h) {
+            const float* rec = recs_in + h * rc.stride;
+            const float E_old = rec[0];
+            const float kb = rec[rc.kb], cq = rec[rc.cq];
+            // Gs rows of the slot's prefix codewords (the large root's prefix 0: G0S(root, .),
+            // scaled by sw0[root]) and ahat_t = a_t * isw_t.
+            const float* rows[L];
+            float ahat[L];
+            float sw0 = 1.0f;
+#pragma unroll
+            for (int t = 0; t < L; ++t) {
+                float isw_t;
+                if (LR && t == 0) {
+                    const uint32_t root = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(rootw), h));
+                    rows[t] = p.gram.G0S + static_cast<int64_t>(root) * ld + offL;
+                    isw_t = p.isw0[root];
+                    sw0 = p.sw0[root];
+                } else {
+                    const uint32_t word =
+                        static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(cw[t >> 2]), h));
+                    const int f = p.gram.off[t] + static_cast<int>((word >> (8 * (t & 3))) & 0xFFu);
+                    rows[t] = p.Gs + static_cast<int64_t>(f) * ld + offL;
+                    isw_t = p.isw[f];
+                }
+                ahat[t] = rec[rc.coef + t] * isw_t;
+            }
+            // Whether chunk j's candidate survives the bound (true when it may enter the top-H).
+            auto keep_of = [&](int j, float gp) -> bool {
+                const uint32_t k = static_cast<uint32_t>(lane + kWave * j);
+                const bool act = FULL || static_cast<int>(k) < K;
+                float et = 0.0f, b2 = 0.0f;
+#pragma unroll
+                for (int t = 0; t < L; ++t) {
+                    float bt = act ? rows[t][k] : 0.0f;
+                    if (LR && t == 0) bt = bt * sw0;
+                    et = t == 0 ? bt * ahat[t] : __builtin_fmaf(bt, ahat[t], et);
+                    b2 = t == 0 ? bt * bt : __builtin_fmaf(bt, bt, b2);
+                }
+                return act && !prune::Prunable(alc[j], b2, gam[j] - et, kb, cq, gp);
+            };
+            auto enqueue = [&](int j, bool keep) -> bool {
+                const uint64_t km = Ballot(keep);
+                if (keep) {
+                    const int pos = (qhead + qlen + __popcll(km & ((1ull << lane) - 1ull))) & (kQueueCap - 1);
+                    queue[pos] = (h << 8) | (lane + kWave * j);
+                }
+                qlen += __popcll(km);
+                return qlen < kWave || flush(kWave);
+            };
+            float gp = 0.0f;
+            const float W0 = worst_now();
+            if (!(W0 < kInfF)) {
+                // A slot is still empty: chunk by chunk, each tested against the worst after the
+                // previous one was evaluated.
+                for (int j = 0; j < nch; ++j) {
+                    const bool act = FULL || lane + kWave * j < K;
+                    const bool bounded = kb < kInfF && prune::ParentGap(E_old, worst_now(), gp);
+                    bool keep = act;
+#pragma unroll
+                    for (int jj = 0; jj < kMaxChunks; ++jj)
+                        if (jj == j && bounded) keep = keep_of(jj, gp);
+                    if (!enqueue(j, keep)) return false;
+                }
+            } else {
+                // The whole slot against the worst at its start (it only falls from there).
+                const bool bounded = kb < kInfF && prune::ParentGap(E_old, W0, gp);
+                bool keep[kMaxChunks];
+#pragma unroll
+                for (int j = 0; j < kMaxChunks; ++j) {
+                    if (!FULL && j >= nch) continue;
+                    keep[j] = bounded ? keep_of(j, gp) : (FULL || lane + kWave * j < K);
+                }
+#pragma unroll
+                for (int j = 0; j < kMaxChunks; ++j) {
+                    if (!FULL && j >= nch) continue;
+                    if (!enqueue(j, keep[j])) return false;
+                }
+            }
+        }
+        if (qlen > 0 && !flush(qlen)) return false;
+        return true;
+    };
+
+    float s_err;
+    int s_cand;
+    bool flagged = false;
+    SelectTopH<true, BEST, BEST>(  // errors clamped at zero (EvalCand)
+        Hb, lane,
+        [&](auto&& replay, auto slow_tag, auto&& worst_now) {
+            if constexpr (L <= kQueueMaxL && !decltype(slow_tag)::value) {
+                if (prune_on) return scan_queue(replay, worst_now);
+            }
+            for (int h = 0; h < curH; ++h) {
+                if (!process(h, replay, slow_tag, worst_now)) return false;
+            }
+            return true;
+        },
+        s_err, s_cand, flagged);
+    if (BEST && flagged) {
+        // No records: the next layers see an empty beam (curH = 0), do no work for this vector
+        // and keep it well-formed until its re-run.
+        if (lane == 0) {
+            p.flags[i] = 1;
+            p.out.curH[w] = 0;
+        }
+        return;
+    }
+
+    // Deferred write-back (beam_search.cpp:337-383; the large root :896-947) or the all-skipped
+    // fallback (:385-400, :949-966). A slot holding a candidate is built even when its error is
+    // NaN (Materialize skips only errors >= +inf); the beam's new size counts the finite errors
+    // (CountFinite), and with none the parent slots are copied instead. The last layer needs no
+    // records, only the final pick.
+    const bool live = lane < Hb && !(s_err >= kInfF);
+    const int newH = __popcll(Ballot(lane < Hb && s_err < kInfF));
+    const int outH = newH == 0 ? max(1, min(curH, Hb)) : newH;  // CountFinite and max(1, .)
+    if (lane == 0) p.out.curH[w] = outH;
+    float out_err = kInfF;
+    int src = -1, knew = 0;
+    if (newH == 0) {
+        if (lane < min(curH, Hb)) {
+            src = lane;
+            out_err = recs_in[lane * rc.stride];
+        }
+    } else if (live) {
+        src = s_cand / K;
+        knew = s_cand - src * K;
+        out_err = s_err;
+    }
+    if (!p.is_last) {
+        float* ro = recs_out + lane * rc.stride;
+        const float* ri = recs_in + (src < 0 ? 0 : src) * rc.stride;
+        auto put_codes = [&](bool from_parent, int kc, uint32_t root) {
+            uint32_t* cwo = reinterpret_cast<uint32_t*>(ro + rc.code);
+#pragma unroll
+            for (int qq = 0; qq <= L / 4; ++qq) {
+                uint32_t word = 0;
+#pragma unroll
+                for (int b = 0; b < 4; ++b) {
+                    const int t = 4 * qq + b;
+                    const uint32_t c = t < L ? (from_parent ? static_cast<uint32_t>(CodeAt(ri, rc.code, t)) : 0u)
+                                             : (t == L ? static_cast<uint32_t>(kc) : 0u);
+                    word |= c << (8 * b);
+                }
+                cwo[qq] = word;
+            }
+            reinterpret_cast<uint32_t*>(ro)[rc.root] = root;
+        };
+        if (newH == 0) {
+            const int nh = min(curH, Hb);
+            if (lane < nh) {
+                // parent slot `lane` with a zero new column
+                ro[0] = ri[0];
+#pragma unroll
+                for (int t = 0; t < L; ++t) ro[rc.coef + t] = ri[rc.coef + t];
+                ro[rc.coef + L] = 0.0f;
+#pragma unroll
+                for (int r = 0; r < L; ++r) {
+#pragma unroll
+                    for (int c = r; c < L; ++c) ro[Rec::R(r, c)] = ri[Rec::R(r, c)];
+                    ro[Rec::R(r, L)] = 0.0f;
+                    ro[Rec::Rinv(r)] = ri[Rec::Rinv(r)];
+                }
+                ro[Rec::R(L, L)] = 0.0f;
+                ro[Rec::Rinv(L)] = 1.0f / 0.0f;
+                put_codes(true, 0, reinterpret_cast<const uint32_t*>(ri)[rc.root]);
+                rc.PutBounds(ro, prune::NoBounds());
+            } else if (nh == 0 && lane == 0) {
+                // No beam at all (layer 0 had no finite candidate): the reference's next-buffer
+                // slot 0 keeps its never-written (zero) state with error +inf.
+                ro[0] = kInfF;
+#pragma unroll
+                for (int t = 0; t <= L; ++t) ro[rc.coef + t] = 0.0f;
+#pragma unroll
+                for (int r = 0; r <= L; ++r) {
+#pragma unroll
+                    for (int c = r; c <= L; ++c) ro[Rec::R(r, c)] = 0.0f;
+                    ro[Rec::Rinv(r)] = 1.0f / 0.0f;
+                }
+                put_codes(false, 0, 0u);
+                rc.PutBounds(ro, prune::NoBounds());
+            }
+        } else if (live) {
+            // The chosen candidate once more with the reference's arithmetic (IEEE division, or the
+            // large root's reciprocal multiply): its new coefficients, Cholesky column and bounds.
+            const uint32_t root = reinterpret_cast<const uint32_t*>(ri)[rc.root];
+            float Rv[L][L], Ri[L], aold[L], A[L];
+            int fl[L];  // flat index of each prefix codeword (the root for a large root's prefix 0)
+#pragma unroll
+            for (int t = 0; t < L; ++t) {
+#pragma unroll
+                for (int c = t; c < L; ++c) Rv[t][c] = ri[Rec::R(t, c)];
+                Ri[t] = ri[Rec::Rinv(t)];
+                aold[t] = ri[rc.coef + t];
+                fl[t] = (LR && t == 0) ? static_cast<int>(root) : p.gram.off[t] + CodeAt(ri, rc.code, t);
+                const float* row = (LR && t == 0) ? p.gram.G0S + static_cast<int64_t>(root) * ld + offL
+                                                  : p.gram.G + static_cast<int64_t>(fl[t]) * ld + offL;
+                A[t] = row[knew];
+            }
+            auto Rf = [&](int r, int c) { return Rv[r][c]; };
+            float y[L], v[L], e, denom, a_last;
+            bool ok, unused = true;
+            if (LR) {
+                EvalCand<L, 2>(Rf, Ri, A, aold, ri[0], p.gdiag[offL + knew], xCi[offL + knew], y, v, e, denom, a_last,
+                               ok, unused);
+            } else {
+                EvalCand<L, 0>(Rf, Ri, A, aold, ri[0], p.gdiag[offL + knew], xCi[offL + knew], y, v, e, denom, a_last,
+                               ok, unused);
+            }
+            ro[0] = s_err;
+            double asq = 0.0;  // ||ahat||^2 of the new coefficients
+#pragma unroll
+            for (int t = 0; t <= L; ++t) {
+                const float at = t < L ? aold[t] - v[t] * a_last : a_last;
+                ro[rc.coef + t] = at;
+                const float iswt = t < L ? ((LR && t == 0) ? p.isw0[fl[t]] : p.isw[fl[t]]) : p.isw[offL + knew];
+                const double ah = static_cast<double>(at) * static_cast<double>(iswt);
+                asq += ah * ah;
+            }
+#pragma unroll
+            for (int r = 0; r < L; ++r) {
+#pragma unroll
+                for (int c = r; c < L; ++c) ro[Rec::R(r, c)] = Rv[r][c];
+                ro[Rec::R(r, L)] = y[r];
+                ro[Rec::Rinv(r)] = Ri[r];
+            }
+            const float rLL = sqrtf(denom);
+            ro[Rec::R(L, L)] = rLL;
+            ro[Rec::Rinv(L)] = 1.0f / rLL;
+            put_codes(true, knew, root);
+            auto swf = [&](int t) { return (LR && t == 0) ? p.sw0[fl[t]] : p.sw[fl[t]]; };
+            rc.PutBounds(ro, prune::NextBounds<L>(y, v, rLL, swf, p.sw[offL + knew], ri[rc.kap], ri[rc.phi], asq));
+        } else if (lane < Hb) {
+            ro[0] = kInfF;  // an empty slot: never read by the next layer
+        }
+        return;
+    }
+
+    // Last layer: the final pick (beam_search.cpp:409-419) over the slots the write-back would
+    // build; with no finite candidate (the fallback) those are the parent slots with code 0.
+    if (BEST && FinalTie(out_err, outH)) {
+        if (lane == 0) p.flags[i] = 1;
+        return;
+    }
+    const int best = BestSlot(out_err, outH, lane);
+    if (lane == best) {
+        // src < 0: no beam at all (the reference's never-written slot 0: codes 0, error +inf)
+        const float* ri = recs_in + (src < 0 ? 0 : src) * rc.stride;
+        const uint32_t root = src < 0 ? 0u : reinterpret_cast<const uint32_t*>(ri)[rc.root];
+        if (LR) {
+            p.cluster_out[i] = root;
+#pragma unroll
+            for (int t = 1; t < L; ++t) p.codes_out[i * (m - 1) + (t - 1)] = src < 0 ? 0 : CodeAt(ri, rc.code, t);
+            p.codes_out[i * (m - 1) + (L - 1)] = static_cast<uint8_t>(knew);
+        } else {
+#pragma unroll
+            for (int t = 0; t < L; ++t) p.codes_out[i * m + t] = src < 0 ? 0 : CodeAt(ri, rc.code, t);
+            p.codes_out[i * m + L] = static_cast<uint8_t>(knew);
+        }
+        if (p.best_err) p.best_err[i] = out_err;
+    }
+}
+
+// Layers outside kQueueMinL..kQueueMaxL (the shallow layers, where a candidate's solve is little
+// more than its bound, and the deep layers of the M=16 and large-root encodes): every candidate of
+// every slot is evaluated exactly, four chunks of 64 at a time with the slot's factor in SGPRs, and
+// the slots are written back by the lanes that hold them, with their pruning constants while a
+// later layer runs the queue scan. LR selects the large-root cross-term source and
+// reciprocal solves.
+// FULL: the layer has exactly 256 codewords (no partial chunk).
+// Minimum waves per SIMD requested from the register allocator, per layer (measured):
+//  * layers >= 11 at 4 waves (<= 128 VGPRs), 5 for the large root: left alone the allocator
+//    gives them 2-3 waves, or 1 at layer 16 (> 256 VGPRs); the M=16, beam-8 encode ran 9% faster
+//    and the large-root 16-layer beam-32 encode 18% faster (5 waves there: another 1%);
+//  * on the M=8, K=256, beam-16 encode layers 4 and 6 run best at 8 waves and layer 7 at 7 (6 in
+//    the best-first pass, where 80 VGPRs remove its spills), and layer 3 of the best-first pass
+//    at 8 (left alone it takes 65 VGPRs, one over);
+//  * the other layers at the allocator's own choice.
+template <int L, bool LR, bool BEST>
+constexpr int DeepMinWaves() {
+    return L >= 11 ? (LR ? 5 : 4)
+                   : (LR ? 1 : ((L == 4 || L == 6 || (BEST && L == 3)) ? 8 : (L == 7 ? (BEST ? 6 : 7) : 1)));
+}
+
+
+// BEST: the best-first pass (LayerArgs::flags). Its input records are rank-indexed, so slots are
+// scanned in ascending error order, and so are its output records. A vector flagged by an earlier
+// layer arrives with an empty beam.
+template <int L, bool LR, bool FULL, bool BEST>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DeepMinWaves<L, LR, BEST>(), 8))) void LayerKernelDeep(
     LayerArgs p) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
@@ -656,7 +1200,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LayerMinWav
 #pragma unroll
         for (int j = 0; j < kMaxChunks; ++j) {
             if (FULL || j < nch) {
-                if (!replay(okc[j], ech[j], h * K + kWave * j)) return false;
+                if (!replay(okc[j], ech[j], h * K + kWave * j + lane)) return false;
             }
         }
         return true;
@@ -667,7 +1211,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LayerMinWav
     bool flagged = false;
     SelectTopH<true, BEST, BEST>(  // errors clamped at zero (EvalCand)
         Hb, lane,
-        [&](auto&& replay, auto slow_tag) {
+        [&](auto&& replay, auto slow_tag, auto) {
             for (int h = 0; h < curH; ++h) {
                 float A[kMaxChunks][L];
                 load_rows(h, A);
@@ -690,6 +1234,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LayerMinWav
     const int newH = __popcll(__ballot(lane < Hb && s_err < kInfF));
     int outH;
     float out_err = kInfF;
+    // pruning constants of the new slots, while a later layer runs the queue scan
+    constexpr bool kNextQueued = L + 1 <= kQueueMaxL;
+    prune::SlotBounds out_bd = prune::NoBounds();
     uint8_t ncode[L + 1];
     uint32_t nroot = 0;
 #pragma unroll
@@ -769,9 +1316,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LayerMinWav
                                unused);
             }
             out_err = s_err;
+            double asq = 0.0;  // ||ahat||^2 of the new coefficients (pruning constants)
 #pragma unroll
-            for (int t = 0; t < L; ++t) ro[rc.coef + t] = aold[t] - v[t] * a_last;
-            ro[rc.coef + L] = a_last;
+            for (int t = 0; t <= L; ++t) {
+                const float at = t < L ? aold[t] - v[t] * a_last : a_last;
+                ro[rc.coef + t] = at;
+                if (kNextQueued) {
+                    const int ft = t < L ? ((LR && t == 0) ? static_cast<int>(nroot) : p.gram.off[t] + ncode[t])
+                                         : offL + k;
+                    const float iswt = (LR && t == 0) ? p.isw0[ft] : p.isw[ft];
+                    const double ah = static_cast<double>(at) * static_cast<double>(iswt);
+                    asq += ah * ah;
+                }
+            }
 #pragma unroll
             for (int r = 0; r < L; ++r) {
 #pragma unroll
@@ -782,11 +1339,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LayerMinWav
             const float rLL = sqrtf(denom);
             ro[Rec::R(L, L)] = rLL;
             ro[Rec::Rinv(L)] = 1.0f / rLL;
+            if (kNextQueued) {
+                auto swf = [&](int t) {
+                    return (LR && t == 0) ? p.sw0[nroot] : p.sw[p.gram.off[t] + ncode[t]];
+                };
+                out_bd = prune::NextBounds<L>(y, v, rLL, swf, p.sw[offL + k], ri[rc.kap], ri[rc.phi], asq);
+            }
         }
     }
     if (lane < Hb) {
         float* ro = recs_out + lane * rc.stride;
         ro[0] = out_err;
+        rc.PutBounds(ro, out_bd);
         uint32_t* cw = reinterpret_cast<uint32_t*>(ro + rc.code);
 #pragma unroll
         for (int q = 0; q <= L / 4; ++q) {
@@ -855,7 +1419,7 @@ __global__ __launch_bounds__(256) void RootSeedKernel(RootArgs p) {
         bool unused_flag = false;
         SelectTopH<false, false, false>(
             rs, lane,
-            [&](auto&& replay, auto) {
+            [&](auto&& replay, auto, auto) {
                 for (int c0 = 0; c0 < p.h0; c0 += kWave) {
                     const int code = c0 + lane;
                     const bool act = code < p.h0;
@@ -864,7 +1428,7 @@ __global__ __launch_bounds__(256) void RootSeedKernel(RootArgs p) {
                     const float gamma = act ? sc[code] : 0.0f;
                     const float a1 = gamma / alpha;
                     const float e1 = nx2 - gamma * a1;
-                    if (!replay(ok, e1, c0)) return false;
+                    if (!replay(ok, e1, c0 + lane)) return false;
                 }
                 return true;
             },
@@ -873,6 +1437,7 @@ __global__ __launch_bounds__(256) void RootSeedKernel(RootArgs p) {
     const bool seeded = lane < rs && !(s_err >= kInfF);
     const int curH = max(1, __popcll(__ballot(seeded)));
     float a0 = 0.0f, r00 = 0.0f;
+    prune::SlotBounds bd = prune::NoBounds();
     uint32_t root = 0;
     if (seeded) {
         root = static_cast<uint32_t>(s_cand);
@@ -880,6 +1445,7 @@ __global__ __launch_bounds__(256) void RootSeedKernel(RootArgs p) {
         const float gamma = p.forced ? p.scores[i * p.ldx] : p.scores[i * p.ldx + s_cand];
         a0 = gamma / alpha;
         r00 = sqrtf(alpha);
+        bd = prune::FirstBounds(r00, p.sw0[s_cand], a0, p.isw0[s_cand]);
     }
     if (lane < Hb) {
         float* rec = p.out.rec + (i * Hb + lane) * rc.stride;
@@ -889,6 +1455,7 @@ __global__ __launch_bounds__(256) void RootSeedKernel(RootArgs p) {
         rec[Rec::Rinv(0)] = 1.0f / r00;
         reinterpret_cast<uint32_t*>(rec + rc.code)[0] = 0u;
         reinterpret_cast<uint32_t*>(rec)[rc.root] = root;
+        rc.PutBounds(rec, bd);
     }
     if (lane == 0) p.out.curH[i] = curH;
     if (p.is_last) {  // m == 1: the root is the whole code
@@ -941,7 +1508,7 @@ __global__ __launch_bounds__(256) void NearestRootFixupKernel(const float* __res
         bool unused_flag = false;
         SelectTopH<false, false, false>(
             1, lane,
-            [&](auto&& replay, auto) {
+            [&](auto&& replay, auto, auto) {
                 for (int c0 = 0; c0 < h0; c0 += kWave) {
                     const int code = c0 + lane;
                     const bool act = code < h0;
@@ -954,7 +1521,7 @@ __global__ __launch_bounds__(256) void NearestRootFixupKernel(const float* __res
                     }
                     const float a1 = gamma / alpha;
                     const float e1 = xn - gamma * a1;
-                    if (!replay(ok, e1, c0)) return false;
+                    if (!replay(ok, e1, c0 + lane)) return false;
                 }
                 return true;
             },
@@ -964,23 +1531,38 @@ __global__ __launch_bounds__(256) void NearestRootFixupKernel(const float* __res
     }
 }
 
-template <int L>
-hipError_t LaunchL(bool lr, const LayerArgs& a, hipStream_t s) {
+template <int L, template <int, bool, bool, bool> class KernelSel>
+hipError_t LaunchWith(bool lr, const LayerArgs& a, hipStream_t s) {
     const unsigned blocks = static_cast<unsigned>((a.n + kBeamWavesPerBlock - 1) / kBeamWavesPerBlock);
     const dim3 block(kWave * kBeamWavesPerBlock);
     const bool full = a.K == kMaxK;
     if (lr) {  // the large-root beam always runs in the reference order
         if (a.flags) return hipErrorInvalidValue;
-        if (full) hipLaunchKernelGGL((LayerKernel<L, true, true, false>), dim3(blocks), block, 0, s, a);
-        else hipLaunchKernelGGL((LayerKernel<L, true, false, false>), dim3(blocks), block, 0, s, a);
+        if (full) hipLaunchKernelGGL((KernelSel<L, true, true, false>::kernel), dim3(blocks), block, 0, s, a);
+        else hipLaunchKernelGGL((KernelSel<L, true, false, false>::kernel), dim3(blocks), block, 0, s, a);
     } else if (a.flags) {
-        if (full) hipLaunchKernelGGL((LayerKernel<L, false, true, true>), dim3(blocks), block, 0, s, a);
-        else hipLaunchKernelGGL((LayerKernel<L, false, false, true>), dim3(blocks), block, 0, s, a);
+        if (full) hipLaunchKernelGGL((KernelSel<L, false, true, true>::kernel), dim3(blocks), block, 0, s, a);
+        else hipLaunchKernelGGL((KernelSel<L, false, false, true>::kernel), dim3(blocks), block, 0, s, a);
     } else {
-        if (full) hipLaunchKernelGGL((LayerKernel<L, false, true, false>), dim3(blocks), block, 0, s, a);
-        else hipLaunchKernelGGL((LayerKernel<L, false, false, false>), dim3(blocks), block, 0, s, a);
+        if (full) hipLaunchKernelGGL((KernelSel<L, false, true, false>::kernel), dim3(blocks), block, 0, s, a);
+        else hipLaunchKernelGGL((KernelSel<L, false, false, false>::kernel), dim3(blocks), block, 0, s, a);
     }
     return hipGetLastError();
+}
+
+template <int L, bool LR, bool FULL, bool BEST>
+struct QueueSel {
+    static constexpr auto kernel = LayerKernel<L, LR, FULL, BEST>;
+};
+template <int L, bool LR, bool FULL, bool BEST>
+struct DeepSel {
+    static constexpr auto kernel = LayerKernelDeep<L, LR, FULL, BEST>;
+};
+
+template <int L>
+hipError_t LaunchL(bool lr, const LayerArgs& a, hipStream_t s) {
+    if constexpr (L >= kQueueMinL && L <= kQueueMaxL) return LaunchWith<L, QueueSel>(lr, a, s);
+    else return LaunchWith<L, DeepSel>(lr, a, s);
 }
 
 }  // namespace

@@ -130,6 +130,34 @@ __global__ void DiagKernel(const float* __restrict__ G, int H, float* __restrict
     if (f < H) diag[f] = G[static_cast<int64_t>(f) * H + f];
 }
 
+__global__ void PruneScaleKernel(const float* __restrict__ g, int64_t n, float* __restrict__ sw,
+                                 float* __restrict__ isw) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float r = sqrtf(g[i]);
+    isw[i] = r;
+    sw[i] = 1.0f / r;
+}
+
+__global__ void RowScaleKernel(const float* __restrict__ G, int64_t rows, int cols, const float* __restrict__ sw,
+                               float* __restrict__ Gs) {
+    const int64_t r = blockIdx.y + static_cast<int64_t>(gridDim.y) * blockIdx.z;
+    const int c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (r >= rows || c >= cols) return;
+    Gs[r * cols + c] = G[r * cols + c] * sw[r];
+}
+
+// Largest |x| as float bits (NaN payloads sort above +inf): per-thread max over a grid stride,
+// wave max by shuffles, one atomic per wave.
+__global__ __launch_bounds__(256) void AbsMaxBitsKernel(const float* __restrict__ x, int64_t n, unsigned* out) {
+    unsigned m = 0;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x)
+        m = max(m, __float_as_uint(x[i]) & 0x7FFFFFFFu);
+    for (int o = 32; o > 0; o >>= 1) m = max(m, static_cast<unsigned>(__shfl_xor(static_cast<int>(m), o)));
+    if ((threadIdx.x & 63) == 0) atomicMax(out, m);
+}
+
 __global__ void TransposeKernel(const float* __restrict__ in, int rows, int cols,
                                 float* __restrict__ out) {
     __shared__ float t[32][33];
@@ -254,6 +282,28 @@ hipError_t LaunchNorms(const float* C, int d, int H, bool lane4, float* norm2, f
 hipError_t LaunchDiag(const float* G_rm, int H, float* diag, hipStream_t s) {
     if (H <= 0) return hipSuccess;
     hipLaunchKernelGGL(DiagKernel, dim3((H + 255) / 256), dim3(256), 0, s, G_rm, H, diag);
+    return hipGetLastError();
+}
+
+hipError_t LaunchPruneScale(const float* g, int64_t n, float* sw, float* isw, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(PruneScaleKernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s, g, n, sw, isw);
+    return hipGetLastError();
+}
+
+hipError_t LaunchRowScale(const float* G, int64_t rows, int cols, const float* sw, float* Gs, hipStream_t s) {
+    if (rows <= 0 || cols <= 0) return hipSuccess;
+    const int64_t ry = std::min<int64_t>(rows, 32768);
+    const dim3 grid(static_cast<unsigned>((cols + 255) / 256), static_cast<unsigned>(ry),
+                    static_cast<unsigned>((rows + ry - 1) / ry));
+    hipLaunchKernelGGL(RowScaleKernel, grid, dim3(256), 0, s, G, rows, cols, sw, Gs);
+    return hipGetLastError();
+}
+
+hipError_t LaunchAbsMaxBits(const float* x, int64_t n, unsigned* out, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    const int64_t blocks = std::min<int64_t>((n + 255) / 256, 2048);
+    hipLaunchKernelGGL(AbsMaxBitsKernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, x, n, out);
     return hipGetLastError();
 }
 

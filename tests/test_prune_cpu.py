@@ -1,0 +1,82 @@
+"""The beam's candidate pruning (stlq_amd/csrc/prune_bound.hpp) rejects only candidates the
+reference rejects (src/quantizer/beam_search.cpp:320): tests/prune_check.cpp replays the reference
+beam in its slot order with the device's pruning constants and test (the product header, built
+with hipcc as host code) on samples of the benchmark workloads and on ill-conditioned codebooks,
+and requires
+  * no pruned candidate the reference would have inserted,
+  * every candidate kept when the threshold is its own error (a strict lower bound),
+  * the beam that skips the pruned candidates equal to the full beam, codes and errors bit for bit,
+  * on the benchmark samples, most candidates pruned (the bound is tight enough to matter)."""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+from stlq_amd import workloads
+from tests.helpers import rvq_problem
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+
+
+@pytest.fixture(scope="module")
+def checker(tmp_path_factory):
+    out = str(tmp_path_factory.mktemp("prune") / "libprune_check.so")
+    cmd = ["/opt/rocm/bin/hipcc", "-O2", "-std=c++17", "-fPIC", "-shared", "-ffp-contract=off",
+           f"-I{os.path.join(ROOT, 'stlq_amd', 'csrc')}", os.path.join(HERE, "prune_check.cpp"), "-o", out]
+    subprocess.run(cmd, check=True, capture_output=True, text=True)
+    lib = ctypes.CDLL(out)
+    f32p = ctypes.POINTER(ctypes.c_float)
+    lib.prune_check.argtypes = [f32p, f32p, f32p, ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_int),
+                                ctypes.c_int64, ctypes.c_int, ctypes.POINTER(ctypes.c_int64)]
+    return lib
+
+
+def _run(checker, orc, X, C, h, Hb):
+    G, _ = orc.build_precomp(C, h)
+    xC = np.ascontiguousarray(orc.gemm_xc(C, X))
+    nx2 = np.ascontiguousarray(orc.xnorm2(X))
+    hv = (ctypes.c_int * len(h))(*h)
+    st = (ctypes.c_int64 * 6)()
+    f32p = ctypes.POINTER(ctypes.c_float)
+    G = np.ascontiguousarray(G)
+    assert checker.prune_check(G.ctypes.data_as(f32p), xC.ctypes.data_as(f32p), nx2.ctypes.data_as(f32p),
+                               int(sum(h)), len(h), hv, X.shape[0], Hb, st) == 0
+    keys = ["candidates", "tested", "pruned", "violations", "self_kept_fail", "mismatches"]
+    return dict(zip(keys, list(st)))
+
+
+@pytest.mark.parametrize("cfg,n,Hb", [("C2", 400, 16), ("C4", 60, 8), ("C3", 300, 16)])
+def test_pruning_never_drops_an_entrant(checker, orc, cfg, n, Hb):
+    w = workloads.CONFIGS[cfg]
+    mix = workloads.Mixture(w.kind, w.d, w.n_comp, w.seed)
+    Xtr = mix.sample(10_000_000, 3000 if w.d < 900 else 1500)
+    C = workloads.residual_codebooks(Xtr, w.m, w.K, 3, w.seed + 5, spherical=(w.kind == "sphere"))
+    X = mix.sample(0, n)
+    rep = _run(checker, orc, X, C, [w.K] * w.m, Hb)
+    print(cfg, rep)
+    assert rep["violations"] == 0 and rep["self_kept_fail"] == 0 and rep["mismatches"] == 0, rep
+    assert rep["pruned"] >= 0.4 * rep["candidates"], rep  # tight enough to matter (reference scan order)
+
+
+@pytest.mark.parametrize("kind", ["near_dependent", "scaled", "tiny"])
+def test_pruning_safe_on_ill_conditioned_codebooks(checker, orc, kind):
+    """Codebooks whose prefixes are nearly linearly dependent (Cholesky pivots near zero), span
+    many orders of magnitude, or are tiny: the constants grow or leave their ranges, pruning backs
+    off, and nothing the reference inserts is ever skipped."""
+    rng = np.random.default_rng(7)
+    X, C = rvq_problem(77, 200, 16, 5, 32, train_n=1500, iters=3)
+    if kind == "near_dependent":
+        C[32:64] = C[0:32] * 1.0001 + 1e-4 * rng.standard_normal((32, 16)).astype(np.float32)
+        C[96:128] = C[64:96] + 1e-3 * rng.standard_normal((32, 16)).astype(np.float32)
+    elif kind == "scaled":
+        C[32:64] *= 1e4
+        C[64:96] *= 1e-4
+    else:
+        C *= 1e-12
+        X *= 1e-12
+    rep = _run(checker, orc, X, C, [32] * 5, 8)
+    print(kind, rep)
+    assert rep["violations"] == 0 and rep["self_kept_fail"] == 0 and rep["mismatches"] == 0, rep
