@@ -194,6 +194,11 @@ typedef struct stlq_mi355_stream_params {
     int large_root;
     int root_mode;
     const float* R;
+    /* Global id of the first streamed vector (EncodeBaseStreaming's start_id,
+     * encode_base_streaming.cpp:1913-1936): the stream covers ids start_id .. start_id + n_total - 1,
+     * fill and sink receive global ids, and the ILS perturbations are keyed by them
+     * (sample_id_offset = res.start + t0, :874). A resumed stream reproduces the whole one. */
+    uint64_t start_id;
 } stlq_mi355_stream_params;
 
 typedef struct stlq_mi355_chunk_out {
@@ -205,6 +210,7 @@ typedef struct stlq_mi355_chunk_out {
     const float* best_err;      /* large root: count */
 } stlq_mi355_chunk_out;
 
+/* first: the global id (start_id + offset in the stream) of the chunk's first vector. */
 typedef int (*stlq_mi355_fill_fn)(void* user, int64_t first, int64_t count, void* dst);
 typedef int (*stlq_mi355_sink_fn)(void* user, int64_t first, int64_t count,
                                   const stlq_mi355_chunk_out* out);

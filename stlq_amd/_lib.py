@@ -59,6 +59,7 @@ class StreamParams(ctypes.Structure):
         ("large_root", ctypes.c_int),
         ("root_mode", ctypes.c_int),
         ("R", ctypes.POINTER(ctypes.c_float)),
+        ("start_id", ctypes.c_uint64),
     ]
 
 

@@ -6,6 +6,7 @@
 #include "prune_bound.hpp"
 
 #include <algorithm>
+#include <climits>
 #include <chrono>
 #include <cstdlib>
 #include <cstring>
@@ -1337,6 +1338,9 @@ int stlq_mi355_encode_stream(stlq_mi355_ctx* c, int64_t n_total, int64_t chunk, 
         RC_TRY(CheckParams(&sp->encode));
     }
     if (n_total < 0 || chunk <= 0 || !fill || !sink) return Fail(STLQ_MI355_ERR_INVALID, "bad arguments");
+    const uint64_t gid0 = sp->start_id;  // global id of the stream's first vector
+    if (gid0 > static_cast<uint64_t>(INT64_MAX) - static_cast<uint64_t>(n_total))
+        return Fail(STLQ_MI355_ERR_INVALID, "start_id + n_total overflows");
     if (stats) std::memset(stats, 0, sizeof(*stats));
     if (n_total == 0) return STLQ_MI355_OK;
     c->ResetTimings();
@@ -1424,7 +1428,7 @@ int stlq_mi355_encode_stream(stlq_mi355_ctx* c, int64_t n_total, int64_t chunk, 
             out.cost = want ? sl.hcost : nullptr;
         }
         const auto s0 = std::chrono::steady_clock::now();
-        const int src = sink(user, sl.first, sl.count, &out);
+        const int src = sink(user, static_cast<int64_t>(gid0) + sl.first, sl.count, &out);
         sink_ms += std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - s0).count();
         if (src != 0) {
             rc = Fail(STLQ_MI355_ERR_CALLBACK, "sink callback failed");
@@ -1440,7 +1444,7 @@ int stlq_mi355_encode_stream(stlq_mi355_ctx* c, int64_t n_total, int64_t chunk, 
         sl.count = std::min(chunk, n_total - first);
         const size_t cnt = static_cast<size_t>(sl.count);
         const auto f0 = std::chrono::steady_clock::now();
-        if (fill(user, sl.first, sl.count, sl.hin) != 0) {
+        if (fill(user, static_cast<int64_t>(gid0) + sl.first, sl.count, sl.hin) != 0) {
             rc = Fail(STLQ_MI355_ERR_CALLBACK, "fill callback failed");
             break;
         }
@@ -1476,13 +1480,14 @@ int stlq_mi355_encode_stream(stlq_mi355_ctx* c, int64_t n_total, int64_t chunk, 
                                    sl.dcluster.as<uint32_t>() + t0, sl.dcodes.as<uint8_t>() + t0 * code_b,
                                    sl.dbest.as<float>() + t0, c->stream, &te, want ? &sp->encode : nullptr,
                                    want ? sl.da.as<float>() + t0 * m : nullptr,
-                                   want ? sl.dcost.as<float>() + t0 : nullptr, static_cast<uint64_t>(sl.first + t0));
+                                   want ? sl.dcost.as<float>() + t0 : nullptr,
+                                   gid0 + static_cast<uint64_t>(sl.first + t0));
                 if (rc == STLQ_MI355_OK) c->tiles.push_back(te);
             } else {
                 EncodeOut o{sl.dcodes.as<uint8_t>() + t0 * m, want ? sl.da.as<float>() + t0 * m : nullptr,
                             want ? sl.dcost.as<float>() + t0 : nullptr, nullptr};
                 rc = EncodeTile(c, dX + t0 * d, nt, sp->encode, o, c->stream, true, true,
-                                static_cast<uint64_t>(sl.first + t0));
+                                gid0 + static_cast<uint64_t>(sl.first + t0));
             }
         }
         if (rc != STLQ_MI355_OK) break;

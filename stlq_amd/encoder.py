@@ -258,11 +258,12 @@ class Context:
 
     # ---- streaming -----------------------------------------------------------------------
     def encode_stream(self, n_total, chunk, cfg: EncodeConfig, fill, sink, input_u8=False, large_root=False,
-                      root_mode=1, R=None):
-        """Streaming encode. fill(first, count, out) fills `out` ((count, d) float32, or uint8 when
-        input_u8). sink(first, count, result) receives a dict of numpy copies: full precomp ->
-        codes; large root -> cluster_id, B_small, best_err; both with a and cost when coefficients
-        or ICM/ILS are asked for."""
+                      root_mode=1, R=None, start_id=0):
+        """Streaming encode of the vectors with global ids start_id .. start_id + n_total - 1.
+        fill(first, count, out) fills `out` ((count, d) float32, or uint8 when input_u8) with the
+        vectors from global id `first`. sink(first, count, result) receives a dict of numpy copies:
+        full precomp -> codes; large root -> cluster_id, B_small, best_err; both with a and cost
+        when coefficients or ICM/ILS are asked for. ILS perturbations are keyed by the global ids."""
         if large_root:
             d, m = self.lr[0], len(self.lr[1])
         else:
@@ -313,7 +314,8 @@ class Context:
             Rc = np.ascontiguousarray(np.asarray(R, dtype=np.float32).T)
             if Rc.shape != (d, d):
                 raise ValueError(f"R must be {d} x {d}")
-        p = _lib.StreamParams(cfg.to_c(), int(bool(input_u8)), int(bool(large_root)), int(root_mode), _p(Rc, _f32p))
+        p = _lib.StreamParams(cfg.to_c(), int(bool(input_u8)), int(bool(large_root)), int(root_mode), _p(Rc, _f32p),
+                              int(start_id))
         rc = self.lib.stlq_mi355_encode_stream(self.h, int(n_total), int(chunk), ctypes.byref(p), f, s, None,
                                                ctypes.byref(st))
         if err:
@@ -450,16 +452,18 @@ def EncodeBase(ctx: Context, X, cfg: EncodeConfig):
     return BaseEncoding(codes, a), bm, fm
 
 
-def EncodeBaseStreamingF32(ctx: Context, n_total, chunk, cfg: EncodeConfig, fill, sink):
-    """src/quantizer/encode_base_streaming.cpp:4544-4579: fp32 chunks, double-buffered H2D."""
-    return ctx.encode_stream(n_total, chunk, cfg, fill, sink)
+def EncodeBaseStreamingF32(ctx: Context, n_total, chunk, cfg: EncodeConfig, fill, sink, start_id=0):
+    """src/quantizer/encode_base_streaming.cpp:4544-4579: fp32 chunks, double-buffered H2D; ids
+    start at start_id (a resumed stream)."""
+    return ctx.encode_stream(n_total, chunk, cfg, fill, sink, start_id=start_id)
 
 
-def EncodeBaseStreaming(ctx: Context, n_total, chunk, cfg: EncodeConfig, fill, sink, root_mode=1):
+def EncodeBaseStreaming(ctx: Context, n_total, chunk, cfg: EncodeConfig, fill, sink, root_mode=1, start_id=0):
     """src/quantizer/encode_base_streaming.cpp:1913 (large pipeline): uint8 chunks widened on the
     device, large-root beam, then the large-root refit (:1117-1210) when cfg asks for
     coefficients or ICM/ILS; sink gets cluster_id, B_small, best_err (and a, cost) per chunk."""
-    return ctx.encode_stream(n_total, chunk, cfg, fill, sink, input_u8=True, large_root=True, root_mode=root_mode)
+    return ctx.encode_stream(n_total, chunk, cfg, fill, sink, input_u8=True, large_root=True, root_mode=root_mode,
+                             start_id=start_id)
 
 
 def BuildPrecompLargeRoot(ctx: Context, C0, C_small, h_vec):

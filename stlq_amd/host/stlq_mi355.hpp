@@ -20,6 +20,7 @@
 #include <memory>
 #include <stdexcept>
 #include <string>
+#include <utility>
 #include <vector>
 
 #include "stlq_mi355.h"
@@ -276,6 +277,60 @@ inline bool EncodeBase(const EncodeOptions& opt, const ColMajorMatrix<float>& Xb
     return true;
 }
 
+// The configuration fields the encoder reads (include/stlq/common/config.h: base.encode.*,
+// :473-482; large.base_block, :573; runtime.*, :60-67). Defaults are the reference's.
+struct BaseEncodeConfig {
+    bool use_abs = true;
+    int H_beam = 2;
+    int ils_iters = 0;
+    int icm_iters = 4;
+    int perturb_k = 3;
+    int seed = 38251450;
+};
+struct BaseConfig {
+    BaseEncodeConfig encode;
+};
+struct LargeConfig {
+    int base_block = 200000;
+    bool write_vector_bucket = true;  // config.h:583: store raw vectors beside the codes
+};
+struct RuntimeConfig {
+    bool use_cuda = false;
+    int cuda_device = 0;
+    std::string cuda_mode = "strict";
+};
+struct Config {
+    BaseConfig base;
+    LargeConfig large;
+    RuntimeConfig runtime;
+};
+
+struct Dataset {  // types.h:190-195
+    ColMajorMatrix<float> Xt;
+    ColMajorMatrix<float> Xb;
+    ColMajorMatrix<float> Xq;
+    std::vector<int> gt;
+};
+
+class KernelProvider;  // legacy provider; EncodeBase ignores it (encoder_encode_base.inc:10)
+
+// EncodeBase with the reference's signature (include/stlq/quantizer/encoder.h:66-74): encodes
+// dataset.Xb with config.base.encode.
+inline bool EncodeBase(const Config& config, const Dataset& dataset, const CodebookPack& codebooks,
+                       const Precomp& precomp, KernelProvider* kernels, BaseEncoding* base, float* out_beam_mse,
+                       float* out_final_mse, std::string* error) {
+    (void)kernels;
+    const BaseEncodeConfig& e = config.base.encode;
+    EncodeOptions opt;
+    opt.use_abs = e.use_abs;
+    opt.H_beam = e.H_beam;
+    opt.ils_iters = e.ils_iters;
+    opt.icm_iters = e.icm_iters;
+    opt.perturb_k = e.perturb_k;
+    opt.seed = e.seed;
+    return EncodeBase(opt, dataset.Xb, codebooks, precomp, base, out_beam_mse, out_final_mse, error);
+}
+
 class StreamKernelProvider;  // the reference's GEMM provider; unused here (the device runs the GEMMs)
 
 struct PrecompLargeRootBuildOptions {  // precomp_large_root.h:40-47 (CPU-only options)
@@ -472,6 +527,154 @@ inline void DynamicIcmWithIlsAbsNoNormalLargeRoot(const ColMajorMatrix<float>& X
     (void)print_progress;
     detail::DynamicIcmLargeRoot(X, pre, xC_small, icm_iters, ils_iters, perturb_k, seed, true, cluster_id, B_small, a,
                                 X_norm2, cost, sample_id_offset);
+}
+
+// Optional hook after each committed output block (include/stlq/quantizer/encode_base_streaming.h:25-28).
+template <class Writer>
+struct StreamingBasicCommitHookT {
+    void* ctx = nullptr;
+    bool (*OnCommit)(std::uint64_t next_id, Writer* writer, void* ctx, std::string* err) = nullptr;
+};
+
+namespace detail {
+
+template <class Reader, class Writer>
+struct StreamUser {
+    const Reader* reader;
+    Writer* writer;
+    const StreamingBasicCommitHookT<Writer>* hook;
+    int d, m;
+    bool large;
+    std::string* err;
+    bool keep_raw;
+    double cost_sum = 0.0;
+    std::int64_t cost_n = 0;
+    // Raw tiles read but not yet written (fill runs up to two chunks ahead of sink).
+    std::vector<std::pair<std::int64_t, std::vector<float>>> raw;
+};
+
+template <class Reader, class Writer>
+int StreamFill(void* u, std::int64_t first, std::int64_t count, void* dst) {
+    auto* s = static_cast<StreamUser<Reader, Writer>*>(u);
+    const std::size_t len = static_cast<std::size_t>(count) * static_cast<std::size_t>(s->d);
+    float* x = static_cast<float*>(dst);
+    if (!s->reader->ReadBlockInto(static_cast<std::uint64_t>(first), static_cast<std::uint32_t>(count), x,
+                                  len * sizeof(float), s->err))
+        return 1;
+    if (s->keep_raw) s->raw.emplace_back(first, std::vector<float>(x, x + len));
+    return 0;
+}
+
+template <class Reader, class Writer>
+int StreamSink(void* u, std::int64_t first, std::int64_t count, const stlq_mi355_chunk_out* out) {
+    auto* s = static_cast<StreamUser<Reader, Writer>*>(u);
+    const int m = s->m;
+    const std::size_t n = static_cast<std::size_t>(count);
+    std::vector<std::uint32_t> cluster_id(n);
+    ColMajorMatrix<Code> B_small(std::max(0, m - 1), static_cast<int>(count));
+    ColMajorMatrix<float> a(m, static_cast<int>(count));
+    if (s->large) {  // the large-root beam's roots and small codes
+        std::copy(out->cluster_id, out->cluster_id + n, cluster_id.begin());
+        if (m > 1) std::copy(out->B_small, out->B_small + n * (m - 1), B_small.data.begin());
+    } else {  // full precomp: layer 0's code is the cluster id (ExtractClusterIdAndCodesSmall)
+        for (std::size_t i = 0; i < n; ++i) {
+            cluster_id[i] = out->codes[i * m];
+            for (int l = 1; l < m; ++l) B_small.data[i * (m - 1) + (l - 1)] = out->codes[i * m + l];
+        }
+    }
+    if (out->a) std::copy(out->a, out->a + n * m, a.data.begin());
+    if (out->cost) {
+        for (std::size_t i = 0; i < n; ++i) s->cost_sum += out->cost[i] < 0.0f ? 0.0 : out->cost[i];
+        s->cost_n += count;
+    }
+    if (s->keep_raw) {
+        auto it = std::find_if(s->raw.begin(), s->raw.end(), [&](const auto& e) { return e.first == first; });
+        if (it == s->raw.end()) {
+            if (s->err) *s->err = "EncodeBaseStreaming: raw tile missing for block.";
+            return 1;
+        }
+        const bool ok = s->writer->AppendBlockRawF32(static_cast<std::uint64_t>(first), cluster_id, B_small, a,
+                                                     it->second.data(), s->d, s->err);
+        s->raw.erase(it);
+        if (!ok) return 1;
+    } else if (!s->writer->AppendBlock(static_cast<std::uint64_t>(first), cluster_id, B_small, a, nullptr,
+                                       s->err)) {
+        return 1;
+    }
+    if (s->hook && s->hook->OnCommit &&
+        !s->hook->OnCommit(static_cast<std::uint64_t>(first + count), s->writer, s->hook->ctx, s->err))
+        return 1;
+    return 0;
+}
+
+}  // namespace detail
+
+// EncodeBaseStreamingF32 (include/stlq/quantizer/encode_base_streaming.h:46-58,
+// src/quantizer/encode_base_streaming.cpp:4544-4579): encodes the reader's vectors start_id..n()-1
+// in blocks of config.large.base_block, double-buffered on the device, and appends each block's
+// cluster ids, small codes and LS coefficients to the writer in order (then calls the commit
+// hook). Reader is io::FvecsReader-like (d(), n(), ReadBlockInto(start, count, dst, bytes, err));
+// Writer is io::BaseBasicWriter-like: AppendBlockRawF32(start_id, cluster_id, B_small, a, x, ld, err)
+// with the raw (unrotated) tile when config.large.write_vector_bucket is set (:4396-4404), else
+// AppendBlock(start_id, cluster_id, B_small, a, nullptr, err).
+// pre_large selects the large-root beam with the nearest root forced (the device beams the
+// reference's streaming calls, :1005-1083) and its refit; otherwise the full precomp
+// is used and layer 0's code becomes the cluster id. The rotation R (d x d) is applied on the
+// device (empty R: none). out_final_mse receives the mean cost; out_beam_mse the same when no ICM
+// runs (the streamed refit is final).
+template <class Reader, class Writer>
+bool EncodeBaseStreamingF32(const Config& cfg, const Reader& base_reader, const ColMajorMatrix<float>& R,
+                            const CodebookPack& C_root, const Precomp& pre_full, const PrecompLargeRoot* pre_large,
+                            StreamKernelProvider* kernels, Writer* writer, float* out_beam_mse, float* out_final_mse,
+                            std::string* err, std::uint64_t start_id = 0,
+                            const StreamingBasicCommitHookT<Writer>* commit_hook = nullptr) {
+    (void)C_root;
+    (void)kernels;
+    if (!writer) {
+        if (err) *err = "EncodeBaseStreaming: writer is null.";
+        return false;
+    }
+    const std::uint64_t nbase = base_reader.n();
+    if (start_id > nbase) {
+        if (err) *err = "EncodeBaseStreaming: start_id out of range.";
+        return false;
+    }
+    const int d = base_reader.d();
+    if (d <= 0 || nbase == 0) {
+        if (err) *err = "EncodeBaseStreaming: empty base reader.";
+        return false;
+    }
+    const std::uint64_t block = static_cast<std::uint64_t>(std::max(1, cfg.large.base_block));
+    if (commit_hook && commit_hook->OnCommit && start_id % block != 0) {
+        if (err) *err = "EncodeBaseStreaming: start_id must be a multiple of large.base_block when using checkpointing.";
+        return false;
+    }
+    const BaseEncodeConfig& e = cfg.base.encode;
+    stlq_mi355_stream_params sp{};
+    sp.encode = stlq_mi355_encode_params{std::max(1, e.H_beam), e.icm_iters, e.ils_iters, e.perturb_k,
+                                          e.use_abs ? 1 : 0, static_cast<std::uint32_t>(e.seed), 1};
+    sp.input_u8 = 0;
+    sp.large_root = pre_large ? 1 : 0;
+    sp.root_mode = 1;
+    sp.R = (R.rows == d && R.cols == d) ? R.data.data() : nullptr;
+    sp.start_id = start_id;
+    detail::StreamUser<Reader, Writer> u{&base_reader, writer, commit_hook, d,
+                                         pre_large ? pre_large->m : pre_full.m, pre_large != nullptr, err,
+                                         cfg.large.write_vector_bucket};
+    stlq_mi355_ctx* ctx = pre_large ? detail::BindLargeRoot(*pre_large) : detail::Bind(pre_full);
+    stlq_mi355_stream_stats st{};
+    const int rc = stlq_mi355_encode_stream(ctx, static_cast<std::int64_t>(nbase - start_id),
+                                            static_cast<std::int64_t>(block), &sp,
+                                            &detail::StreamFill<Reader, Writer>, &detail::StreamSink<Reader, Writer>,
+                                            &u, &st);
+    if (rc != STLQ_MI355_OK) {
+        if (err && err->empty()) *err = stlq_mi355_last_error();
+        return false;
+    }
+    const float mse = u.cost_n > 0 ? static_cast<float>(u.cost_sum / static_cast<double>(u.cost_n)) : 0.0f;
+    if (out_final_mse) *out_final_mse = mse;
+    if (out_beam_mse) *out_beam_mse = mse;
+    return true;
 }
 
 }  // namespace stlq

@@ -33,6 +33,81 @@ s::CodebookPack MakePack(int d, int m, const int* h_vec, const float* C_all) {
     return pack;
 }
 
+// FvecsReader-like view of a caller array (d x n column-major).
+struct MemReader {
+    int d_;
+    std::uint64_t n_;
+    const float* x;
+    int d() const { return d_; }
+    std::uint64_t n() const { return n_; }
+    bool ReadBlockInto(std::uint64_t start, std::uint32_t count, float* dst, std::size_t bytes, std::string* err) const {
+        const std::size_t want = static_cast<std::size_t>(count) * static_cast<std::size_t>(d_) * sizeof(float);
+        if (start + count > n_ || bytes < want) {
+            if (err) *err = "MemReader: block out of range";
+            return false;
+        }
+        std::memcpy(dst, x + start * static_cast<std::uint64_t>(d_), want);
+        return true;
+    }
+};
+
+// BaseBasicWriter-like recorder: places each block's records at their global ids and checks that
+// blocks arrive in order.
+struct MemWriter {
+    int d, m;
+    std::uint64_t next = 0;
+    int blocks = 0;
+    std::uint32_t* cluster_id;
+    std::uint8_t* B_small;
+    float* a;
+    float* raw;  // may be null
+    bool Put(std::uint64_t start, const std::vector<std::uint32_t>& cid, const s::ColMajorMatrix<s::Code>& Bs,
+             const s::ColMajorMatrix<float>& am, const float* x, int ld, std::string* err) {
+        if (start != next || Bs.cols != static_cast<int>(cid.size()) || am.cols != Bs.cols || am.rows != m ||
+            Bs.rows != m - 1) {
+            if (err) *err = "MemWriter: block out of order or misshapen";
+            return false;
+        }
+        const std::size_t n = cid.size();
+        std::memcpy(cluster_id + start, cid.data(), n * sizeof(std::uint32_t));
+        std::memcpy(B_small + start * (m - 1), Bs.data.data(), Bs.data.size());
+        std::memcpy(a + start * m, am.data.data(), am.data.size() * sizeof(float));
+        if (x && raw)
+            for (std::size_t i = 0; i < n; ++i)
+                std::memcpy(raw + (start + i) * d, x + i * static_cast<std::size_t>(ld), sizeof(float) * d);
+        next = start + n;
+        ++blocks;
+        return true;
+    }
+    bool AppendBlock(std::uint64_t start, const std::vector<std::uint32_t>& cid, const s::ColMajorMatrix<s::Code>& Bs,
+                     const s::ColMajorMatrix<float>& am, const s::ColMajorMatrix<std::uint8_t>*, std::string* err) {
+        return Put(start, cid, Bs, am, nullptr, 0, err);
+    }
+    bool AppendBlockRawF32(std::uint64_t start, const std::vector<std::uint32_t>& cid,
+                           const s::ColMajorMatrix<s::Code>& Bs, const s::ColMajorMatrix<float>& am, const float* x,
+                           int ld, std::string* err) {
+        if (!x) {
+            if (err) *err = "MemWriter: raw tile missing";
+            return false;
+        }
+        return Put(start, cid, Bs, am, x, ld, err);
+    }
+};
+
+struct HookLog {
+    std::uint64_t last = 0;
+    int calls = 0;
+    bool ordered = true;
+};
+
+bool OnCommit(std::uint64_t next_id, MemWriter* w, void* ctx, std::string*) {
+    auto* h = static_cast<HookLog*>(ctx);
+    h->ordered = h->ordered && next_id == w->next && next_id > h->last;
+    h->last = next_id;
+    ++h->calls;
+    return true;
+}
+
 }  // namespace
 
 extern "C" {
@@ -71,14 +146,16 @@ int mirror_encode(int d, int m, const int* h_vec, const float* C_all, const floa
         std::memcpy(a, am.data.data(), am.data.size() * sizeof(float));
         std::memcpy(cost, cst.data(), cst.size() * sizeof(float));
 
-        s::EncodeOptions opt;
-        opt.use_abs = use_abs != 0;
-        opt.H_beam = H_beam;
-        opt.icm_iters = icm_iters;
-        opt.seed = static_cast<int>(seed);
+        s::Config cfg;  // the reference-signature EncodeBase (encoder.h:66-74)
+        cfg.base.encode.use_abs = use_abs != 0;
+        cfg.base.encode.H_beam = H_beam;
+        cfg.base.encode.icm_iters = icm_iters;
+        cfg.base.encode.seed = static_cast<int>(seed);
+        s::Dataset ds;
+        ds.Xb = Xm;
         s::BaseEncoding base;
         std::string e;
-        if (!s::EncodeBase(opt, Xm, pack, pre, &base, &mse[0], &mse[1], &e)) {
+        if (!s::EncodeBase(cfg, ds, pack, pre, nullptr, &base, &mse[0], &mse[1], &e)) {
             PutError("EncodeBase: " + e, err, errlen);
             return 2;
         }
@@ -138,6 +215,62 @@ int mirror_large_root(int d, int m, const int* h_vec, const float* C0, const flo
         }
         std::memcpy(cluster_id, cid.data(), cid.size() * sizeof(std::uint32_t));
         std::memcpy(B_small, Bs.data.data(), Bs.data.size());
+        return 0;
+    } catch (const std::exception& ex) {
+        PutError(ex.what(), err, errlen);
+        return 4;
+    }
+}
+
+// EncodeBaseStreamingF32 over an in-memory reader and a recording writer. large != 0: C_all holds
+// the root layer then the small layers and the large-root beam runs; else the full precomp. The
+// writer's arrays are indexed by global id (entries below start_id stay untouched); raw (d x n) gets
+// the raw tiles when write_raw. hook_calls (out) counts the commit hook's calls (-1: out of order).
+// Return 0 on success, 1 when the call returned false (err holds its message), 4 on an exception.
+int mirror_stream(int d, int m, const int* h_vec, const float* C_all, const float* X, int n, int large, int H_beam,
+                  int icm_iters, int ils_iters, int base_block, uint64_t start_id, int write_raw, int use_hook,
+                  uint32_t* cluster_id, uint8_t* B_small, float* a, float* raw, float* mse, int* hook_calls,
+                  char* err, int errlen) {
+    try {
+        s::Config cfg;
+        cfg.base.encode.H_beam = H_beam;
+        cfg.base.encode.icm_iters = icm_iters;
+        cfg.base.encode.ils_iters = ils_iters;
+        cfg.large.base_block = base_block;
+        cfg.large.write_vector_bucket = write_raw != 0;
+        const s::CodebookPack pack = MakePack(d, m, h_vec, C_all);
+        s::Precomp pre_full;
+        s::PrecompLargeRoot pre_large;
+        std::string e;
+        if (d > 0 && m > 0) {
+            if (large) {
+                if (!s::BuildPrecompLargeRoot(pack, nullptr, s::PrecompLargeRootBuildOptions{}, &pre_large, &e)) {
+                    PutError("BuildPrecompLargeRoot: " + e, err, errlen);
+                    return 4;
+                }
+            } else if (!s::BuildPrecomp(pack, &pre_full)) {
+                PutError("BuildPrecomp failed", err, errlen);
+                return 4;
+            }
+        }
+        const MemReader reader{d, static_cast<std::uint64_t>(n), X};
+        MemWriter writer{d, m, start_id, 0, cluster_id, B_small, a, raw};
+        HookLog log;
+        s::StreamingBasicCommitHookT<MemWriter> hook;
+        hook.ctx = &log;
+        hook.OnCommit = &OnCommit;
+        const bool ok = s::EncodeBaseStreamingF32(cfg, reader, s::ColMajorMatrix<float>(), pack, pre_full,
+                                                  large ? &pre_large : nullptr, nullptr, &writer, &mse[0], &mse[1],
+                                                  &e, start_id, use_hook ? &hook : nullptr);
+        *hook_calls = log.ordered ? log.calls : -1;
+        if (!ok) {
+            PutError(e, err, errlen);
+            return 1;
+        }
+        if (writer.next != static_cast<std::uint64_t>(n)) {
+            PutError("stream ended before the last id", err, errlen);
+            return 4;
+        }
         return 0;
     } catch (const std::exception& ex) {
         PutError(ex.what(), err, errlen);

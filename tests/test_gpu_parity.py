@@ -244,11 +244,11 @@ def _oracle_encode(orc, X, C, h, Hb, icm_iters=0, use_abs=True, seed=38251450, g
     return codes, a, cost
 
 
-def _scaled_config(cfg):
+def _scaled_config(cfg, n=None):
     from stlq_amd import workloads
 
     w = workloads.CONFIGS[cfg]
-    n = {"C1": 20000, "C2": 4000, "C3": 4000, "C4": 1000}[cfg]
+    n = n or {"C1": 20000, "C2": 4000, "C3": 4000, "C4": 1000}[cfg]
     mix = workloads.Mixture(w.kind, w.d, w.n_comp, w.seed)
     Xtr = mix.sample(10_000_000, 4000 if w.d < 900 else 2000)
     C = workloads.residual_codebooks(Xtr, w.m, w.K, 4, w.seed + 5, spherical=(w.kind == "sphere"))
@@ -307,19 +307,49 @@ def test_encode_with_ils_end_to_end(ctx, orc, monkeypatch):
     assert np.array_equal(codes_s, codes_g) and np.array_equal(_bits(cost_s), _bits(cost_g))
 
 
-@pytest.mark.parametrize("cfg", ["C1", "C2", "C3", "C4"])
+@pytest.mark.parametrize("cfg", ["C1", "C2", "C3"])
 def test_encode_parity_unfused_oracle_xc(ctx, orc, cfg):
     """Sensitivity to the GEMM summation order (the reference's BLAS order is unpinned): against
     an oracle whose xC is a non-fused sequential dot, the codes differ only on cost ties —
     every differing vector's two tuples have fp64 LS costs equal within 1e-5 relative — and on
-    at most 0.1% of the vectors (1% for the 1000-vector d=960 case, where a single tie is 0.1%)."""
+    at most 0.1% of the vectors."""
     w, X, C, h = _scaled_config(cfg)
+    print(f"unfused parity {cfg} n={X.shape[0]}", flush=True)
     ctx.set_codebooks(C, h)
     cfgc = EncodeConfig(H_beam=w.H_beam, icm_iters=w.icm_iters, want_coeffs=True)
     codes_g, _, _, _ = ctx.encode(X, cfgc)
     codes_o, _, _ = _oracle_encode(orc, X, C, h, w.H_beam, w.icm_iters, gemm_mode=0)
-    rep = parity(orc, X, C, h, codes_o, codes_g, max_frac=(1e-2 if cfg == "C4" else 1e-3))
+    rep = parity(orc, X, C, h, codes_o, codes_g, max_frac=1e-3)
+    print(rep, flush=True)
     assert rep["ok"], rep
+
+
+def test_encode_parity_c4_10k(ctx, orc):
+    """C4 (d=960, M=16, K=256, beam 8) on 10,000 vectors. With the oracle's xC in the device GEMM's
+    fused k order the whole encode is bit-exact: codes, coefficients and costs, 0 of 10,000
+    differing. Against an xC summed in the other (non-fused, sequential) order, the ulp-level
+    differences of 960-term dot products change the beam's choices on a few tenths of a percent of
+    the vectors, with real fp64-MSE differences (the beam is discontinuous in its inputs), so the
+    per-vector tie rule cannot hold across summation orders. There the test bounds the share of
+    differing vectors (< 1%) and the mean fp64 MSE (within 1e-4 relative, either direction)."""
+    w, X, C, h = _scaled_config("C4", n=10_000)
+    print(f"c4 10k: n={X.shape[0]}", flush=True)
+    ctx.set_codebooks(C, h)
+    cfgc = EncodeConfig(H_beam=w.H_beam, icm_iters=w.icm_iters, want_coeffs=True)
+    codes_g, a_g, cost_g, _ = ctx.encode(X, cfgc)
+    codes_f, a_f, cost_f = _oracle_encode(orc, X, C, h, w.H_beam, w.icm_iters, gemm_mode=1)
+    bad = np.nonzero(np.any(codes_f != codes_g, axis=1))[0]
+    assert bad.size == 0, (bad.size, bad[:10])
+    assert np.array_equal(_bits(a_f), _bits(a_g))
+    assert np.array_equal(_bits(cost_f), _bits(cost_g))
+    codes_o, _, _ = _oracle_encode(orc, X, C, h, w.H_beam, w.icm_iters, gemm_mode=0)
+    diff = np.any(codes_o != codes_g, axis=1)
+    mse_g = orc.mse_fp64_refit(X, C, h, codes_g)
+    mse_o = orc.mse_fp64_refit(X, C, h, codes_o)
+    rel = (mse_g.sum() - mse_o.sum()) / mse_o.sum()
+    print(f"c4 10k vs the non-fused xC order: {diff.sum()} differ, mean fp64 MSE rel diff {rel:.2e}", flush=True)
+    assert diff.mean() < 1e-2
+    assert abs(rel) <= 1e-4
 
 
 def test_encode_device_matches_host(ctx, orc):
@@ -734,3 +764,103 @@ def test_large_root_nearest_nan_roots(ctx, orc, nan_roots):
     assert np.array_equal(Bs_o, Bs_g)
     same = (_bits(err_o) == _bits(err_g)) | (np.isnan(err_o) & np.isnan(err_g))
     assert np.all(same)
+
+
+@pytest.mark.parametrize("large_root", [False, True])
+def test_stream_resume_start_id(ctx, orc, large_root):
+    """EncodeBaseStreaming from a start_id (encode_base_streaming.cpp:1913-1936, :874): two resumed
+    half-streams (the second at start_id = n/2) give exactly the whole stream's codes, coefficients
+    and costs, with ILS perturbations keyed by the global id, and both equal the oracle with
+    sample_id_offset 0 over all n; fill and sink see global ids."""
+    n, half, chunk = 4000, 2000, 700
+    cfg = EncodeConfig(H_beam=4, icm_iters=1, ils_iters=3, perturb_k=3, want_coeffs=True)
+    print(f"stream resume large_root={large_root}", flush=True)
+    if large_root:
+        p = _lr_refit_problem(ctx, orc, 5, 811, n=n, d=64, h0=1024, K=64)
+        X = p["X"]
+        cid, Bs, _ = ctx.beam_search_large_root(X, 4, root_mode=1)
+        nx2 = orc.xnorm2(X)
+        xs = orc.gemm_xc(p["Cs"], X, mode=1)
+        B_o, a_o, c_o, _ = orc.icm_ils_large_root(X, p["C0"], p["norm0"], xs, p["Gs"], p["G0S"], p["invs"], p["h"],
+                                                  cid, nx2, Bs, 1, 3, 3, True, 38251450, 0)
+        want = {"cluster_id": cid, "B_small": B_o, "a": a_o, "cost": c_o}
+        kw = dict(large_root=True, root_mode=1)
+    else:
+        X, C = rvq_problem(812, n, 32, 5, 64, train_n=2000, iters=3)
+        h = [64] * 5
+        ctx.set_codebooks(C, h)
+        codes_o, a_o, cost_o = _oracle_encode(orc, X, C, h, 4, icm_iters=1, ils_iters=3, perturb_k=3)
+        want = {"codes": codes_o, "a": a_o, "cost": cost_o}
+        kw = {}
+
+    def run(start, count):
+        got = {k: np.zeros((count,) + v.shape[1:], v.dtype) for k, v in want.items()}
+        seen = []
+
+        def fill(first, cnt, out):
+            assert start <= first and first + cnt <= start + count
+            out[:] = X[first:first + cnt]
+
+        def sink(first, cnt, res):
+            seen.append(first)
+            for k in got:
+                got[k][first - start:first - start + cnt] = res[k]
+
+        ctx.encode_stream(count, chunk, cfg, fill, sink, start_id=start, **kw)
+        assert seen[0] == start and seen == sorted(seen)
+        return got
+
+    whole = run(0, n)
+    first, second = run(0, half), run(half, n - half)
+    for k in want:
+        joined = np.concatenate([first[k], second[k]])
+        assert np.array_equal(np.ascontiguousarray(joined).view(np.uint8),
+                              np.ascontiguousarray(whole[k]).view(np.uint8)), k
+        assert np.array_equal(np.ascontiguousarray(whole[k]).view(np.uint8),
+                              np.ascontiguousarray(want[k]).view(np.uint8)), k
+
+
+def test_stream_large_root_c5_shape(ctx, orc):
+    """The C5 workload's shape on a 2,048-vector sample: uint8 descriptor-like vectors streamed in
+    chunks, nearest of h0 = 65,536 root codewords (the fused root GEMM sweeps all 512 root tiles),
+    16 residual codebooks of 256 (layers 1..16, the deep large-root kernels), beam 32, then the
+    large-root LS refit and costs (encode_base_streaming.cpp:1117-1210). Cluster ids, B_small,
+    coefficients and costs are identical to the oracle's."""
+    from stlq_amd import workloads
+
+    w = workloads.CONFIGS["C5"]
+    n, h0, msmall, K, Hb = 2048, 65536, 16, 256, 32
+    mix = workloads.Mixture(w.kind, w.d, w.n_comp, w.seed)
+    C0 = mix.sample(20_000_000, h0)
+    Xtr = mix.sample(10_000_000, 4000)
+    lab = np.argmax(2.0 * (Xtr @ C0.T) - np.sum(C0 * C0, axis=1)[None, :], axis=1)
+    Cs = workloads.residual_codebooks(Xtr - C0[lab], msmall, K, 2, w.seed + 77)
+    Xu8 = mix.sample(0, n).astype(np.uint8)  # clipped, rounded to [0, 255]: exact as uint8
+    Xf = Xu8.astype(np.float32)
+    h = [h0] + [K] * msmall
+    print(f"c5 shape: n={n} h0={h0} small={msmall}x{K} beam={Hb}", flush=True)
+    ctx.set_large_root(C0, Cs, h)
+    got = {"cluster_id": np.zeros(n, np.uint32), "B_small": np.zeros((n, msmall), np.uint8),
+           "a": np.zeros((n, msmall + 1), np.float32), "cost": np.zeros(n, np.float32)}
+
+    def fill(first, count, out):
+        out[:] = Xu8[first:first + count]
+
+    def sink(first, count, res):
+        for k in got:
+            got[k][first:first + count] = res[k]
+
+    cfg = EncodeConfig(H_beam=Hb, icm_iters=0, want_coeffs=True)
+    ctx.encode_stream(n, 700, cfg, fill, sink, input_u8=True, large_root=True, root_mode=1)
+    print("c5 shape: device stream done", flush=True)
+    norm0, Gs, G0S = orc.build_precomp_large_root(C0, Cs)
+    invs = orc.invnorm_small(Cs)
+    nx2 = orc.xnorm2(Xf)
+    xs = orc.gemm_xc(Cs, Xf, mode=1)
+    cid, Bs, _ = orc.beam_search_large_root(Xf, nx2, C0, norm0, xs, Gs, G0S, h, Hb, root_mode=1)
+    B_o, a_o, c_o, _ = orc.icm_ils_large_root(Xf, C0, norm0, xs, Gs, G0S, invs, h, cid, nx2, Bs, 0, 0, 3, True,
+                                              38251450, 0)
+    assert np.array_equal(got["cluster_id"], cid), np.nonzero(got["cluster_id"] != cid)[0][:10]
+    assert np.array_equal(got["B_small"], B_o), np.nonzero(np.any(got["B_small"] != B_o, axis=1))[0][:10]
+    assert np.array_equal(_bits(got["a"]), _bits(a_o))
+    assert np.array_equal(_bits(got["cost"]), _bits(c_o))

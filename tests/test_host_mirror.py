@@ -2,7 +2,8 @@
 
 tests/host_mirror_check.cpp drives the reference-named functions (BuildPrecomp, BeamSearchPrefixLS,
 ComputeXNorm2, DynamicIcmWithIls*NoNormal, EncodeBase, BuildPrecompLargeRoot,
-BeamSearchPrefixLSLargeRoot) on arrays handed over from here; the GPU tests compare what they
+BeamSearchPrefixLSLargeRoot, EncodeBaseStreamingF32 over a reader/writer pair) on arrays handed
+over from here; the GPU tests compare what they
 return with the oracle, bit for bit, so a transposed operand or a misplaced argument in the
 mirror's plumbing fails them.
 """
@@ -35,6 +36,11 @@ def _lib():
     lib.mirror_large_root.argtypes = [ctypes.c_int, ctypes.c_int, _i32p, _f32p, _f32p, _f32p, ctypes.c_int,
                                       ctypes.c_int, ctypes.c_int, ctypes.c_int, _u32p, _u8p, _f32p, _f32p,
                                       ctypes.c_char_p, ctypes.c_int]
+    lib.mirror_stream.restype = ctypes.c_int
+    lib.mirror_stream.argtypes = [ctypes.c_int, ctypes.c_int, _i32p, _f32p, _f32p, ctypes.c_int, ctypes.c_int,
+                                  ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_uint64,
+                                  ctypes.c_int, ctypes.c_int, _u32p, _u8p, _f32p, _f32p, _f32p, _i32p,
+                                  ctypes.c_char_p, ctypes.c_int]
     return lib
 
 
@@ -48,7 +54,34 @@ def _bits(a):
 
 def test_hostcheck_library_loads():
     lib = _lib()
-    assert lib.mirror_encode is not None and lib.mirror_large_root is not None
+    assert lib.mirror_encode is not None and lib.mirror_large_root is not None and lib.mirror_stream is not None
+
+
+def _stream(d, m, h, C_all, X, n, large, Hb, icm, ils, block, start_id, write_raw, use_hook):
+    cid = np.full(n, 0xFFFFFFFF, np.uint32)
+    Bs = np.zeros((n, max(m - 1, 0)), np.uint8)
+    a = np.zeros((n, m), np.float32)
+    raw = np.zeros((n, d), np.float32)
+    mse = np.zeros(2, np.float32)
+    calls = np.zeros(1, np.int32)
+    err = ctypes.create_string_buffer(512)
+    rc = _lib().mirror_stream(d, m, _p(h, _i32p), _p(C_all, _f32p), _p(X, _f32p), n, large, Hb, icm, ils, block,
+                              start_id, write_raw, use_hook, _p(cid, _u32p), _p(Bs, _u8p), _p(a, _f32p),
+                              _p(raw, _f32p), _p(mse, _f32p), _p(calls, _i32p), err, 512)
+    return rc, err.value.decode(), dict(cid=cid, Bs=Bs, a=a, raw=raw, mse=mse, calls=int(calls[0]))
+
+
+@pytest.mark.parametrize("start_id,block,hook,msg", [(101, 50, 0, "start_id out of range"),
+                                                     (30, 50, 1, "multiple of large.base_block")])
+def test_mirror_stream_rejects_bad_start(start_id, block, hook, msg):
+    """EncodeBaseStreamingF32's argument checks (encode_base_streaming.cpp:4551-4579) run before
+    any device work: m = 0 here builds no precomp."""
+    d, n = 8, 100
+    h = np.zeros(1, np.int32)
+    C = np.zeros(1, np.float32)
+    X = np.zeros((n, d), np.float32)
+    rc, err, _ = _stream(d, 0, h, C, X, n, 1, 4, 0, 0, block, start_id, 1, hook)
+    assert rc == 1 and msg in err, (rc, err)
 
 
 @pytest.mark.gpu
@@ -116,3 +149,70 @@ def test_mirror_large_root_matches_oracle(orc):
     assert np.array_equal(B_o, Bs)
     assert np.array_equal(_bits(a_o), _bits(a))
     assert np.array_equal(_bits(c_o), _bits(cost))
+
+
+def _stream_problem(large):
+    from stlq_amd import workloads
+
+    n, d, K, m, seed = 1800, 32, 64, 4, 95
+    mix = workloads.Mixture("desc", d, 256, seed)
+    rng = np.random.default_rng(seed)
+    if large:
+        h0 = 1200
+        C0 = mix.sample(5_000_000, h0)
+        Xtr = mix.sample(1_000_000, 3000)
+        Cs = workloads.residual_codebooks(Xtr - C0[rng.integers(0, h0, 3000)], m - 1, K, 3, seed + 1)
+        C_all = np.ascontiguousarray(np.concatenate([C0, Cs]), np.float32)
+        h = np.array([h0] + [K] * (m - 1), np.int32)
+    else:
+        C_all = np.ascontiguousarray(workloads.residual_codebooks(mix.sample(1_000_000, 3000), m, K, 3, seed + 1),
+                                     np.float32)
+        h = np.full(m, K, np.int32)
+    X = np.ascontiguousarray(mix.sample(0, n), np.float32)
+    return n, d, m, h, C_all, X
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("large", [1, 0], ids=["large_root", "full_precomp"])
+def test_mirror_stream_matches_oracle_and_resumes(orc, large):
+    """EncodeBaseStreamingF32 through the mirror: blocks reach the writer in id order with the raw
+    tiles, the commit hook sees every block, the records equal the oracle's encode (large root:
+    beam + ICM + ILS keyed by global id; full precomp: layer 0's code as the cluster id), and a run
+    resumed at start_id = 2 blocks writes the same records for the ids it covers."""
+    n, d, m, h, C_all, X = _stream_problem(large)
+    Hb, icm, ils, block = 8, 1, (2 if large else 0), 400
+    print(f"mirror_stream large={large} n={n} d={d} h={list(h)} beam={Hb} icm={icm} ils={ils}", flush=True)
+    rc, err, full = _stream(d, m, h, C_all, X, n, large, Hb, icm, ils, block, 0, 1, 1)
+    assert rc == 0, err
+    assert full["calls"] == (n + block - 1) // block
+    assert np.array_equal(full["raw"], X)
+    nx2 = orc.xnorm2(X)
+    if large:
+        C0, Cs = C_all[:h[0]], C_all[h[0]:]
+        norm0, Gs, G0S = orc.build_precomp_large_root(C0, Cs)
+        xs = orc.gemm_xc(Cs, X, mode=1)
+        # the streamed beam forces the nearest root (root_mode 1), as the reference's device beams do
+        cid_o, Bs_o, _ = orc.beam_search_large_root(X, nx2, C0, norm0, xs, Gs, G0S, list(h), Hb, root_mode=1)
+        B_o, a_o, c_o, _ = orc.icm_ils_large_root(X, C0, norm0, xs, Gs, G0S, orc.invnorm_small(Cs), list(h), cid_o,
+                                                  nx2, Bs_o, icm, ils, 3, True, 38251450, 0)
+        assert np.array_equal(cid_o, full["cid"])
+        assert np.array_equal(B_o, full["Bs"])
+    else:
+        G_o, inv_o = orc.build_precomp(C_all, h)
+        xC = orc.gemm_xc(C_all, X, mode=1)
+        codes_o, _ = orc.beam_search(nx2, xC, G_o, h, Hb)
+        codes_f, a_o, c_o, _ = orc.icm(xC, G_o, inv_o, h, nx2, codes_o, icm, True, 38251450)
+        assert np.array_equal(codes_f[:, 0].astype(np.uint32), full["cid"])
+        assert np.array_equal(codes_f[:, 1:], full["Bs"])
+    assert np.array_equal(_bits(a_o), _bits(full["a"]))
+    want = np.float32(np.mean(np.maximum(c_o.astype(np.float64), 0.0)))
+    assert abs(full["mse"][1] - want) <= 1e-6 * abs(want)
+
+    start = 2 * block
+    rc, err, part = _stream(d, m, h, C_all, X, n, large, Hb, icm, ils, block, start, 0, 1)
+    assert rc == 0, err
+    assert part["calls"] == (n - start + block - 1) // block
+    assert np.all(part["cid"][:start] == 0xFFFFFFFF)
+    for key in ("cid", "Bs", "a"):
+        assert np.array_equal(part[key][start:], full[key][start:]), key
+    assert not part["raw"].any()  # write_vector_bucket off: AppendBlock without the raw tile
