@@ -507,6 +507,73 @@ def test_large_root_bit_exact(ctx, orc, name, seed, n, d, h0, small, Hb, mode):
         assert np.array_equal(cid_g, forced)
 
 
+def _crafted_roots(variant, seed=90, n=500, d=32, h0=300, K=16, m=4):
+    """Root codebooks built to hit the root scan's corner cases (beam_search.cpp:686-705):
+    ties: exact duplicate roots (adjacent and far apart; the lower code must win), zero roots
+    (skipped) and a root that the first 40 vectors are orthogonal to (gamma = 0 exactly: the
+    quotient's range check sends the column to IEEE division);
+    scaled: roots scaled by 2^40 and 2^-40 (alpha outside [2^-60, 2^60]: the IEEE division path)
+    and by 2^64 (alpha overflows to +inf: a0 = 0, error ||x||^2);
+    nan: a root with an infinite entry (alpha = +inf, gamma infinite or NaN, a NaN error that
+    enters the scan and is then replaced or stays, per the slot rule)."""
+    from stlq_amd import workloads
+
+    mix = workloads.Mixture("desc", d, 128, seed)
+    rng = np.random.default_rng(seed)
+    C0 = mix.sample(5_000_000, h0)
+    Xtr = mix.sample(1_000_000, 2000)
+    Cs = workloads.residual_codebooks(Xtr - C0[rng.integers(0, h0, 2000)], m - 1, K, 3, seed + 1)
+    X = mix.sample(0, n)
+    if variant == "ties":
+        for dst in (11, 50, 120, 299):
+            C0[dst] = C0[10]
+        C0[[5, 77, 200]] = 0.0
+        C0[3] = 0.0
+        C0[3, 0] = 1.5
+        X[:40, 0] = 0.0
+        # make the duplicated root the nearest one for some vectors
+        X[40:80] = C0[10] + 0.01 * X[40:80]
+    elif variant == "scaled":
+        C0[30] *= np.float32(2.0 ** 40)
+        C0[31] *= np.float32(2.0 ** -40)
+        C0[32] *= np.float32(2.0 ** 64)
+        X[:30] = C0[31] * np.float32(2.0 ** 40) + 0.01 * X[:30]  # near the tiny root's direction
+    else:
+        C0[250, 0] = np.inf
+        X[:20, 0] = 0.0  # 0 * inf: a NaN gamma
+    return X.astype(np.float32), C0.astype(np.float32), Cs, [h0] + [K] * (m - 1)
+
+
+@pytest.mark.parametrize("variant", ["ties", "scaled", "nan"])
+@pytest.mark.parametrize("root_mode", [1, 0], ids=["nearest", "topH"])
+def test_large_root_crafted_roots(ctx, orc, variant, root_mode):
+    """Device root scans (the nearest-root GEMM with its NaN fixup, and the top-H seed) on
+    crafted root codebooks equal the oracle's cluster ids, small codes and errors bit for bit."""
+    X, C0, Cs, h = _crafted_roots(variant)
+    Hb = 4
+    print(f"crafted roots {variant} root_mode={root_mode} n={X.shape[0]} h={h} beam={Hb}", flush=True)
+    ctx.set_large_root(C0, Cs, h)
+    cid_g, Bs_g, err_g = ctx.beam_search_large_root(X, Hb, root_mode=root_mode)
+    with np.errstate(all="ignore"):
+        norm0, Gs, G0S = orc.build_precomp_large_root(C0, Cs)
+    nx2 = orc.xnorm2(X)
+    xs = orc.gemm_xc(Cs, X, mode=1)
+    cid_o, Bs_o, err_o = orc.beam_search_large_root(X, nx2, C0, norm0, xs, Gs, G0S, h, Hb, root_mode=root_mode)
+    assert np.array_equal(cid_o, cid_g), (variant, np.nonzero(cid_o != cid_g)[0][:10])
+    assert np.array_equal(Bs_o, Bs_g)
+    # IEEE 754 leaves the sign and payload of a generated NaN to the platform (x86 SSE: 0xFFC00000,
+    # CDNA: 0x7FC00000), so NaN errors match as NaN; every other error bit for bit.
+    nan_o, nan_g = np.isnan(err_o), np.isnan(err_g)
+    assert np.array_equal(nan_o, nan_g)
+    assert np.array_equal(_bits(err_o)[~nan_o], _bits(err_g)[~nan_g])
+    if variant == "ties":
+        assert not np.isin(cid_g, [5, 77, 200]).any()  # zero roots never enter
+        if root_mode == 1:  # one slot: a later duplicate never displaces the first
+            assert not np.isin(cid_g, [11, 50, 120, 299]).any() and np.any(cid_g == 10)
+    if variant == "nan" and root_mode == 1:
+        assert np.all(cid_g > 250)  # the NaN entered at 250 and the next root replaced it
+
+
 @pytest.mark.parametrize("chunk", [700, 2500])
 def test_stream_large_root_u8_matches_in_memory(ctx, chunk):
     """Streaming large-root encode of uint8 chunks (EncodeBaseStreaming's u8 path) equals the

@@ -290,3 +290,131 @@ def test_ils_never_worse_and_shard_invariant(orc):
     # ils_iters = 0 is the plain ICM
     k2, _, c2, _ = orc.icm_ils(xC, G, inv, h, nx2, codes, 2, 0, 3, True, 9)
     assert np.array_equal(k2, k0) and np.array_equal(c2.view(np.uint32), c0.view(np.uint32))
+
+
+# ---------------------------------------------------------------------------------------------
+# Root scan of the large-root beam (beam_search.cpp:686-705; RecomputeWorst :101-113). Roots are
+# scaled unit vectors s e_j with s a power of two and x has small integer entries, so every
+# quantity of the scan is exact in fp32: gamma = s x_j, a0 = x_j / s, e = |x|^2 - x_j^2, r00 = s.
+
+def _unit_roots(spec, d):
+    """spec: list of (axis, scale) -> C0 rows (scale 0: a zero root)."""
+    C0 = np.zeros((len(spec), d), np.float32)
+    for c, (j, s) in enumerate(spec):
+        C0[c, j] = s
+    return C0
+
+
+def _scan(orc, x, C0, H, root_mode=0, norm0=None, forced=None):
+    X = np.asarray(x, np.float32)[None, :]
+    nx2 = orc.xnorm2(X)
+    if norm0 is None:
+        norm0 = np.sum(C0.astype(np.float64) ** 2, axis=1).astype(np.float32)
+    fr = None if forced is None else np.array([forced], np.uint32)
+    e, c, a0, r00 = orc.large_root_candidates(X, nx2, C0, norm0, H, forced_root=fr, root_mode=root_mode)
+    return e[0], c[0], a0[0], r00[0]
+
+
+X_ROOT = [3.0, 1.0, 2.0, 0.0]  # |x|^2 = 14; a root on axis 0/1/2/3 leaves 5/13/10/14
+
+
+def test_root_scan_duplicates_lower_code_wins(orc):
+    """Equal errors never displace a kept root (the e >= worst skip), so among duplicates the
+    lowest code is kept; with two slots, the replaced slot is the first one holding the worst."""
+    C0 = _unit_roots([(1, 1.0), (0, 2.0), (2, 1.0), (0, 4.0), (0, 2.0)], 4)  # errors 13, 5, 10, 5, 5
+    e, c, a0, r00 = _scan(orc, X_ROOT, C0, 1, root_mode=1)
+    assert (c[0], e[0], a0[0], r00[0]) == (1, 5.0, 1.5, 2.0)
+    e, c, a0, r00 = _scan(orc, X_ROOT, C0, 2)
+    # slots: [13,inf] -> [13,5] -> [10,5] -> [5(code 3),5(code 1)]; code 4 (5 >= 5) is skipped
+    assert list(c) == [3, 1] and list(e) == [5.0, 5.0] and list(a0) == [0.75, 1.5] and list(r00) == [4.0, 2.0]
+    # equal errors in both slots: a better root replaces slot 0, evicting code 0 and keeping code 1
+    x = [2.0, 1.0, 3.0, 0.0]  # |x|^2 = 14: errors 10, 10, 5
+    e, c, _, _ = _scan(orc, x, _unit_roots([(0, 1.0), (0, 2.0), (2, 1.0)], 4), 2)
+    assert list(c) == [2, 1] and list(e) == [5.0, 10.0]
+
+
+def test_root_scan_zero_norm_roots_are_skipped(orc):
+    """alpha == 0 roots never enter (their 0/0 would be NaN), also under a forced root; with
+    every root zero, all slots keep the initial (+inf, code 0, 0, 0)."""
+    C0 = _unit_roots([(1, 1.0), (0, 0.0), (2, 1.0)], 4)  # the zero root would otherwise be free
+    e, c, _, _ = _scan(orc, X_ROOT, C0, 1, root_mode=1)
+    assert (c[0], e[0]) == (2, 10.0)
+    e, c, a0, r00 = _scan(orc, X_ROOT, _unit_roots([(0, 0.0)] * 3, 4), 2)
+    assert np.all(np.isinf(e)) and not c.any() and not a0.any() and not r00.any()
+    e, c, _, _ = _scan(orc, X_ROOT, C0, 2, forced=1)
+    assert np.isinf(e[0]) and np.isinf(e[1])
+    e, c, a0, r00 = _scan(orc, X_ROOT, C0, 2, forced=2)
+    assert (c[0], e[0], a0[0], r00[0]) == (2, 10.0, 2.0, 1.0) and np.isinf(e[1])
+
+
+def test_root_scan_nan_root_enters_and_is_replaced(orc):
+    """A NaN error passes the e >= worst skip, so it enters; RecomputeWorst's e > we never selects
+    it unless it sits in slot 0, where it is the worst and the next root replaces it. Elsewhere
+    it stays. norm0 is handed in, so a NaN norm gives the NaN error."""
+    C0 = _unit_roots([(1, 1.0), (0, 1.0), (2, 1.0), (0, 1.0)], 4)  # errors 13, 5, NaN, 5
+    norm0 = np.array([1.0, 1.0, np.nan, 1.0], np.float32)
+    e, c, _, _ = _scan(orc, X_ROOT, C0, 1, root_mode=1, norm0=norm0)
+    assert (c[0], e[0]) == (3, 5.0)  # NaN replaced code 1, then code 3 (5 >= NaN is false) replaced it
+    C0 = _unit_roots([(0, 1.0), (1, 1.0), (2, 1.0), (2, 1.0), (3, 2.0)], 4)  # errors 5, 13, NaN, 10, 14
+    norm0 = np.array([1.0, 1.0, np.nan, 1.0, 4.0], np.float32)
+    X2 = [2.0, 1.0, 2.0, 3.0]  # |x|^2 = 18: errors 14, 17, NaN, 14, 9
+    e, c, _, _ = _scan(orc, X2, C0, 2, norm0=norm0)
+    # [14,inf] -> [14,17] -> [14,NaN] (worst slot 1 held 17) -> code 3 (14 >= 14) skipped ->
+    # code 4 (9 < 14) takes slot 0; the NaN in slot 1 is never the worst again
+    assert c[0] == 4 and e[0] == 9.0 and c[1] == 2 and np.isnan(e[1])
+
+
+def test_root_scan_keeps_h_smallest_errors(orc):
+    """Without NaN the kept errors are the H smallest errors (a strict-improvement top-H), each
+    with its own code; which of several equal errors survives depends on the slot order (the
+    first slot holding the worst is replaced, so an equal later code can outlive an earlier one).
+    Brute force over many ties."""
+    rng = np.random.default_rng(21)
+    d, h0 = 5, 40
+    for trial in range(60):
+        axes = rng.integers(0, d, h0)
+        scales = 2.0 ** rng.integers(-2, 3, h0)
+        scales[rng.random(h0) < 0.1] = 0.0
+        C0 = _unit_roots(list(zip(axes, scales)), d)
+        x = rng.integers(-3, 4, d).astype(np.float32)
+        H = int(rng.integers(1, 9))
+        e, c, _, _ = _scan(orc, x, C0, H)
+        err = np.array([np.sum(x ** 2) - x[j] ** 2 if s else np.inf for j, s in zip(axes, scales)])
+        live = [k for k in range(h0) if scales[k] != 0.0]
+        want = sorted(err[k] for k in live)[:H]
+        kept = [(int(k), float(ek)) for k, ek in zip(c, e) if np.isfinite(ek)]
+        assert sorted(ek for _, ek in kept) == want, (trial, kept, want)
+        assert len({k for k, _ in kept}) == len(kept)
+        for k, ek in kept:
+            assert scales[k] != 0.0 and ek == err[k]
+
+
+def test_precomp_large_root_exact_on_integers(orc):
+    """Integer codebooks: every sum is exact in fp32, so norm0, G_small and G0S equal the integer
+    products whatever the summation order; d = 37 exercises the 4-lane tail. Pins the layouts
+    (G0S[flat, root] = <C_small[flat], C0[root]>, G_small symmetric)."""
+    rng = np.random.default_rng(5)
+    d, h0, Hs = 37, 23, 19
+    C0 = rng.integers(-8, 9, (h0, d)).astype(np.float32)
+    Cs = rng.integers(-8, 9, (Hs, d)).astype(np.float32)
+    norm0, Gs, G0S = orc.build_precomp_large_root(C0, Cs)
+    C0i, Csi = C0.astype(np.int64), Cs.astype(np.int64)
+    assert np.array_equal(norm0.astype(np.int64), np.sum(C0i * C0i, axis=1))
+    assert np.array_equal(Gs.astype(np.int64), Csi @ Csi.T)
+    assert np.array_equal(G0S.astype(np.int64), Csi @ C0i.T)
+
+
+def test_precomp_large_root_fp64_bound(orc):
+    """Random codebooks: each entry within the fp32 dot-product bound gamma_d sum |a_i b_i| of the
+    fp64 product (Higham Thm 3.1)."""
+    rng = np.random.default_rng(6)
+    d, h0, Hs = 96, 50, 40
+    C0 = rng.standard_normal((h0, d)).astype(np.float32)
+    Cs = (rng.standard_normal((Hs, d)) * 0.3).astype(np.float32)
+    norm0, Gs, G0S = orc.build_precomp_large_root(C0, Cs)
+    gam = d * 2.0 ** -24 / (1 - d * 2.0 ** -24)
+    A0, As = C0.astype(np.float64), Cs.astype(np.float64)
+    for got, exact, mag in ((norm0, np.sum(A0 * A0, 1), np.sum(A0 * A0, 1)),
+                            (Gs, As @ As.T, np.abs(As) @ np.abs(As).T),
+                            (G0S, As @ A0.T, np.abs(As) @ np.abs(A0).T)):
+        assert np.all(np.abs(got.astype(np.float64) - exact) <= gam * mag)
