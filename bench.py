@@ -30,40 +30,90 @@ sys.path.insert(0, ROOT)
 
 PEAK_HBM_GBS = 8000.0
 PEAK_FP32_MFMA_TFLOPS = 157.3
+# VALU issue ceiling: a wave64 fp32 VALU instruction occupies one 16-lane SIMD for 4 cycles; 4 SIMDs
+# per CU, 256 CUs, 2.4 GHz peak engine clock. With packed fp32 disabled this is the vector fp32
+# rate of 78.6 TFLOP/s (FMA), half of the packed 157.3.
+PEAK_VALU_WAVE_INSTS = 256 * 4 * 2.4e9 / 4
 
 
 def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def _profiled_traffic(kernel: str):
-    """HBM bytes per launch of `kernel` from the committed rocprofv3 summary of this workload
-    (FETCH_SIZE/WRITE_SIZE calibrated against a plain copy kernel), or None when it has no row."""
-    path = os.path.join(ROOT, "profiles", "c2_encode_hbm_traffic.md")
+def _profile_table(name: str):
+    """Rows of the first markdown table in profiles/<name> as {kernel: {column: value}}."""
+    path = os.path.join(ROOT, "profiles", name)
+    rows, head = {}, None
     try:
         with open(path) as f:
             for line in f:
+                if not line.startswith("|"):
+                    if head is not None and rows:
+                        break
+                    continue
                 cells = [c.strip() for c in line.strip().strip("|").split("|")]
-                if len(cells) == 5 and cells[0] == kernel:
-                    return (float(cells[3]) + float(cells[4])) * 1e9, os.path.relpath(path, ROOT)
-    except (OSError, ValueError):
-        pass
-    return None, None
+                if head is None:
+                    head = cells
+                elif not set(cells[0]) <= set("-: "):
+                    rows[cells[0]] = dict(zip(head[1:], cells[1:]))
+    except OSError:
+        return {}, None
+    return rows, os.path.relpath(path, ROOT)
 
 
-def _profiled_valu(kernel: str):
+def _profiled_traffic(kernel: str, stem: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary
+    of this workload (calibrated against a plain copy kernel), or (None, None)."""
+    rows, src = _profile_table(f"{stem}_hbm_traffic.md")
+    try:
+        r = rows[kernel]
+        return (float(r["read GB"]) + float(r["write GB"])) * 1e9, src
+    except (KeyError, ValueError):
+        return None, None
+
+
+def _profiled_valu(kernel: str, stem: str):
     """VALU and SALU wave instructions per launch of `kernel` from the committed rocprofv3 SQ
     counter summary of this workload, or (None, None, None)."""
-    path = os.path.join(ROOT, "profiles", "c2_encode_sq_counters.md")
+    rows, src = _profile_table(f"{stem}_sq_counters.md")
     try:
-        with open(path) as f:
-            for line in f:
-                cells = [c.strip() for c in line.strip().strip("|").split("|")]
-                if len(cells) == 8 and cells[0] == kernel:
-                    return float(cells[1]), float(cells[2]), os.path.relpath(path, ROOT)
-    except (OSError, ValueError):
-        pass
-    return None, None, None
+        r = rows[kernel]
+        return float(r["INSTS_VALU"]), float(r["INSTS_SALU"]), src
+    except (KeyError, ValueError):
+        return None, None, None
+
+
+def _roofline_valu(kernel: str, valu, avg_ms, src):
+    """The VALU-issue roofline of `kernel`: its SQ_INSTS_VALU per launch (committed profile of the
+    same workload) over this run's average launch time, against PEAK_VALU_WAVE_INSTS."""
+    rate = valu / (avg_ms * 1e-3) if valu and avg_ms > 0 else None
+    return {"kernel": kernel, "bound": "valu", "achieved": rate, "peak": PEAK_VALU_WAVE_INSTS,
+            "unit": "wave-instructions/s", "frac": rate / PEAK_VALU_WAVE_INSTS if rate else None,
+            "valu_wave_insts_per_launch": valu, "avg_launch_ms": avg_ms, "valu_source": src}
+
+
+def _calib_copy(ctx, mb: int):
+    """A plain device copy of mb MiB (DevCopyKernel) whose FETCH_SIZE/WRITE_SIZE readings scale the
+    counters of the profiled kernels to bytes."""
+    if mb <= 0:
+        return
+    nb = mb * (1 << 20)
+    a_ = ctx.dev_alloc(nb)
+    b_ = ctx.dev_alloc(nb)
+    ctx.lib.stlq_mi355_dev_copy_kernel(ctx.h, a_, b_, nb)
+    ctx.synchronize()
+    ctx.dev_free(a_)
+    ctx.dev_free(b_)
+    log(f"calibration copy of {mb} MiB done")
+
+
+def _layer_kernel_name(L: int, lr: bool) -> str:
+    """The profiled name of the beam layer kernel that runs layer L (full codebook, best-first
+    pass): the survivor-queue kernel for layers 3..8, the per-parent kernel otherwise."""
+    b = "true" if lr else "false"
+    if 3 <= L <= 8:
+        return f"LayerKernel<{L}, {b}, true, true>"
+    return f"LayerKernelDeep<{L}, {b}, true, true>"
 
 
 def _cpu_model() -> str:
@@ -149,15 +199,7 @@ def main():
     codes = ctx.d2h(np.empty((n, w.m), np.uint8), dcodes)
     cost = ctx.d2h(np.empty(n, np.float32), dcost)
 
-    if args.calib_copy_mb > 0:
-        nb = args.calib_copy_mb * (1 << 20)
-        a_ = ctx.dev_alloc(nb)
-        b_ = ctx.dev_alloc(nb)
-        ctx.lib.stlq_mi355_dev_copy_kernel(ctx.h, a_, b_, nb)
-        ctx.synchronize()
-        ctx.dev_free(a_)
-        ctx.dev_free(b_)
-        log(f"calibration copy of {args.calib_copy_mb} MiB done")
+    _calib_copy(ctx, args.calib_copy_mb)
 
     steps = max(args.steps, 1)
     ms_per_step = wall * 1000.0 / steps
@@ -181,11 +223,10 @@ def main():
     }
 
     # the timed layer kernel: full codebook, best-first pass (the default beam order)
-    prof_kernel = f"LayerKernel<{last}, false, true, true>"
-    traffic, traffic_src = (_profiled_traffic(prof_kernel) if args.config == "C2"
-                            else (None, None))
-    valu, salu, valu_src = (_profiled_valu(prof_kernel) if args.config == "C2"
-                            else (None, None, None))
+    prof_kernel = _layer_kernel_name(last, lr=False)
+    stem = f"{args.config.lower()}_encode"
+    traffic, traffic_src = _profiled_traffic(prof_kernel, stem)
+    valu, salu, valu_src = _profiled_valu(prof_kernel, stem)
     metric = ("vectors encoded/sec (d=128,M=8,K=256,B=16)" if args.config == "C2" else
               f"vectors encoded/sec (d={d},M={M},K={K},B={B}" + (f",ICM={w.icm_iters})" if w.icm_iters else ")"))
     workload = {
@@ -223,14 +264,11 @@ def main():
             "traffic_source": traffic_src,
             "algorithmic_bytes_per_launch": sel_bytes,
             "avg_launch_ms": avg_last_ms,
-            # What bounds this kernel instead: VALU issue (exact fp32 candidate arithmetic and the
-            # top-H replay); wave instructions per launch from the SQ counters, rate at this run's
-            # launch time.
-            "valu_wave_insts_per_launch": valu,
-            "salu_wave_insts_per_launch": salu,
-            "valu_wave_insts_per_s": (valu / (avg_last_ms * 1e-3)) if valu else None,
-            "valu_source": valu_src,
         },
+        # What bounds this kernel instead: VALU issue (the pruning test, the exact fp32 candidate
+        # arithmetic of the survivors and the top-H replay).
+        "roofline_valu": dict(_roofline_valu(prof_kernel, valu, avg_last_ms, valu_src),
+                              salu_wave_insts_per_launch=salu),
         "roofline_distance": {
             "kernel": "xC GEMM (GemmXcKernel, fp32 MFMA, lookup form)",
             "bound": "mfma",
@@ -354,7 +392,13 @@ def bench_stream_large_root(args, w):
         if k < count:
             out[k:] = pool[:count - k]
 
+    t_prog = [time.perf_counter(), 0]
+
     def sink(first, count, res):
+        t_prog[1] += 1
+        if time.perf_counter() - t_prog[0] > 20.0:
+            log(f"stream progress: {first + count} vectors written ({t_prog[1]} chunks)")
+            t_prog[0] = time.perf_counter()
         if first == 0:
             first_codes["cid"] = res["cluster_id"][:keep].copy()
             first_codes["Bs"] = res["B_small"][:keep].copy()
@@ -365,10 +409,12 @@ def bench_stream_large_root(args, w):
     ctx.encode_stream(warm, warm, cfg, fill, sink, input_u8=True, large_root=True, root_mode=1)
     log("warmup stream done")
     t_start = time.perf_counter()
+    t_prog[0] = t_start
     st = ctx.encode_stream(n, chunk, cfg, fill, sink, input_u8=True, large_root=True, root_mode=1)
     wall = time.perf_counter() - t_start
     t = ctx.last_timings()
     log(f"streamed {n} vectors in {wall:.2f}s ({st.chunks} chunks)")
+    _calib_copy(ctx, args.calib_copy_mb)
     M = w.m
     last = M - 1
     layer_ms = np.array(t.layer_ms[:20])
@@ -377,6 +423,9 @@ def bench_stream_large_root(args, w):
     sel_bytes = 4.0 * w.K * w.H_beam * chunk
     beam_ach = sel_bytes / (avg_last_ms * 1e-3) / 1e9
     h2d_gbs = st.h2d_bytes / (st.h2d_ms * 1e-3) / 1e9 if st.h2d_ms > 0 else None
+    prof_kernel = _layer_kernel_name(last, lr=True)
+    traffic, traffic_src = _profiled_traffic(prof_kernel, "c5_stream")
+    valu, _, valu_src = _profiled_valu(prof_kernel, "c5_stream")
     out = {
         "metric": "vectors encoded/sec (stream, d=128 uint8, forced nearest root h0=65536 + 16x256, B=32)",
         "value": n / wall,
@@ -396,16 +445,18 @@ def bench_stream_large_root(args, w):
                    "name": "C5", "n": n, "chunk": chunk, "d": w.d, "h0": h0, "M_small": M - 1, "K": w.K,
                    "H_beam": w.H_beam},
         "roofline": {
-            "kernel": f"large-root beam layer L={last} (LayerKernel<{last}, large root>)",
+            "kernel": f"large-root beam layer L={last} ({prof_kernel})",
             "bound": "hbm",
             "achieved": beam_ach,
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
             "frac": beam_ach / PEAK_HBM_GBS,
-            "traffic": None,
+            "traffic": traffic,
+            "traffic_source": traffic_src,
             "algorithmic_bytes_per_launch": sel_bytes,
             "avg_launch_ms": avg_last_ms,
         },
+        "roofline_valu": _roofline_valu(prof_kernel, valu, avg_last_ms, valu_src),
         "streaming": {
             "h2d_GBps": h2d_gbs,
             "h2d_bytes": st.h2d_bytes,

@@ -332,13 +332,15 @@ __device__ __forceinline__ int BestSlot(float err, int curH, int lane) {
 }
 
 // Record layout of one beam slot (dword offsets); stride dwords per slot:
-// [err, R column by column, coef[m], codes, root id, kap, phi, kb, cq, padding to 16 bytes].
+// [err, R column by column, coef[m], codes, root id, kap, phi, kb, cq, (nf2, k1, k2 when a layer
+// of the encode uses the diagonal split), padding to 16 bytes].
 // Column c of the Cholesky factor holds R(0..c, c) followed by RN(1/R(c,c)) (formed once when the
 // slot is made), so the first L columns sit at offsets that depend on L only and a layer-L kernel
-// reads them with immediate offsets. kap, phi, kb and cq are the slot's pruning constants
-// (prune_bound.hpp).
+// reads them with immediate offsets. kap, phi, kb, cq, nf2, k1 and k2 are the slot's pruning
+// constants (prune_bound.hpp).
 struct Rec {
-    int coef, code, root, kap, phi, kb, cq, stride;
+    int coef, code, root, kap, phi, kb, cq, nf2, k1, k2, stride;
+    bool diag;
     __host__ __device__ explicit Rec(int m) {
         coef = 1 + m * (m + 3) / 2;
         code = coef + m;
@@ -347,14 +349,28 @@ struct Rec {
         phi = root + 2;
         kb = root + 3;
         cq = root + 4;
-        stride = (root + 5 + 3) & ~3;
+        // the diagonal split's constants only where a layer uses it
+        diag = m - 1 >= prune::kDiagMinL;
+        nf2 = root + 5;
+        k1 = root + 6;
+        k2 = root + 7;
+        stride = (root + (diag ? 8 : 5) + 3) & ~3;
     }
     __device__ void PutBounds(float* rec, const prune::SlotBounds& b) const {
         rec[kap] = b.kap;
         rec[phi] = b.phi;
         rec[kb] = b.kb;
         rec[cq] = b.cq;
+        if (diag) {
+            float c1, c2;
+            prune::DiagConsts(b, c1, c2);
+            rec[nf2] = b.nf2;
+            rec[k1] = c1;
+            rec[k2] = c2;
+        }
     }
+    // nF2 of a stored slot (0 where the record carries none: the split is never used below it)
+    __device__ float Nf2(const float* rec) const { return diag ? rec[nf2] : 0.0f; }
     __host__ __device__ static constexpr int R(int r, int c) { return 1 + c * (c + 3) / 2 + r; }
     __host__ __device__ static constexpr int Rinv(int c) { return 1 + c * (c + 3) / 2 + c + 1; }
 };
@@ -398,10 +414,17 @@ __device__ __forceinline__ bool DiagFastOk(float d) { return d >= 0x1p-20f && d 
 // MODE 0: IEEE division; 1: Markstein quotient with reciprocal table `rinv` (clears `safe` when
 // a numerator leaves the exact range);
 // 2: reciprocal multiply (large-root semantics).
-template <int L, int MODE, typename RFn>
-__device__ __forceinline__ void EvalCand(RFn R, const float (&rinv)[L], const float (&A)[L], const float (&aold)[L],
-                                         float E_old, float alpha, float gamma, float (&y)[L], float (&v)[L],
-                                         float& e, float& denom, float& a_last, bool& ok, bool& safe) {
+// Element i of an array or of an accessor (a callable taking the index).
+template <typename T>
+__device__ __forceinline__ float At(const T& x, int i) {
+    if constexpr (std::is_invocable_v<const T&, int>) return x(i);
+    else return x[i];
+}
+
+template <int L, int MODE, typename RFn, typename RiT, typename AoT>
+__device__ __forceinline__ void EvalCand(RFn R, const RiT& rinv, const float (&A)[L], const AoT& aold, float E_old,
+                                         float alpha, float gamma, float (&y)[L], float (&v)[L], float& e,
+                                         float& denom, float& a_last, bool& ok, bool& safe) {
     float lo = __builtin_huge_valf(), hi = 0.0f;
 #pragma unroll
     for (int r = 0; r < L; ++r) {
@@ -409,8 +432,8 @@ __device__ __forceinline__ void EvalCand(RFn R, const float (&rinv)[L], const fl
 #pragma unroll
         for (int j = 0; j < r; ++j) s = s - R(j, r) * y[j];
         if (MODE == 0) y[r] = s / R(r, r);
-        else if (MODE == 1) y[r] = QuotFast(s, R(r, r), rinv[r], lo, hi);
-        else y[r] = s * rinv[r];
+        else if (MODE == 1) y[r] = QuotFast(s, R(r, r), At(rinv, r), lo, hi);
+        else y[r] = s * At(rinv, r);
     }
 #pragma unroll
     for (int r = L - 1; r >= 0; --r) {
@@ -418,15 +441,70 @@ __device__ __forceinline__ void EvalCand(RFn R, const float (&rinv)[L], const fl
 #pragma unroll
         for (int j = r + 1; j < L; ++j) s = s - R(r, j) * v[j];
         if (MODE == 0) v[r] = s / R(r, r);
-        else if (MODE == 1) v[r] = QuotFast(s, R(r, r), rinv[r], lo, hi);
-        else v[r] = s * rinv[r];
+        else if (MODE == 1) v[r] = QuotFast(s, R(r, r), At(rinv, r), lo, hi);
+        else v[r] = s * At(rinv, r);
     }
     if (MODE == 1) safe = safe && (lo >= 0x1p-100f) && (hi <= 0x1p100f);
     float delta = 0.0f, eta = 0.0f;
 #pragma unroll
     for (int t = 0; t < L; ++t) {
         delta = delta + A[t] * v[t];
-        eta = eta + A[t] * aold[t];
+        eta = eta + A[t] * At(aold, t);
+    }
+    denom = alpha - delta;
+    ok = denom != 0.0f;
+    const float diff = gamma - eta;
+    a_last = diff / denom;
+    const float ee = E_old - diff * a_last;
+    e = ee < 0.0f ? 0.0f : ee;
+}
+
+// A zero that depends on `dep`: an address offset by it cannot be read before `dep` exists.
+__device__ __forceinline__ int ZeroAfter(float dep) {
+    int z;
+    asm("v_mov_b32 %0, 0" : "=v"(z) : "v"(dep));
+    return z;
+}
+
+// EvalCand with the slot's factor in LDS at f, laid out as the record from dword 1 (R(0..c, c) then
+// RN(1/R(c,c)) for c < L), followed by a_old. The same operations in the same order, so the same
+// bits. The reads of column r (forward) and row r (backward) wait for the quotient two steps back:
+// the compiler then keeps about two rows of the factor in registers instead of all of it.
+template <int L, int MODE>
+__device__ __forceinline__ void EvalStaged(const float* f, const float (&A)[L], float E_old, float alpha, float gamma,
+                                           float (&y)[L], float (&v)[L], float& e, float& denom, float& a_last,
+                                           bool& ok, bool& safe) {
+    constexpr int kRWords = L * (L + 3) / 2;
+    float lo = __builtin_huge_valf(), hi = 0.0f;
+#pragma unroll
+    for (int r = 0; r < L; ++r) {
+        const float* fr = r >= 2 ? f + ZeroAfter(y[r - 2]) : f;
+        float s = A[r];
+#pragma unroll
+        for (int j = 0; j < r; ++j) s = s - fr[Rec::R(j, r) - 1] * y[j];
+        const float d = fr[Rec::R(r, r) - 1];
+        if (MODE == 0) y[r] = s / d;
+        else if (MODE == 1) y[r] = QuotFast(s, d, fr[Rec::Rinv(r) - 1], lo, hi);
+        else y[r] = s * fr[Rec::Rinv(r) - 1];
+    }
+#pragma unroll
+    for (int r = L - 1; r >= 0; --r) {
+        const float* fr = f + ZeroAfter(r + 2 < L ? v[r + 2] : y[L - 1]);
+        float s = y[r];
+#pragma unroll
+        for (int j = r + 1; j < L; ++j) s = s - fr[Rec::R(r, j) - 1] * v[j];
+        const float d = fr[Rec::R(r, r) - 1];
+        if (MODE == 0) v[r] = s / d;
+        else if (MODE == 1) v[r] = QuotFast(s, d, fr[Rec::Rinv(r) - 1], lo, hi);
+        else v[r] = s * fr[Rec::Rinv(r) - 1];
+    }
+    if (MODE == 1) safe = safe && (lo >= 0x1p-100f) && (hi <= 0x1p100f);
+    const float* fa = f + ZeroAfter(v[0]);
+    float delta = 0.0f, eta = 0.0f;
+#pragma unroll
+    for (int t = 0; t < L; ++t) {
+        delta = delta + A[t] * v[t];
+        eta = eta + A[t] * fa[kRWords + t];
     }
     denom = alpha - delta;
     ok = denom != 0.0f;
@@ -539,7 +617,7 @@ __global__ __launch_bounds__(256) void Layer0Kernel(LayerArgs p) {
 //  * the other layers at the allocator's own choice.
 template <int L, bool LR, bool BEST>
 constexpr int LayerMinWaves() {
-    return L >= 11 ? (LR ? 5 : 4) : 1;
+    return L >= 11 ? (LR ? 5 : 4) : (L == 3 && !LR ? 7 : 1);  // layer 3: 72 VGPRs, one wave more than left alone
 }
 
 // Layers up to kVStateMaxL read the slot state into VGPRs (see process() in LayerKernel): on the
@@ -554,6 +632,10 @@ constexpr int kVStateMaxL = 3;
 constexpr int kQueueMinL = 3;
 constexpr int kQueueMaxL = 8;
 constexpr int kQueueCap = 128;  // ring capacity: at most 63 carried over plus one chunk of 64
+// Layers above kQueueMaxL run the staged kernel (pruned, factor in LDS) where its solves outweigh
+// its per-slot staging and bound; the large-root beam (32 slots in the streaming encode) keeps the
+// unpruned per-slot kernel below layer kLrStagedMinL, where that measured faster.
+constexpr int kLrStagedMinL = 14;
 
 // BEST: the best-first pass (LayerArgs::flags). Its input records are rank-indexed, so slots are
 // scanned in ascending error order, and so are its output records. A vector flagged by an earlier
@@ -620,6 +702,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LayerMinWav
         const float* rowb[L];
         const float* rows[L];
         float ahat[L];  // a_t * isw_t
+        float cdg[L];   // c_t of the diagonal split
         uint32_t root = 0;
 #pragma unroll
         for (int t = 0; t < L; ++t) {
@@ -637,9 +720,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LayerMinWav
                 isw_t = p.isw[f];
             }
             ahat[t] = rec[rc.coef + t] * isw_t;
+            cdg[t] = prune::DiagCoef(rec[Rec::Rinv(t)], isw_t);
         }
         const float sw0 = LR ? p.sw0[root] : 1.0f;
         const float kb = rec[rc.kb], cq = rec[rc.cq];
+        const float k1 = L >= prune::kDiagMinL ? rec[rc.k1] : 0.0f, k2 = L >= prune::kDiagMinL ? rec[rc.k2] : 0.0f;
 
         int next = 0;  // first chunk not yet listed
         while (next < nch) {
@@ -656,18 +741,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LayerMinWav
                 const bool act = FULL || k < K;
                 bool keep = act;
                 if (bounded) {
-                    // eta~ = sum_t b_t ahat_t and b2 = sum_t b_t^2 by fma, b_t = Gs(f_t, k)
-                    float et = 0.0f, b2 = 0.0f;
+                    // eta~ = sum_t b_t ahat_t, b2 = sum_t b_t^2 and X~ = sum_t (c_t b_t)^2 by fma,
+                    // b_t = Gs(f_t, k)
+                    float et = 0.0f, b2 = 0.0f, xs = 0.0f;
 #pragma unroll
                     for (int t = 0; t < L; ++t) {
                         float bt = act ? rows[t][static_cast<uint32_t>(k)] : 0.0f;
                         if (LR && t == 0) bt = bt * sw0;
                         et = t == 0 ? bt * ahat[t] : __builtin_fmaf(bt, ahat[t], et);
                         b2 = t == 0 ? bt * bt : __builtin_fmaf(bt, bt, b2);
+                        if (L >= prune::kDiagMinL) {
+                            const float ut = cdg[t] * bt;
+                            xs = t == 0 ? ut * ut : __builtin_fmaf(ut, ut, xs);
+                        }
                     }
                     const float alc = (act ? p.gdiag[offL + k] : 0.0f) * prune::kAlphaScale;
                     const float gm = act ? xCi[offL + k] : 0.0f;
-                    keep = act && !prune::Prunable(alc, b2, gm - et, kb, cq, gp);
+                    keep = act && !(L >= prune::kDiagMinL ? prune::Prunable2(alc, b2, xs, gm - et, kb, k1, k2, cq, gp)
+                                                   : prune::Prunable(alc, b2, gm - et, kb, cq, gp));
                 }
                 const uint64_t km = Ballot(keep);
                 if (keep) pack[total + __popcll(km & ((1ull << lane) - 1ull))] = k;
@@ -793,10 +884,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LayerMinWav
             const float* rec = recs_in + h * rc.stride;
             const float E_old = rec[0];
             const float kb = rec[rc.kb], cq = rec[rc.cq];
+        const float k1 = L >= prune::kDiagMinL ? rec[rc.k1] : 0.0f, k2 = L >= prune::kDiagMinL ? rec[rc.k2] : 0.0f;
             // Gs rows of the slot's prefix codewords (the large root's prefix 0: G0S(root, .),
-            // scaled by sw0[root]) and ahat_t = a_t * isw_t.
+            // scaled by sw0[root]), ahat_t = a_t * isw_t and the diagonal split's c_t.
             const float* rows[L];
-            float ahat[L];
+            float ahat[L], cdg[L];
             float sw0 = 1.0f;
 #pragma unroll
             for (int t = 0; t < L; ++t) {
@@ -814,20 +906,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LayerMinWav
                     isw_t = p.isw[f];
                 }
                 ahat[t] = rec[rc.coef + t] * isw_t;
+                cdg[t] = prune::DiagCoef(rec[Rec::Rinv(t)], isw_t);
             }
             // Whether chunk j's candidate survives the bound (true when it may enter the top-H).
             auto keep_of = [&](int j, float gp) -> bool {
                 const uint32_t k = static_cast<uint32_t>(lane + kWave * j);
                 const bool act = FULL || static_cast<int>(k) < K;
-                float et = 0.0f, b2 = 0.0f;
+                float et = 0.0f, b2 = 0.0f, xs = 0.0f;
 #pragma unroll
                 for (int t = 0; t < L; ++t) {
                     float bt = act ? rows[t][k] : 0.0f;
                     if (LR && t == 0) bt = bt * sw0;
                     et = t == 0 ? bt * ahat[t] : __builtin_fmaf(bt, ahat[t], et);
                     b2 = t == 0 ? bt * bt : __builtin_fmaf(bt, bt, b2);
+                    if (L >= prune::kDiagMinL) {
+                        const float ut = cdg[t] * bt;
+                        xs = t == 0 ? ut * ut : __builtin_fmaf(ut, ut, xs);
+                    }
                 }
-                return act && !prune::Prunable(alc[j], b2, gam[j] - et, kb, cq, gp);
+                return act && !(L >= prune::kDiagMinL ? prune::Prunable2(alc[j], b2, xs, gam[j] - et, kb, k1, k2, cq, gp)
+                                               : prune::Prunable(alc[j], b2, gam[j] - et, kb, cq, gp));
             };
             auto enqueue = [&](int j, bool keep) -> bool {
                 const uint64_t km = Ballot(keep);
@@ -1020,7 +1118,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LayerMinWav
             ro[Rec::Rinv(L)] = 1.0f / rLL;
             put_codes(true, knew, root);
             auto swf = [&](int t) { return (LR && t == 0) ? p.sw0[fl[t]] : p.sw[fl[t]]; };
-            rc.PutBounds(ro, prune::NextBounds<L>(y, v, rLL, swf, p.sw[offL + knew], ri[rc.kap], ri[rc.phi], asq));
+            rc.PutBounds(ro, prune::NextBounds<L>(y, v, rLL, swf, p.sw[offL + knew], ri[rc.kap], ri[rc.phi], rc.Nf2(ri),
+                                                  asq));
         } else if (lane < Hb) {
             ro[0] = kInfF;  // an empty slot: never read by the next layer
         }
@@ -1052,12 +1151,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LayerMinWav
     }
 }
 
-// Layers outside kQueueMinL..kQueueMaxL (the shallow layers, where a candidate's solve is little
-// more than its bound, and the deep layers of the M=16 and large-root encodes): every candidate of
+// Layers 1-2, and the large-root beam's layers kQueueMaxL+1 .. kLrStagedMinL-1 (where a candidate's
+// solve costs little more than its bound and the staging of the pruned kernels): every candidate of
 // every slot is evaluated exactly, four chunks of 64 at a time with the slot's factor in SGPRs, and
-// the slots are written back by the lanes that hold them, with their pruning constants while a
-// later layer runs the queue scan. LR selects the large-root cross-term source and
-// reciprocal solves.
+// the slots are written back by the lanes that hold them, with their pruning constants for the
+// later layers. LR selects the large-root cross-term source and reciprocal solves.
 // FULL: the layer has exactly 256 codewords (no partial chunk).
 // Minimum waves per SIMD requested from the register allocator, per layer (measured):
 //  * layers >= 11 at 4 waves (<= 128 VGPRs), 5 for the large root: left alone the allocator
@@ -1235,7 +1333,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DeepMinWave
     int outH;
     float out_err = kInfF;
     // pruning constants of the new slots, while a later layer runs the queue scan
-    constexpr bool kNextQueued = L + 1 <= kQueueMaxL;
+    constexpr bool kNextQueued = true;  // every later layer prunes
     prune::SlotBounds out_bd = prune::NoBounds();
     uint8_t ncode[L + 1];
     uint32_t nroot = 0;
@@ -1343,7 +1441,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DeepMinWave
                 auto swf = [&](int t) {
                     return (LR && t == 0) ? p.sw0[nroot] : p.sw[p.gram.off[t] + ncode[t]];
                 };
-                out_bd = prune::NextBounds<L>(y, v, rLL, swf, p.sw[offL + k], ri[rc.kap], ri[rc.phi], asq);
+                out_bd =
+                    prune::NextBounds<L>(y, v, rLL, swf, p.sw[offL + k], ri[rc.kap], ri[rc.phi], rc.Nf2(ri), asq);
             }
         }
     }
@@ -1531,6 +1630,438 @@ __global__ __launch_bounds__(256) void NearestRootFixupKernel(const float* __res
     }
 }
 
+// Layers above kQueueMaxL (the deep layers of the M=16 and large-root encodes). Per slot of the
+// beam, the candidates are bound-tested chunk by chunk (prune_bound.hpp) and the survivors listed
+// in ascending code order, then solved 64 at a time with the slot's factor, 1/diag and
+// coefficients staged once in the wave's LDS. Every lane reads the same LDS address, so the
+// solves' products take VGPR operands and the factor holds no registers (a factor in SGPRs or
+// VGPRs would outgrow the register files from layer 11 on). The new slots are written back with
+// the parents' factor columns copied by the whole wave, coalesced, and each new column solved by
+// the lane that owns the slot, reading its parent's factor from memory.
+template <int L>
+constexpr int StagedWords() {
+    return L * (L + 3) / 2 + L;  // R(0..c, c) and 1/R(c,c) for c < L (record dwords 1..), then a_old
+}
+constexpr int kWbSlots = 8;  // slots whose new column is solved per write-back round
+template <int L>
+constexpr int WbStride() {
+    return StagedWords<L>() | 1;  // odd: the lanes of a round read distinct banks
+}
+template <int L>
+constexpr int StagedWaveWords() {
+    return kMaxK + StagedWords<L>() + 2 * L > kWbSlots * WbStride<L>() ? kMaxK + StagedWords<L>() + 2 * L
+                                                                      : kWbSlots * WbStride<L>();
+}
+
+// Waves per SIMD asked of the register allocator: the kernel needs about 5L + 60 VGPRs, so 4 waves
+// (128) hold it without spills up to layer 12, 3 waves (168) up to layer 18.
+template <int L>
+constexpr int StagedMinWaves() {
+    return L <= 12 ? 4 : 3;
+}
+
+template <int L, bool LR, bool FULL, bool BEST>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(StagedMinWaves<L>(), 8))) void LayerKernelStaged(
+    LayerArgs p) {
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    int64_t i, w;
+    if (!WaveItem(p, wave, i, w)) return;
+    const int m = p.m, Hb = p.Hb, K = FULL ? kMaxK : p.K, offL = p.offL;
+    const Rec rc(m);
+    const int ld = p.gram.ld;
+    const float* xCi = p.xC + i * p.ldx;
+    const int nch = FULL ? kMaxChunks : (K + kWave - 1) / kWave;
+    const float* __restrict__ recs_in = p.in.rec + w * Hb * rc.stride;
+    float* __restrict__ recs_out = p.out.rec + w * Hb * rc.stride;
+    const bool prune_on = p.prune != 0;
+
+    // Per codeword of the layer: gamma = <x, c_k> and fl(alpha (1 - 2^-20)) for the pruning bound.
+    float gam[kMaxChunks], alc[kMaxChunks];
+#pragma unroll
+    for (int j = 0; j < kMaxChunks; ++j) {
+        const int k = lane + kWave * j;
+        const bool act = FULL || (j < nch && k < K);
+        gam[j] = act ? xCi[offL + k] : 0.0f;
+        alc[j] = (act ? p.gdiag[offL + k] : 0.0f) * prune::kAlphaScale;
+    }
+
+    const int curH = p.in.curH[w];
+    // Beam slot h's codes (and root) sit in lane h.
+    constexpr int kCodeWords = (L + 3) / 4;
+    uint32_t cw[kCodeWords];
+    uint32_t rootw = 0;
+    {
+        const uint32_t* rl = reinterpret_cast<const uint32_t*>(recs_in + (lane < curH ? lane : 0) * rc.stride);
+#pragma unroll
+        for (int q = 0; q < kCodeWords; ++q) cw[q] = rl[rc.code + q];
+        if (LR) rootw = rl[rc.root];
+    }
+    constexpr int kRWords = L * (L + 3) / 2;
+    // Per wave: the survivor list and the staged factor during the scan, the write-back's staged
+    // factors after it.
+    __shared__ float s_wave[kBeamWavesPerBlock][StagedWaveWords<L>()];
+    float* __restrict__ wbuf = s_wave[wave];
+    int* __restrict__ pack = reinterpret_cast<int*>(wbuf);
+    float* __restrict__ fac = wbuf + kMaxK;
+    float* __restrict__ cf = fac + StagedWords<L>();  // per slot: ahat[L], then c[L]
+
+    // Evaluates slot h's candidates and replays them into the top-H (scan order: slot, then code).
+    // Returns false when the replay asks for the slow pass. While a slot of the top-H is still
+    // empty the chunks are listed one at a time without a bound, so the worst can become finite
+    // after each; after that every chunk is bound-tested against the worst of that moment.
+    auto process = [&](int h, auto&& replay, auto slow_tag, auto&& worst_now) -> bool {
+        constexpr bool kSlow = decltype(slow_tag)::value;
+        const float* rec = recs_in + h * rc.stride;
+        const float E_old = rec[0];
+        // Element offsets of the slot's prefix rows in G (and Gs, same layout); the large root's
+        // prefix 0 reads G0S(root, .), scaled by sw0[root] in the bound. ahat_t = a_t * isw_t.
+        uint32_t rowo[L];
+        const float* row0 = nullptr;
+        float sw0 = 1.0f;
+        uint32_t root = 0;
+#pragma unroll
+        for (int t = 0; t < L; ++t) {
+            if (LR && t == 0) {
+                root = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(rootw), h));
+                row0 = p.gram.G0S + static_cast<int64_t>(root) * ld + offL;
+                rowo[0] = 0;
+                sw0 = p.sw0[root];
+            } else {
+                const uint32_t word = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(cw[t >> 2]), h));
+                const uint32_t f = static_cast<uint32_t>(p.gram.off[t]) + ((word >> (8 * (t & 3))) & 0xFFu);
+                rowo[t] = f * static_cast<uint32_t>(ld) + static_cast<uint32_t>(offL);
+            }
+        }
+        // ahat_t = a_t * isw_t and the diagonal split's c_t, formed by lane t into the wave's LDS
+        // and read back by all lanes at one address (no registers held across the slot).
+        {
+            uint32_t wsel = 0;
+            int offl = 0;
+#pragma unroll
+            for (int q = 0; q < kCodeWords; ++q) {
+                const uint32_t wq = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(cw[q]), h));
+                if ((lane >> 2) == q) wsel = wq;
+            }
+#pragma unroll
+            for (int t = 0; t < L; ++t) {
+                if (lane == t) offl = p.gram.off[t];
+            }
+            if (lane < L) {
+                const int t = lane;
+                const float isw_t = (LR && t == 0) ? p.isw0[root]
+                                                   : p.isw[offl + static_cast<int>((wsel >> (8 * (t & 3))) & 0xFFu)];
+                cf[t] = rec[rc.coef + t] * isw_t;
+                cf[L + t] = prune::DiagCoef(rec[Rec::Rinv(t)], isw_t);
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        }
+        // 32-bit byte offsets from one base (H <= 5120, so H * ld * 4 < 2^32): the loads take the
+        // scalar-base form with one VGPR offset instead of a 64-bit address per row.
+        auto ld32 = [](const float* base, uint32_t elem) {
+            return *reinterpret_cast<const float*>(reinterpret_cast<const char*>(base) + (elem << 2));
+        };
+        auto gv = [&](int t, uint32_t k) { return (LR && t == 0) ? ld32(row0, k) : ld32(p.gram.G, rowo[t] + k); };
+        auto gs = [&](int t, uint32_t k) { return (LR && t == 0) ? ld32(row0, k) * sw0 : ld32(p.Gs, rowo[t] + k); };
+        const float kb = rec[rc.kb], cq = rec[rc.cq];
+        const float k1 = L >= prune::kDiagMinL ? rec[rc.k1] : 0.0f, k2 = L >= prune::kDiagMinL ? rec[rc.k2] : 0.0f;
+
+        bool staged = false, diag_fast = false;
+        int next = 0;  // first chunk not yet listed
+        while (next < nch) {
+            float gp = 0.0f;
+            const float W = worst_now();
+            const bool bounded = !kSlow && prune_on && kb < kInfF && prune::ParentGap(E_old, W, gp);
+            const bool filling = !kSlow && prune_on && !(W < kInfF);
+            const int last = (bounded || !filling) ? nch : next + 1;
+            int total = 0;
+            // Whether candidate (this slot, lane + 64 j) survives the bound: eta~ = sum_t b_t ahat_t,
+            // b2 = sum_t b_t^2 and X~ = sum_t (c_t b_t)^2 by fma, b_t = Gs(f_t, k).
+            auto keep_of = [&](int j, float alj, float gmj) -> bool {
+                const uint32_t k = static_cast<uint32_t>(lane + kWave * j);
+                const bool act = FULL || static_cast<int>(k) < K;
+                float et = 0.0f, b2 = 0.0f, xs = 0.0f;
+#pragma unroll
+                for (int t = 0; t < L; ++t) {
+                    const float bt = act ? gs(t, k) : 0.0f;
+                    const float ut = cf[L + t] * bt;
+                    et = t == 0 ? bt * cf[t] : __builtin_fmaf(bt, cf[t], et);
+                    b2 = t == 0 ? bt * bt : __builtin_fmaf(bt, bt, b2);
+                    xs = t == 0 ? ut * ut : __builtin_fmaf(ut, ut, xs);
+                }
+                return act && !prune::Prunable2(alj, b2, xs, gmj - et, kb, k1, k2, cq, gp);
+            };
+            auto list = [&](int j, bool keep) {
+                const uint64_t km = Ballot(keep);
+                if (keep) pack[total + __popcll(km & ((1ull << lane) - 1ull))] = lane + kWave * j;
+                total += __popcll(km);
+            };
+            {
+#pragma unroll 1
+                for (int j = next; j < last; ++j) {
+                    bool keep = FULL || lane + kWave * j < K;
+                    if (bounded) {
+                        float alj = 0.0f, gmj = 0.0f;
+#pragma unroll
+                        for (int jj = 0; jj < kMaxChunks; ++jj) {
+                            if (jj == j) {
+                                alj = alc[jj];
+                                gmj = gam[jj];
+                            }
+                        }
+                        keep = keep_of(j, alj, gmj);
+                    }
+                    list(j, keep);
+                }
+            }
+            next = last;
+            if (total == 0) continue;
+            if (!staged) {
+                // the slot's factor columns with 1/diag (record dwords 1..kRWords) and coefficients
+#pragma unroll
+                for (int q0 = 0; q0 < kRWords; q0 += kWave) {
+                    if (q0 + lane < kRWords) fac[q0 + lane] = rec[1 + q0 + lane];
+                }
+                if (lane < L) fac[kRWords + lane] = rec[rc.coef + lane];
+                staged = true;
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                bool diag_ok = true;
+#pragma unroll
+                for (int r = 0; r < L; ++r) diag_ok = diag_ok && DiagFastOk(fac[Rec::R(r, r) - 1]);
+                diag_fast = !LR && diag_ok;
+            } else {
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            }
+            for (int b = 0; b < total; b += kWave) {
+                const int idx = b + lane;
+                const bool act = idx < total;
+                const uint32_t k = static_cast<uint32_t>(act ? pack[idx] : 0);
+                float A[L];
+#pragma unroll
+                for (int t = 0; t < L; ++t) A[t] = gv(t, k);
+                const float alpha = p.gdiag[offL + k];
+                const float gamma = xCi[offL + k];
+                float y[L], v[L], denom, a_last, e;
+                bool ok, safe = true;
+                if (LR) {
+                    EvalStaged<L, 2>(fac, A, E_old, alpha, gamma, y, v, e, denom, a_last, ok, safe);
+                } else {
+                    bool ieee = kSlow || !diag_fast;
+                    if (!ieee) {
+                        EvalStaged<L, 1>(fac, A, E_old, alpha, gamma, y, v, e, denom, a_last, ok, safe);
+                        ieee = Ballot(!safe) != 0ull;
+                    }
+                    if (ieee) EvalStaged<L, 0>(fac, A, E_old, alpha, gamma, y, v, e, denom, a_last, ok, safe);
+                }
+                if (!replay(ok && act, e, h * K + static_cast<int>(k))) return false;
+            }
+        }
+        return true;
+    };
+
+    float s_err;
+    int s_cand;
+    bool flagged = false;
+    SelectTopH<true, BEST, BEST>(  // errors clamped at zero (EvalCand)
+        Hb, lane,
+        [&](auto&& replay, auto slow_tag, auto&& worst_now) {
+            for (int h = 0; h < curH; ++h) {
+                if (!process(h, replay, slow_tag, worst_now)) return false;
+            }
+            return true;
+        },
+        s_err, s_cand, flagged);
+    if (BEST && flagged) {
+        // No records: the next layers see an empty beam (curH = 0), do no work for this vector
+        // and keep it well-formed until its re-run.
+        if (lane == 0) {
+            p.flags[i] = 1;
+            p.out.curH[w] = 0;
+        }
+        return;
+    }
+
+    // Deferred write-back (beam_search.cpp:337-383; the large root :896-947) or the all-skipped
+    // fallback (:385-400, :949-966), as in LayerKernel.
+    const bool live = lane < Hb && !(s_err >= kInfF);
+    const int newH = __popcll(Ballot(lane < Hb && s_err < kInfF));
+    const int outH = newH == 0 ? max(1, min(curH, Hb)) : newH;  // CountFinite and max(1, .)
+    if (lane == 0) p.out.curH[w] = outH;
+    float out_err = kInfF;
+    int src = -1, knew = 0;
+    if (newH == 0) {
+        if (lane < min(curH, Hb)) {
+            src = lane;
+            out_err = recs_in[lane * rc.stride];
+        }
+    } else if (live) {
+        src = s_cand / K;
+        knew = s_cand - src * K;
+        out_err = s_err;
+    }
+    if (!p.is_last) {
+        float* ro = recs_out + lane * rc.stride;
+        const float* ri = recs_in + (src < 0 ? 0 : src) * rc.stride;
+        auto put_codes = [&](bool from_parent, int kc, uint32_t root) {
+            uint32_t* cwo = reinterpret_cast<uint32_t*>(ro + rc.code);
+#pragma unroll
+            for (int qq = 0; qq <= L / 4; ++qq) {
+                uint32_t word = 0;
+#pragma unroll
+                for (int b = 0; b < 4; ++b) {
+                    const int t = 4 * qq + b;
+                    const uint32_t c = t < L ? (from_parent ? static_cast<uint32_t>(CodeAt(ri, rc.code, t)) : 0u)
+                                             : (t == L ? static_cast<uint32_t>(kc) : 0u);
+                    word |= c << (8 * b);
+                }
+                cwo[qq] = word;
+            }
+            reinterpret_cast<uint32_t*>(ro)[rc.root] = root;
+        };
+        if (newH == 0) {
+            const int nh = min(curH, Hb);
+            // the parents' factor columns 0..L-1 with 1/diag, copied by the whole wave
+            for (int q = 0; q < nh; ++q) {
+                const float* rs = recs_in + q * rc.stride + 1;
+                float* rd = recs_out + q * rc.stride + 1;
+#pragma unroll
+                for (int q0 = 0; q0 < kRWords; q0 += kWave) {
+                    if (q0 + lane < kRWords) rd[q0 + lane] = rs[q0 + lane];
+                }
+            }
+            if (lane < nh) {
+                // parent slot `lane` with a zero new column
+                ro[0] = ri[0];
+#pragma unroll
+                for (int t = 0; t < L; ++t) ro[rc.coef + t] = ri[rc.coef + t];
+                ro[rc.coef + L] = 0.0f;
+#pragma unroll
+                for (int r = 0; r < L; ++r) ro[Rec::R(r, L)] = 0.0f;
+                ro[Rec::R(L, L)] = 0.0f;
+                ro[Rec::Rinv(L)] = 1.0f / 0.0f;
+                put_codes(true, 0, reinterpret_cast<const uint32_t*>(ri)[rc.root]);
+                rc.PutBounds(ro, prune::NoBounds());
+            } else if (nh == 0 && lane == 0) {
+                // No beam at all (layer 0 had no finite candidate): the reference's next-buffer
+                // slot 0 keeps its never-written (zero) state with error +inf.
+                ro[0] = kInfF;
+#pragma unroll
+                for (int t = 0; t <= L; ++t) ro[rc.coef + t] = 0.0f;
+#pragma unroll
+                for (int r = 0; r <= L; ++r) {
+#pragma unroll
+                    for (int c = r; c <= L; ++c) ro[Rec::R(r, c)] = 0.0f;
+                    ro[Rec::Rinv(r)] = 1.0f / 0.0f;
+                }
+                put_codes(false, 0, 0u);
+                rc.PutBounds(ro, prune::NoBounds());
+            }
+        } else {
+            // In rounds of kWbSlots slots: the whole wave copies each slot's parent factor columns
+            // 0..L-1 (with 1/diag) into the new record and stages them with the parent's
+            // coefficients in LDS; then each slot's lane solves its chosen candidate once more
+            // with the reference's arithmetic (IEEE division, or the large root's reciprocal
+            // multiply) for the new coefficients, Cholesky column and bounds.
+            for (int q0 = 0; q0 < Hb; q0 += kWbSlots) {
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                const int qn = min(Hb - q0, kWbSlots);
+                for (int q = 0; q < qn; ++q) {
+                    const int sq = __builtin_amdgcn_readlane(src, q0 + q);
+                    if (sq < 0) continue;
+                    const float* rs = recs_in + sq * rc.stride;
+                    float* rd = recs_out + (q0 + q) * rc.stride + 1;
+                    float* st = wbuf + q * WbStride<L>();
+#pragma unroll
+                    for (int c0 = 0; c0 < kRWords + L; c0 += kWave) {
+                        const int c = c0 + lane;
+                        if (c < kRWords) {
+                            const float x = rs[1 + c];
+                            rd[c] = x;
+                            st[c] = x;
+                        } else if (c < kRWords + L) {
+                            st[c] = rs[rc.coef + (c - kRWords)];
+                        }
+                    }
+                }
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                if (live && lane >= q0 && lane < q0 + qn) {
+                    const float* st = wbuf + (lane - q0) * WbStride<L>();
+                    const uint32_t root = reinterpret_cast<const uint32_t*>(ri)[rc.root];
+                    float A[L];
+                    int fl[L];  // flat index of each prefix codeword (the root for a large root's prefix 0)
+#pragma unroll
+                    for (int t = 0; t < L; ++t) {
+                        fl[t] = (LR && t == 0) ? static_cast<int>(root) : p.gram.off[t] + CodeAt(ri, rc.code, t);
+                        const float* row = (LR && t == 0) ? p.gram.G0S + static_cast<int64_t>(root) * ld + offL
+                                                          : p.gram.G + static_cast<int64_t>(fl[t]) * ld + offL;
+                        A[t] = row[knew];
+                    }
+                    float y[L], v[L], e, denom, a_last;
+                    bool ok, unused = true;
+                    if (LR) {
+                        EvalStaged<L, 2>(st, A, ri[0], p.gdiag[offL + knew], xCi[offL + knew], y, v, e, denom, a_last,
+                                         ok, unused);
+                    } else {
+                        EvalStaged<L, 0>(st, A, ri[0], p.gdiag[offL + knew], xCi[offL + knew], y, v, e, denom, a_last,
+                                         ok, unused);
+                    }
+                    ro[0] = s_err;
+                    double asq = 0.0;  // ||ahat||^2 of the new coefficients
+#pragma unroll
+                    for (int t = 0; t <= L; ++t) {
+                        const float at = t < L ? st[kRWords + t] - v[t] * a_last : a_last;
+                        ro[rc.coef + t] = at;
+                        const float iswt =
+                            t < L ? ((LR && t == 0) ? p.isw0[fl[t]] : p.isw[fl[t]]) : p.isw[offL + knew];
+                        const double ah = static_cast<double>(at) * static_cast<double>(iswt);
+                        asq += ah * ah;
+                    }
+#pragma unroll
+                    for (int r = 0; r < L; ++r) ro[Rec::R(r, L)] = y[r];
+                    const float rLL = sqrtf(denom);
+                    ro[Rec::R(L, L)] = rLL;
+                    ro[Rec::Rinv(L)] = 1.0f / rLL;
+                    put_codes(true, knew, root);
+                    auto swf = [&](int t) { return (LR && t == 0) ? p.sw0[fl[t]] : p.sw[fl[t]]; };
+                    rc.PutBounds(ro, prune::NextBounds<L>(y, v, rLL, swf, p.sw[offL + knew], ri[rc.kap], ri[rc.phi],
+                                                          rc.Nf2(ri), asq));
+                }
+            }
+            if (!live && lane < Hb) ro[0] = kInfF;  // an empty slot: never read by the next layer
+        }
+        return;
+    }
+
+    // Last layer: the final pick (beam_search.cpp:409-419) over the slots the write-back would
+    // build; with no finite candidate (the fallback) those are the parent slots with code 0.
+    if (BEST && FinalTie(out_err, outH)) {
+        if (lane == 0) p.flags[i] = 1;
+        return;
+    }
+    const int best = BestSlot(out_err, outH, lane);
+    if (lane == best) {
+        // src < 0: no beam at all (the reference's never-written slot 0: codes 0, error +inf)
+        const float* ri = recs_in + (src < 0 ? 0 : src) * rc.stride;
+        const uint32_t root = src < 0 ? 0u : reinterpret_cast<const uint32_t*>(ri)[rc.root];
+        if (LR) {
+            p.cluster_out[i] = root;
+#pragma unroll
+            for (int t = 1; t < L; ++t) p.codes_out[i * (m - 1) + (t - 1)] = src < 0 ? 0 : CodeAt(ri, rc.code, t);
+            p.codes_out[i * (m - 1) + (L - 1)] = static_cast<uint8_t>(knew);
+        } else {
+#pragma unroll
+            for (int t = 0; t < L; ++t) p.codes_out[i * m + t] = src < 0 ? 0 : CodeAt(ri, rc.code, t);
+            p.codes_out[i * m + L] = static_cast<uint8_t>(knew);
+        }
+        if (p.best_err) p.best_err[i] = out_err;
+    }
+}
+
 template <int L, template <int, bool, bool, bool> class KernelSel>
 hipError_t LaunchWith(bool lr, const LayerArgs& a, hipStream_t s) {
     const unsigned blocks = static_cast<unsigned>((a.n + kBeamWavesPerBlock - 1) / kBeamWavesPerBlock);
@@ -1559,10 +2090,22 @@ struct DeepSel {
     static constexpr auto kernel = LayerKernelDeep<L, LR, FULL, BEST>;
 };
 
+template <int L, bool LR, bool FULL, bool BEST>
+struct StagedSel {
+    static constexpr auto kernel = LayerKernelStaged<L, LR, FULL, BEST>;
+};
+
 template <int L>
 hipError_t LaunchL(bool lr, const LayerArgs& a, hipStream_t s) {
-    if constexpr (L >= kQueueMinL && L <= kQueueMaxL) return LaunchWith<L, QueueSel>(lr, a, s);
-    else return LaunchWith<L, DeepSel>(lr, a, s);
+    if constexpr (L < kQueueMinL) {
+        return LaunchWith<L, DeepSel>(lr, a, s);
+    } else if constexpr (L <= kQueueMaxL) {
+        return LaunchWith<L, QueueSel>(lr, a, s);
+    } else if constexpr (L < kLrStagedMinL) {
+        return lr ? LaunchWith<L, DeepSel>(true, a, s) : LaunchWith<L, StagedSel>(false, a, s);
+    } else {
+        return LaunchWith<L, StagedSel>(lr, a, s);
+    }
 }
 
 }  // namespace

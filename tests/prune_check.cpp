@@ -26,6 +26,7 @@ using stlq_mi355::prune::NextBounds;
 using stlq_mi355::prune::NoBounds;
 using stlq_mi355::prune::ParentGap;
 using stlq_mi355::prune::Prunable;
+using stlq_mi355::prune::Prunable2;
 using stlq_mi355::prune::SlotBounds;
 
 namespace {
@@ -83,20 +84,29 @@ int FirstMax(const std::vector<float>& e, int Hb, float& worst) {
 }
 
 // The device's test for candidate k of slot s at threshold W (prune_bound.hpp).
-bool DeviceTest(const Slot& s, int L, const float* Gs, const float* sw, const float* isw, const int* off, int H,
+bool DeviceTest(const Slot& s, int L, int m, const float* Gs, const float* sw, const float* isw, const int* off, int H,
                 int fk, float alpha, float gamma, float W) {
     float gp = 0.0f;
     if (!(s.bd.kb < kInf) || !ParentGap(s.err, W, gp)) return false;
-    float et = 0.0f, b2 = 0.0f;
+    float et = 0.0f, b2 = 0.0f, xs = 0.0f;
     for (int t = 0; t < L; ++t) {
         const int f = off[t] + s.code[t];
         const float bt = Gs[static_cast<int64_t>(f) * H + fk];
         const float ah = s.a[t] * isw[f];
+        // c_t from the slot's RN(1/R_tt), as the device stores it
+        const float ut = stlq_mi355::prune::DiagCoef(1.0f / s.R[t * m + t], isw[f]) * bt;
         et = t == 0 ? bt * ah : std::fma(bt, ah, et);
         b2 = t == 0 ? bt * bt : std::fma(bt, bt, b2);
+        xs = t == 0 ? ut * ut : std::fma(ut, ut, xs);
     }
     (void)sw;
-    return Prunable(alpha * stlq_mi355::prune::kAlphaScale, b2, gamma - et, s.bd.kb, s.bd.cq, gp);
+    const float alc = alpha * stlq_mi355::prune::kAlphaScale;
+    if (L >= stlq_mi355::prune::kDiagMinL) {
+        float k1, k2;
+        stlq_mi355::prune::DiagConsts(s.bd, k1, k2);
+        return Prunable2(alc, b2, xs, gamma - et, s.bd.kb, k1, k2, s.bd.cq, gp);
+    }
+    return Prunable(alc, b2, gamma - et, s.bd.kb, s.bd.cq, gp);
 }
 
 }  // namespace
@@ -174,7 +184,7 @@ int prune_check(const float* G, const float* xC, const float* nx2, int H, int m,
                         for (int t = 0; t < L; ++t) A[t] = G[static_cast<int64_t>(fk) * H + off[t] + s.code[t]];
                         float ec, dn, al;
                         const bool elig = EvalRef(s, L, m, A.data(), gd[fk], xc[fk], y.data(), v.data(), ec, dn, al);
-                        const bool pruned = DeviceTest(s, L, Gs.data(), sw.data(), isw.data(), off.data(), H, fk,
+                        const bool pruned = DeviceTest(s, L, m, Gs.data(), sw.data(), isw.data(), off.data(), H, fk,
                                                        gd[fk], xc[fk], W0);
                         if (pass == 0) {
                             ++st.candidates;
@@ -185,7 +195,7 @@ int prune_check(const float* G, const float* xC, const float* nx2, int H, int m,
                             }
                             // at its own error the test must keep the candidate
                             if (elig && std::isfinite(ec) &&
-                                DeviceTest(s, L, Gs.data(), sw.data(), isw.data(), off.data(), H, fk, gd[fk], xc[fk],
+                                DeviceTest(s, L, m, Gs.data(), sw.data(), isw.data(), off.data(), H, fk, gd[fk], xc[fk],
                                            ec))
                                 ++st.self_kept_fail;
                         }
@@ -247,7 +257,7 @@ int prune_check(const float* G, const float* xC, const float* nx2, int H, int m,
             ya[t] = yy[t];                                                                                      \
             va[t] = vv[t];                                                                                      \
         }                                                                                                       \
-        s.bd = NextBounds<LL>(ya, va, s.R[L * m + L], swf, swL, src.bd.kap, src.bd.phi, asq);                   \
+        s.bd = NextBounds<LL>(ya, va, s.R[L * m + L], swf, swL, src.bd.kap, src.bd.phi, src.bd.nf2, asq);                   \
         break;                                                                                                  \
     }
                             STLQ_NB(1) STLQ_NB(2) STLQ_NB(3) STLQ_NB(4) STLQ_NB(5) STLQ_NB(6) STLQ_NB(7) STLQ_NB(8)
