@@ -208,6 +208,8 @@ typedef struct stlq_mi355_chunk_out {
     const uint32_t* cluster_id; /* large root: count */
     const uint8_t* B_small;     /* large root: (m-1) x count */
     const float* best_err;      /* large root: count */
+    const void* input;          /* the chunk's input as fill wrote it (d x count, uint8 with input_u8,
+                                   else float; before any rotation), valid during the sink call */
 } stlq_mi355_chunk_out;
 
 /* first: the global id (start_id + offset in the stream) of the chunk's first vector. */

@@ -217,3 +217,71 @@ def icm_large_root(X, C0, norm0, G_small, G0S, invs, h_vec, xC_small, cluster_id
                              _p(cid, _u32p), icm_iters, ils_iters, perturb_k, int(bool(use_abs)), seed & 0xFFFFFFFF,
                              int(sample_id_offset), _p(Bs, _u8p), _p(a, _f32p), _p(cost, _f32p))
     return Bs, a, cost
+
+
+def _store_lib():
+    L = lib()
+    if not getattr(L, "_store_declared", False):
+        _u64p = ctypes.POINTER(ctypes.c_uint64)
+        _i64p = ctypes.POINTER(ctypes.c_int64)
+        L.ref_store_write.argtypes = [ctypes.c_char_p, _int, _int, _i32p, _int, _int, _int, _int, _int, _int, _int,
+                                      _int, ctypes.c_uint64, _u64p, _int, _int, _u64p, _i64p, _u32p, _u8p, _f32p,
+                                      _int, ctypes.c_void_p, ctypes.c_char_p, _u64p, ctypes.c_char_p, _int]
+        L.ref_store_write.restype = _int
+        L.ref_store_truncate.argtypes = [ctypes.c_char_p, _int, _i32p, _int, _int, _int, ctypes.c_char_p, _u64p,
+                                         _u64p, _int, ctypes.POINTER(_int), ctypes.c_char_p, _int]
+        L.ref_store_truncate.restype = _int
+        L._store_declared = True
+    return L
+
+
+def store_write(dir, d, m, h_vec, blocks, raw_kind=0, shard_size=2000000, bucket_size=256, bucket_flush_mb=256,
+                write_vector_bucket=True, write_basic_to_bucket=True, raw_bytes_per_vec=0, resume_start=None,
+                bucket_sizes=None, ckpt_path=None):
+    """Writes a store with the reference's io::BaseBasicWriter. blocks: list of
+    (start_id, cluster_id (n,), B_small (n, m-1), a (n, m), raw (n, d) or None). raw_kind 0 AppendBlock
+    without vectors, 1 AppendBlockRawU8, 2 AppendBlockRawF32, 3 AppendBlock with a uint8 matrix.
+    resume_start (with bucket_sizes) opens with OpenResume; ckpt_path commits after every block.
+    Returns (ok, err, bucket_file_bytes)."""
+    L = _store_lib()
+    hv = _c(h_vec, np.int32)
+    starts = np.array([b[0] for b in blocks], dtype=np.uint64)
+    counts = np.array([len(b[1]) for b in blocks], dtype=np.int64)
+    cid = _c(np.concatenate([np.asarray(b[1], np.uint32) for b in blocks]) if blocks else np.zeros(0), np.uint32)
+    mc = max(0, m - 1)
+    Bs = _c(np.concatenate([np.asarray(b[2], np.uint8).reshape(len(b[1]), mc) for b in blocks]) if blocks
+            else np.zeros((0, mc)), np.uint8)
+    A = _c(np.concatenate([np.asarray(b[3], np.float32).reshape(len(b[1]), m) for b in blocks]) if blocks
+           else np.zeros((0, m)), np.float32)
+    raw = None
+    if blocks and blocks[0][4] is not None:
+        raw = np.ascontiguousarray(np.concatenate([np.asarray(b[4]) for b in blocks]))
+    h0 = int(hv[0]) if len(hv) else 0
+    nlayout = (h0 + max(1, bucket_size) - 1) // max(1, bucket_size) if h0 > 0 else 0
+    # A fresh Open ignores bucket_sizes; their count then only caps the bucket bytes read back.
+    sizes = _c(bucket_sizes if resume_start is not None else np.zeros(max(nlayout, 1)), np.uint64)
+    out = np.zeros(len(sizes), np.uint64)
+    err = ctypes.create_string_buffer(512)
+    _u64p = ctypes.POINTER(ctypes.c_uint64)
+    ok = L.ref_store_write(dir.encode(), d, m, _p(hv, _i32p), len(hv), shard_size, bucket_size, bucket_flush_mb,
+                           int(bool(write_vector_bucket)), int(bool(write_basic_to_bucket)), raw_bytes_per_vec,
+                           int(resume_start is not None), int(resume_start or 0), _p(sizes, _u64p), len(sizes),
+                           len(blocks), _p(starts, _u64p), _p(counts, ctypes.POINTER(ctypes.c_int64)),
+                           _p(cid, _u32p), _p(Bs, _u8p), _p(A, _f32p), raw_kind,
+                           None if raw is None else raw.ctypes.data_as(ctypes.c_void_p),
+                           ckpt_path.encode() if ckpt_path else None, _p(out, _u64p), err, 512)
+    return bool(ok), err.value.decode(), out[:nlayout]
+
+
+def store_truncate(dir, m, h_vec, ckpt_path, shard_size=2000000, bucket_size=256):
+    """app::ReadBaseBasicCheckpoint + app::TruncateBaseBasicToCheckpoint; returns (ok, err, next_id, sizes)."""
+    L = _store_lib()
+    hv = _c(h_vec, np.int32)
+    nid = ctypes.c_uint64()
+    sizes = np.zeros(1 << 16, np.uint64)
+    nb = ctypes.c_int()
+    err = ctypes.create_string_buffer(512)
+    ok = L.ref_store_truncate(dir.encode(), m, _p(hv, _i32p), len(hv), shard_size, bucket_size, ckpt_path.encode(),
+                              ctypes.byref(nid), _p(sizes, ctypes.POINTER(ctypes.c_uint64)), len(sizes),
+                              ctypes.byref(nb), err, 512)
+    return bool(ok), err.value.decode(), int(nid.value), sizes[:nb.value].copy()

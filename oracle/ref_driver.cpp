@@ -5,7 +5,8 @@
 //
 // Compiled with the reference's translation units
 //   src/quantizer/beam_search.cpp, linear_algebra.cpp, cost_utils.cpp, least_squares.cpp,
-//   icm.cpp, src/common/timer.cpp, logger.cpp
+//   icm.cpp, src/common/timer.cpp, logger.cpp, src/io/base_store.cpp (the BaseBasicStore writer)
+//   and src/pipeline/main_virtual_helpers.cpp (its checkpoint helpers)
 // and linked against the image's MKL runtime for LAPACK spotrf_/spotrs_ (least_squares.cpp).
 // blas.cpp is not buildable here (it includes cblas.h, which the image lacks), so GemmRaw and
 // BlasSetThreads stay unresolved. They are only reached from the root-score GEMM of
@@ -14,6 +15,7 @@
 //
 // Array conventions (all column-major as in the reference's ColMajorMatrix):
 //   X d x n, xC H x n, G H x H, codes m x n (uint8), a m x n.
+#include <algorithm>
 #include <cstdint>
 #include <cstring>
 #include <vector>
@@ -24,6 +26,10 @@
 #include "stlq/quantizer/icm.h"
 #include "stlq/quantizer/least_squares.h"
 #include "stlq/quantizer/precomp_large_root.h"
+#include "stlq/io/base_store.h"
+#include "stlq/pipeline/main_virtual_helpers.h"
+
+#include <string>
 
 namespace {
 
@@ -239,6 +245,113 @@ void ref_icm_large_root(const float* X, int d, int n, const float* C0, const flo
     std::memcpy(B_small, Bs.data.data(), Bs.data.size());
     std::memcpy(a, am.data.data(), sizeof(float) * am.data.size());
     std::memcpy(cost, cst.data(), sizeof(float) * cst.size());
+}
+
+
+// Writes a store with the reference's io::BaseBasicWriter (src/io/base_store.cpp): Open (or, with
+// resume, OpenResume at resume_start with the given committed bucket sizes), then one append per
+// block (block b: vectors off_b .. off_b + counts[b] - 1 of the concatenated arrays, global ids
+// from starts[b]) by the variant raw_kind selects (0 AppendBlock without vectors, 1
+// AppendBlockRawU8, 2 AppendBlockRawF32, 3 AppendBlock with a d x count uint8 matrix), each
+// followed, when ckpt_path is set, by the pipeline's commit (writer Flush, then
+// app::OnCommitBaseBasicCkpt with next id = block end). Close at the end. Returns 1, or 0 with
+// the reference's message in err; out_bucket_bytes (nbucket entries) gets bucket_file_bytes().
+int ref_store_write(const char* dir, int d, int m, const int* h_vec, int h_len, int shard_size, int bucket_size,
+                    int flush_mb, int wvb, int wbb, int raw_bytes, int resume, uint64_t resume_start,
+                    const uint64_t* bucket_sizes, int nbucket, int nblocks, const uint64_t* starts,
+                    const int64_t* counts, const uint32_t* cluster_id, const uint8_t* B_small, const float* a,
+                    int raw_kind, const void* raw, const char* ckpt_path, uint64_t* out_bucket_bytes, char* err,
+                    int err_len) {
+    stlq::io::BaseBasicStoreConfig cfg;
+    cfg.dir = dir;
+    cfg.d = d;
+    cfg.m = m;
+    cfg.h_vec.assign(h_vec, h_vec + h_len);
+    cfg.shard_size = shard_size;
+    cfg.bucket_size = bucket_size;
+    cfg.bucket_flush_mb = flush_mb;
+    cfg.write_vector_bucket = wvb != 0;
+    cfg.write_basic_to_bucket = wbb != 0;
+    cfg.raw_bytes_per_vec = raw_bytes;
+    std::string e;
+    auto done = [&](int ok) {
+        if (err && err_len > 0) {
+            std::strncpy(err, e.c_str(), static_cast<std::size_t>(err_len) - 1);
+            err[err_len - 1] = 0;
+        }
+        return ok;
+    };
+    stlq::io::BaseBasicWriter w;
+    const bool opened = resume ? w.OpenResume(cfg, resume_start,
+                                              std::vector<std::uint64_t>(bucket_sizes, bucket_sizes + nbucket), &e)
+                               : w.Open(cfg, &e);
+    if (!opened) return done(0);
+    stlq::app::BaseBasicCkptCtx hook;
+    if (ckpt_path) {
+        hook.path = ckpt_path;
+        hook.nbucket = static_cast<std::uint32_t>(stlq::app::ComputeNbucketsForBasic(cfg));
+    }
+    const int mc = std::max(0, m - 1);
+    const std::size_t esz = raw_kind == 2 ? sizeof(float) : 1;
+    std::size_t off = 0;
+    for (int b = 0; b < nblocks; ++b) {
+        const int cnt = static_cast<int>(counts[b]);
+        const std::vector<std::uint32_t> cid(cluster_id + off, cluster_id + off + cnt);
+        const auto Bs = Wrap(B_small ? B_small + off * mc : nullptr, mc, cnt);
+        const auto am = Wrap(a + off * m, m, cnt);
+        const auto* rp = raw ? static_cast<const std::uint8_t*>(raw) + off * static_cast<std::size_t>(d) * esz : nullptr;
+        bool ok = false;
+        if (raw_kind == 1) {
+            ok = w.AppendBlockRawU8(starts[b], cid, Bs, am, rp, d, &e);
+        } else if (raw_kind == 2) {
+            ok = w.AppendBlockRawF32(starts[b], cid, Bs, am, reinterpret_cast<const float*>(rp), d, &e);
+        } else if (raw_kind == 3) {
+            const auto xm = Wrap(rp, d, cnt);
+            ok = w.AppendBlock(starts[b], cid, Bs, am, &xm, &e);
+        } else {
+            ok = w.AppendBlock(starts[b], cid, Bs, am, nullptr, &e);
+        }
+        if (!ok) return done(0);
+        if (ckpt_path) {
+            if (!w.Flush(&e)) return done(0);
+            if (!stlq::app::OnCommitBaseBasicCkpt(starts[b] + static_cast<std::uint64_t>(cnt), &w, &hook, &e))
+                return done(0);
+        }
+        off += static_cast<std::size_t>(cnt);
+    }
+    if (!w.Close(&e)) return done(0);
+    if (out_bucket_bytes)
+        for (std::size_t i = 0; i < w.bucket_file_bytes().size() && static_cast<int>(i) < nbucket; ++i)
+            out_bucket_bytes[i] = w.bucket_file_bytes()[i];
+    return done(1);
+}
+
+// app::ReadBaseBasicCheckpoint + app::TruncateBaseBasicToCheckpoint
+// (src/pipeline/main_virtual_helpers.cpp:126-275): reads ckpt_path, cuts the store back to it and
+// returns the checkpoint's next id and bucket sizes (cap entries). Returns 1, or 0 with err.
+int ref_store_truncate(const char* dir, int m, const int* h_vec, int h_len, int shard_size, int bucket_size,
+                       const char* ckpt_path, uint64_t* next_id, uint64_t* bucket_sizes, int cap, int* nbucket,
+                       char* err, int err_len) {
+    stlq::io::BaseBasicStoreConfig cfg;
+    cfg.dir = dir;
+    cfg.m = m;
+    cfg.h_vec.assign(h_vec, h_vec + h_len);
+    cfg.shard_size = shard_size;
+    cfg.bucket_size = bucket_size;
+    std::string e;
+    stlq::app::BaseBasicCheckpoint ck;
+    bool ok = stlq::app::ReadBaseBasicCheckpoint(ckpt_path, &ck, &e) &&
+              stlq::app::TruncateBaseBasicToCheckpoint(dir, cfg, ck, &e);
+    if (ok) {
+        *next_id = ck.next_id;
+        *nbucket = static_cast<int>(ck.bucket_sizes.size());
+        for (int i = 0; i < cap && i < *nbucket; ++i) bucket_sizes[i] = ck.bucket_sizes[static_cast<std::size_t>(i)];
+    }
+    if (err && err_len > 0) {
+        std::strncpy(err, e.c_str(), static_cast<std::size_t>(err_len) - 1);
+        err[err_len - 1] = 0;
+    }
+    return ok ? 1 : 0;
 }
 
 }  // extern "C"

@@ -17,6 +17,7 @@ _i32p = ctypes.POINTER(ctypes.c_int)
 _u8p = ctypes.POINTER(ctypes.c_uint8)
 _u32p = ctypes.POINTER(ctypes.c_uint32)
 _i64p = ctypes.POINTER(ctypes.c_int64)
+_u64p = ctypes.POINTER(ctypes.c_uint64)
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
 _int = ctypes.c_int
@@ -71,6 +72,25 @@ class ChunkOut(ctypes.Structure):
         ("cluster_id", _u32p),
         ("B_small", _u8p),
         ("best_err", _f32p),
+        ("input", _vp),
+    ]
+
+
+class StoreConfig(ctypes.Structure):
+    """stlq_mi355_store_config (io::BaseBasicStoreConfig, include/stlq/io/base_store.h:12-25)."""
+
+    _fields_ = [
+        ("dir", ctypes.c_char_p),
+        ("d", ctypes.c_int),
+        ("m", ctypes.c_int),
+        ("h_vec", _i32p),
+        ("h_len", ctypes.c_int),
+        ("shard_size", ctypes.c_int),
+        ("bucket_size", ctypes.c_int),
+        ("bucket_flush_mb", ctypes.c_int),
+        ("write_vector_bucket", ctypes.c_int),
+        ("write_basic_to_bucket", ctypes.c_int),
+        ("raw_bytes_per_vec", ctypes.c_int),
     ]
 
 
@@ -126,6 +146,21 @@ SIGNATURES = {
     "stlq_mi355_synchronize": ([_vp], _int),
     "stlq_mi355_dev_copy_kernel": ([_vp, _vp, _vp, ctypes.c_size_t], _int),
     "stlq_mi355_device_info": ([_vp, ctypes.c_char_p, _int, _i32p], _int),
+    # include/stlq_mi355_store.h
+    "stlq_mi355_store_config_init": ([ctypes.POINTER(StoreConfig)], None),
+    "stlq_mi355_store_open": ([ctypes.POINTER(StoreConfig), ctypes.POINTER(_vp)], _int),
+    "stlq_mi355_store_open_resume": ([ctypes.POINTER(StoreConfig), ctypes.c_uint64, _u64p, _i64,
+                                      ctypes.POINTER(_vp)], _int),
+    "stlq_mi355_store_append": ([_vp, ctypes.c_uint64, _i64, _u32p, _int, _u8p, _int, _f32p, _int, _vp, _i64], _int),
+    "stlq_mi355_store_flush": ([_vp], _int),
+    "stlq_mi355_store_bucket_bytes": ([_vp, _u64p, _i64, _i64p], _int),
+    "stlq_mi355_store_info": ([_vp, _i32p, _i32p, _i32p, _i32p, _i32p], _int),
+    "stlq_mi355_store_close": ([_vp], _int),
+    "stlq_mi355_checkpoint_write": ([ctypes.c_char_p, ctypes.c_uint64, _u64p, _i64], _int),
+    "stlq_mi355_checkpoint_read": ([ctypes.c_char_p, _u64p, _u64p, _i64, _i64p], _int),
+    "stlq_mi355_store_truncate_to_checkpoint": ([ctypes.POINTER(StoreConfig), ctypes.c_uint64, _u64p, _i64], _int),
+    "stlq_mi355_encode_stream_store": ([_vp, _i64, _i64, ctypes.POINTER(StreamParams), FILL_FN, _vp, _vp,
+                                        ctypes.c_char_p, ctypes.POINTER(StreamStats)], _int),
 }
 
 _lib = None

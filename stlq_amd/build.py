@@ -24,6 +24,7 @@ LIB = os.path.join(LIBDIR, "libstlq_mi355.so")
 HOSTCHECK_SRC = os.path.join(ROOT, "tests", "host_mirror_check.cpp")
 HOSTCHECK = os.path.join(LIBDIR, "libstlq_mi355_hostcheck.so")
 SOURCES = ["k_precomp.hip", "k_gemm.hip", "k_beam.hip", "k_ls.hip", "capi.hip"]
+HOST_SOURCES = ["base_store.cpp"]  # plain host C++ (the on-disk store), built by the host compiler
 ARCH = "gfx950"
 
 
@@ -58,12 +59,28 @@ def _compile(src: str) -> str:
     return out
 
 
+def host_flags() -> list[str]:
+    return ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra",
+            f"-I{os.path.join(ROOT, 'include')}", f"-I{CSRC}"]
+
+
+def _compile_host(src: str) -> str:
+    out = os.path.join(OBJ, os.path.splitext(src)[0] + ".host.o")
+    cmd = [os.environ.get("CXX", "g++")] + host_flags() + ["-c", os.path.join(CSRC, src), "-o", out]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
+    return out
+
+
 def build(verbose: bool = False) -> str:
     os.makedirs(OBJ, exist_ok=True)
     os.makedirs(LIBDIR, exist_ok=True)
-    jobs = min(len(SOURCES), int(os.environ.get("MAX_JOBS", "8")))
+    jobs = min(len(SOURCES) + len(HOST_SOURCES), int(os.environ.get("MAX_JOBS", "8")))
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(_compile, SOURCES))
+        hip_objs = ex.map(_compile, SOURCES)
+        host_objs = ex.map(_compile_host, HOST_SOURCES)
+        objs = list(hip_objs) + list(host_objs)
     tmp = LIB + ".tmp"
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp] + objs
     res = subprocess.run(cmd, capture_output=True, text=True)

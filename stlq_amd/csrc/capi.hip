@@ -2,6 +2,8 @@
 // The reference routine each entry point replaces is named in include/stlq_mi355.h.
 #include "stlq_mi355.h"
 #include "stlq_mi355_tools.h"
+#include "stlq_mi355_store.h"
+#include "errors.hpp"
 #include "internal.hpp"
 #include "prune_bound.hpp"
 
@@ -699,6 +701,8 @@ double Mean(const std::vector<float>& v) {
 }
 
 }  // namespace
+
+int stlq_mi355::SetLastError(int code, const std::string& msg) { return Fail(code, msg); }
 
 extern "C" {
 
@@ -1416,6 +1420,7 @@ int stlq_mi355_encode_stream(stlq_mi355_ctx* c, int64_t n_total, int64_t chunk, 
         if (hip_ok(hipEventElapsedTime(&ms, sl.k0, sl.done), "hipEventElapsedTime")) comp_ms += ms;
         sl.busy = false;
         stlq_mi355_chunk_out out{};
+        out.input = sl.hin;  // not refilled before the next fill, which follows this sink call
         if (lr) {
             out.cluster_id = sl.hcluster;
             out.B_small = m > 1 ? sl.hcodes : nullptr;
@@ -1523,6 +1528,108 @@ int stlq_mi355_encode_stream(stlq_mi355_ctx* c, int64_t n_total, int64_t chunk, 
         stats->h2d_bytes = h2d_bytes;
         stats->chunks = nchunks;
     }
+    return rc;
+}
+
+namespace {
+
+// The stream-to-store adapter: every chunk the sink receives becomes one block of the store,
+// then (with a checkpoint path) a committed block.
+struct StoreSink {
+    stlq_mi355_fill_fn fill;
+    void* user;
+    stlq_mi355_store* store;
+    const char* ckpt;
+    bool lr;
+    int m;
+    int raw_kind;
+    int d;
+    std::vector<uint32_t> cluster;
+    std::vector<uint8_t> small;
+    std::vector<uint64_t> bucket_bytes;
+    int rc = STLQ_MI355_OK;
+    std::string err;
+};
+
+int StoreFill(void* u, int64_t first, int64_t count, void* dst) {
+    auto* s = static_cast<StoreSink*>(u);
+    return s->fill(s->user, first, count, dst);
+}
+
+int StoreSinkChunk(void* u, int64_t first, int64_t count, const stlq_mi355_chunk_out* out) {
+    auto* s = static_cast<StoreSink*>(u);
+    const size_t n = static_cast<size_t>(count);
+    const size_t mc = static_cast<size_t>(std::max(0, s->m - 1));
+    const uint32_t* cluster = out->cluster_id;
+    const uint8_t* small = out->B_small;
+    if (!s->lr) {  // full precomp: layer 0's code is the cluster id (ExtractClusterIdAndCodesSmall)
+        s->cluster.resize(n);
+        s->small.resize(n * mc);
+        const size_t m = static_cast<size_t>(s->m);
+        for (size_t i = 0; i < n; ++i) {
+            s->cluster[i] = out->codes[i * m];
+            std::memcpy(s->small.data() + i * mc, out->codes + i * m + 1, mc);
+        }
+        cluster = s->cluster.data();
+        small = s->small.data();
+    }
+    auto fail = [&](int rc) {
+        s->rc = rc;
+        s->err = stlq_mi355_last_error();
+        return 1;
+    };
+    if (int rc = stlq_mi355_store_append(s->store, static_cast<uint64_t>(first), count, cluster, static_cast<int>(mc),
+                                         small, s->m, out->a, s->raw_kind, out->input, s->d))
+        return fail(rc);
+    if (!s->ckpt) return 0;
+    int64_t nb = 0;
+    if (int rc = stlq_mi355_store_flush(s->store)) return fail(rc);
+    if (int rc = stlq_mi355_store_bucket_bytes(s->store, nullptr, 0, &nb)) return fail(rc);
+    s->bucket_bytes.resize(static_cast<size_t>(nb));
+    if (int rc = stlq_mi355_store_bucket_bytes(s->store, s->bucket_bytes.data(), nb, &nb)) return fail(rc);
+    if (int rc = stlq_mi355_checkpoint_write(s->ckpt, static_cast<uint64_t>(first + count), s->bucket_bytes.data(), nb))
+        return fail(rc);
+    return 0;
+}
+
+}  // namespace
+
+int stlq_mi355_encode_stream_store(stlq_mi355_ctx* c, int64_t n_total, int64_t chunk,
+                                   const stlq_mi355_stream_params* sp, stlq_mi355_fill_fn fill, void* user,
+                                   stlq_mi355_store* store, const char* checkpoint_path,
+                                   stlq_mi355_stream_stats* stats) {
+    RC_TRY(CheckCtx(c));
+    if (!sp || !fill || !store) return Fail(STLQ_MI355_ERR_INVALID, "encode_stream_store: null argument");
+    const bool lr = sp->large_root != 0;
+    if (lr) {
+        RC_TRY(CheckLargeRoot(c, sp->encode.H_beam, sp->root_mode));
+    } else {
+        RC_TRY(CheckPre(c));
+    }
+    if (chunk <= 0) return Fail(STLQ_MI355_ERR_INVALID, "encode_stream_store: chunk must be positive");
+    const int m = lr ? c->lr_m : c->m;
+    const int d = lr ? c->lr_d : c->d;
+    const int h0 = lr ? c->h0 : c->h_vec[0];
+    int sd = 0, sm = 0, sh0 = 0, svb = 0, sraw = 0;
+    RC_TRY(stlq_mi355_store_info(store, &sd, &sm, &sh0, &svb, &sraw));
+    if (sd != d || sm != m || sh0 != h0)
+        return Fail(STLQ_MI355_ERR_INVALID, "encode_stream_store: the store's d, m or h_vec[0] (" + std::to_string(sd) +
+                                                ", " + std::to_string(sm) + ", " + std::to_string(sh0) +
+                                                ") differ from the codebooks' (" + std::to_string(d) + ", " +
+                                                std::to_string(m) + ", " + std::to_string(h0) + ")");
+    const int esz = sp->input_u8 ? 1 : 4;
+    if (svb && sraw != d * esz)
+        return Fail(STLQ_MI355_ERR_INVALID, "encode_stream_store: raw_bytes_per_vec must be d for uint8 input and 4d "
+                                            "for float input");
+    if (checkpoint_path && sp->start_id % static_cast<uint64_t>(chunk) != 0)
+        return Fail(STLQ_MI355_ERR_INVALID, "EncodeBaseStreaming: start_id must be a multiple of large.base_block when "
+                                            "using checkpointing.");
+    stlq_mi355_stream_params p = *sp;
+    p.encode.want_coeffs = 1;
+    StoreSink sink{fill, user, store, checkpoint_path, lr, m,
+                   svb ? (sp->input_u8 ? STLQ_MI355_RAW_U8 : STLQ_MI355_RAW_F32) : STLQ_MI355_RAW_NONE, d};
+    const int rc = stlq_mi355_encode_stream(c, n_total, chunk, &p, &StoreFill, &StoreSinkChunk, &sink, stats);
+    if (rc == STLQ_MI355_ERR_CALLBACK && sink.rc != STLQ_MI355_OK) return Fail(sink.rc, sink.err);
     return rc;
 }
 

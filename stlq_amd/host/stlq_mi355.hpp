@@ -24,6 +24,7 @@
 #include <vector>
 
 #include "stlq_mi355.h"
+#include "stlq_mi355_store.h"
 
 namespace stlq_mi355 {
 namespace stlq {
@@ -529,12 +530,236 @@ inline void DynamicIcmWithIlsAbsNoNormalLargeRoot(const ColMajorMatrix<float>& X
                                 X_norm2, cost, sample_id_offset);
 }
 
+namespace io {
+
+// io::BaseBasicStoreConfig (include/stlq/io/base_store.h:12-25), the reference's defaults.
+struct BaseBasicStoreConfig {
+    std::string dir;
+    int d = 0;
+    int m = 0;
+    std::vector<int> h_vec;
+    int shard_size = 2000000;
+    int bucket_size = 256;
+    int bucket_flush_mb = 256;
+    bool write_vector_bucket = true;
+    bool write_basic_to_bucket = true;
+    int raw_bytes_per_vec = 0;
+};
+
+// io::BaseBasicWriter (include/stlq/io/base_store.h:28-100) over include/stlq_mi355_store.h:
+// the reference's on-disk BaseBasicStore, byte for byte. Methods return false and set *err.
+class BaseBasicWriter {
+public:
+    BaseBasicWriter() = default;
+    BaseBasicWriter(const BaseBasicWriter&) = delete;
+    BaseBasicWriter& operator=(const BaseBasicWriter&) = delete;
+    ~BaseBasicWriter() {
+        std::string ignored;
+        (void)Close(&ignored);
+    }
+
+    bool Open(const BaseBasicStoreConfig& cfg, std::string* err) {
+        std::string ignored;
+        (void)Close(&ignored);
+        const stlq_mi355_store_config c = ToC(cfg);
+        return Ok(stlq_mi355_store_open(&c, &h_), err);
+    }
+    bool OpenResume(const BaseBasicStoreConfig& cfg, std::uint64_t start_id,
+                    const std::vector<std::uint64_t>& bucket_sizes, std::string* err) {
+        std::string ignored;
+        (void)Close(&ignored);
+        const stlq_mi355_store_config c = ToC(cfg);
+        return Ok(stlq_mi355_store_open_resume(&c, start_id, bucket_sizes.data(),
+                                               static_cast<std::int64_t>(bucket_sizes.size()), &h_),
+                  err);
+    }
+    bool Close(std::string* err) {
+        if (!h_) return true;
+        const bool flushed = Ok(stlq_mi355_store_flush(h_), err);  // Close's own write-out, kept readable
+        if (flushed) committed_ = Committed();
+        stlq_mi355_store* h = h_;
+        h_ = nullptr;
+        return Ok(stlq_mi355_store_close(h), err) && flushed;
+    }
+    bool Flush(std::string* err) { return Ok(stlq_mi355_store_flush(h_), err); }
+
+    const std::vector<std::uint64_t>& bucket_file_bytes() const {
+        if (h_) committed_ = Committed();
+        return committed_;
+    }
+
+    bool AppendBlock(std::uint64_t start_id, const std::vector<std::uint32_t>& cluster_id,
+                     const ColMajorMatrix<Code>& B_small, const ColMajorMatrix<float>& a,
+                     const ColMajorMatrix<std::uint8_t>* x_u8_optional, std::string* err) {
+        if (x_u8_optional && x_u8_optional->cols != static_cast<int>(cluster_id.size())) {
+            if (err) *err = "BaseBasicWriter::AppendBlock: x_u8 shape mismatch.";
+            return false;
+        }
+        return Append(start_id, cluster_id, B_small, a,
+                      x_u8_optional ? STLQ_MI355_RAW_U8 : STLQ_MI355_RAW_NONE,
+                      x_u8_optional ? x_u8_optional->data.data() : nullptr,
+                      x_u8_optional ? x_u8_optional->rows : 0, err);
+    }
+    bool AppendBlockRawU8(std::uint64_t start_id, const std::vector<std::uint32_t>& cluster_id,
+                          const ColMajorMatrix<Code>& B_small, const ColMajorMatrix<float>& a,
+                          const std::uint8_t* x_u8, int ld_x_u8, std::string* err) {
+        return Append(start_id, cluster_id, B_small, a, STLQ_MI355_RAW_U8, x_u8, ld_x_u8, err);
+    }
+    bool AppendBlockRawF32(std::uint64_t start_id, const std::vector<std::uint32_t>& cluster_id,
+                           const ColMajorMatrix<Code>& B_small, const ColMajorMatrix<float>& a,
+                           const float* x_f32, int ld_x_f32, std::string* err) {
+        return Append(start_id, cluster_id, B_small, a, STLQ_MI355_RAW_F32, x_f32, ld_x_f32, err);
+    }
+
+    stlq_mi355_store* handle() const { return h_; }
+
+private:
+    static stlq_mi355_store_config ToC(const BaseBasicStoreConfig& cfg) {
+        stlq_mi355_store_config c{};
+        c.dir = cfg.dir.c_str();
+        c.d = cfg.d;
+        c.m = cfg.m;
+        c.h_vec = cfg.h_vec.data();
+        c.h_len = static_cast<int>(cfg.h_vec.size());
+        c.shard_size = cfg.shard_size;
+        c.bucket_size = cfg.bucket_size;
+        c.bucket_flush_mb = cfg.bucket_flush_mb;
+        c.write_vector_bucket = cfg.write_vector_bucket ? 1 : 0;
+        c.write_basic_to_bucket = cfg.write_basic_to_bucket ? 1 : 0;
+        c.raw_bytes_per_vec = cfg.raw_bytes_per_vec;
+        return c;
+    }
+    static bool Ok(int rc, std::string* err) {
+        if (rc == STLQ_MI355_OK) return true;
+        if (err) *err = stlq_mi355_last_error();
+        return false;
+    }
+    std::vector<std::uint64_t> Committed() const {
+        std::int64_t nb = 0;
+        stlq_mi355_store_bucket_bytes(h_, nullptr, 0, &nb);
+        std::vector<std::uint64_t> v(static_cast<std::size_t>(nb));
+        stlq_mi355_store_bucket_bytes(h_, v.data(), nb, &nb);
+        return v;
+    }
+    bool Append(std::uint64_t start_id, const std::vector<std::uint32_t>& cluster_id,
+                const ColMajorMatrix<Code>& B_small, const ColMajorMatrix<float>& a, int kind, const void* raw,
+                int ld, std::string* err) {
+        const int n = static_cast<int>(cluster_id.size());
+        if (n > 0 && (B_small.cols != n || a.cols != n)) {
+            if (err) *err = "BaseBasicWriter::AppendBlock: B/a shape mismatch.";
+            return false;
+        }
+        return Ok(stlq_mi355_store_append(h_, start_id, n, cluster_id.data(), B_small.rows, B_small.data.data(),
+                                          a.rows, a.data.data(), kind, raw, ld),
+                  err);
+    }
+
+    stlq_mi355_store* h_ = nullptr;
+    mutable std::vector<std::uint64_t> committed_;
+};
+
+}  // namespace io
+
+namespace app {
+
+// The pipeline's BaseBasic checkpoint (include/stlq/pipeline/main_virtual_helpers.h:35-69).
+struct BaseBasicCheckpoint {
+    static constexpr std::uint32_t kMagic = 0x544b4342u;  // "BCKT"
+    std::uint32_t magic = kMagic;
+    std::uint32_t version = 1;
+    std::uint32_t nbucket = 0;
+    std::uint32_t reserved = 0;
+    std::uint64_t next_id = 0;
+    std::vector<std::uint64_t> bucket_sizes;
+};
+
+inline int ComputeNbucketsForBasic(const io::BaseBasicStoreConfig& cfg) {
+    const int h0 = cfg.h_vec.empty() ? 0 : cfg.h_vec.front();
+    const int bs = std::max(1, cfg.bucket_size);
+    return h0 > 0 ? (h0 + bs - 1) / bs : 0;
+}
+
+inline std::string BaseBasicCheckpointPath(const std::string& base_basic_dir) {
+    return base_basic_dir + "/checkpoint/base_basic/ckpt.bin";
+}
+
+inline bool ReadBaseBasicCheckpoint(const std::string& path, BaseBasicCheckpoint* out, std::string* err) {
+    std::int64_t nb = 0;
+    std::uint64_t next = 0;
+    if (stlq_mi355_checkpoint_read(path.c_str(), &next, nullptr, 0, &nb) != STLQ_MI355_OK) {
+        if (err) *err = stlq_mi355_last_error();
+        return false;
+    }
+    BaseBasicCheckpoint ck;
+    ck.bucket_sizes.resize(static_cast<std::size_t>(nb));
+    stlq_mi355_checkpoint_read(path.c_str(), &next, ck.bucket_sizes.data(), nb, &nb);
+    ck.nbucket = static_cast<std::uint32_t>(nb);
+    ck.next_id = next;
+    *out = std::move(ck);
+    return true;
+}
+
+inline bool WriteBaseBasicCheckpointAtomic(const std::string& path, const BaseBasicCheckpoint& ck, std::string* err) {
+    if (stlq_mi355_checkpoint_write(path.c_str(), ck.next_id, ck.bucket_sizes.data(),
+                                    static_cast<std::int64_t>(ck.bucket_sizes.size())) == STLQ_MI355_OK)
+        return true;
+    if (err) *err = stlq_mi355_last_error();
+    return false;
+}
+
+inline bool TruncateBaseBasicToCheckpoint(const std::string& out_dir, const io::BaseBasicStoreConfig& store_cfg,
+                                          const BaseBasicCheckpoint& ck, std::string* err) {
+    stlq_mi355_store_config c{};
+    c.dir = out_dir.c_str();
+    c.d = store_cfg.d;
+    c.m = store_cfg.m;
+    c.h_vec = store_cfg.h_vec.data();
+    c.h_len = static_cast<int>(store_cfg.h_vec.size());
+    c.shard_size = store_cfg.shard_size;
+    c.bucket_size = store_cfg.bucket_size;
+    if (ck.bucket_sizes.size() != ck.nbucket) {
+        if (err) *err = "Checkpoint bucket layout mismatch.";
+        return false;
+    }
+    if (stlq_mi355_store_truncate_to_checkpoint(&c, ck.next_id, ck.bucket_sizes.data(),
+                                                static_cast<std::int64_t>(ck.bucket_sizes.size())) == STLQ_MI355_OK)
+        return true;
+    if (err) *err = stlq_mi355_last_error();
+    return false;
+}
+
+struct BaseBasicCkptCtx {
+    std::string path;
+    std::uint32_t nbucket = 0;
+};
+
+// The commit hook the pipeline installs (main_virtual_helpers.cpp:277-297).
+inline bool OnCommitBaseBasicCkpt(std::uint64_t next_id, io::BaseBasicWriter* writer, void* vctx, std::string* err) {
+    auto* ctx = static_cast<BaseBasicCkptCtx*>(vctx);
+    if (!ctx || !writer) {
+        if (err) *err = "OnCommitBaseBasicCkpt: ctx or writer is null.";
+        return false;
+    }
+    BaseBasicCheckpoint ck;
+    ck.nbucket = ctx->nbucket;
+    ck.next_id = next_id;
+    ck.bucket_sizes = writer->bucket_file_bytes();
+    if (ck.bucket_sizes.size() != ck.nbucket) {
+        if (err) *err = "OnCommitBaseBasicCkpt: bucket sizes length mismatch.";
+        return false;
+    }
+    return WriteBaseBasicCheckpointAtomic(ctx->path, ck, err);
+}
+
+}  // namespace app
+
 // Optional hook after each committed output block (include/stlq/quantizer/encode_base_streaming.h:25-28).
 template <class Writer>
 struct StreamingBasicCommitHookT {
     void* ctx = nullptr;
     bool (*OnCommit)(std::uint64_t next_id, Writer* writer, void* ctx, std::string* err) = nullptr;
 };
+using StreamingBasicCommitHook = StreamingBasicCommitHookT<io::BaseBasicWriter>;
 
 namespace detail {
 
@@ -547,24 +772,23 @@ struct StreamUser {
     bool large;
     std::string* err;
     bool keep_raw;
+    bool u8;
     double cost_sum = 0.0;
     std::int64_t cost_n = 0;
-    // Raw tiles read but not yet written (fill runs up to two chunks ahead of sink).
-    std::vector<std::pair<std::int64_t, std::vector<float>>> raw;
 };
 
-template <class Reader, class Writer>
+template <class Reader, class Writer, class T>
 int StreamFill(void* u, std::int64_t first, std::int64_t count, void* dst) {
     auto* s = static_cast<StreamUser<Reader, Writer>*>(u);
     const std::size_t len = static_cast<std::size_t>(count) * static_cast<std::size_t>(s->d);
-    float* x = static_cast<float*>(dst);
-    if (!s->reader->ReadBlockInto(static_cast<std::uint64_t>(first), static_cast<std::uint32_t>(count), x,
-                                  len * sizeof(float), s->err))
-        return 1;
-    if (s->keep_raw) s->raw.emplace_back(first, std::vector<float>(x, x + len));
-    return 0;
+    return s->reader->ReadBlockInto(static_cast<std::uint64_t>(first), static_cast<std::uint32_t>(count),
+                                    static_cast<T*>(dst), len * sizeof(T), s->err)
+               ? 0
+               : 1;
 }
 
+// One block to the writer (encode_base_streaming.cpp:3112-3135, :4393-4414), then CommitBlock
+// (:2054-2059): Flush, then the hook with next id = block end.
 template <class Reader, class Writer>
 int StreamSink(void* u, std::int64_t first, std::int64_t count, const stlq_mi355_chunk_out* out) {
     auto* s = static_cast<StreamUser<Reader, Writer>*>(u);
@@ -587,49 +811,28 @@ int StreamSink(void* u, std::int64_t first, std::int64_t count, const stlq_mi355
         for (std::size_t i = 0; i < n; ++i) s->cost_sum += out->cost[i] < 0.0f ? 0.0 : out->cost[i];
         s->cost_n += count;
     }
-    if (s->keep_raw) {
-        auto it = std::find_if(s->raw.begin(), s->raw.end(), [&](const auto& e) { return e.first == first; });
-        if (it == s->raw.end()) {
-            if (s->err) *s->err = "EncodeBaseStreaming: raw tile missing for block.";
-            return 1;
-        }
-        const bool ok = s->writer->AppendBlockRawF32(static_cast<std::uint64_t>(first), cluster_id, B_small, a,
-                                                     it->second.data(), s->d, s->err);
-        s->raw.erase(it);
-        if (!ok) return 1;
-    } else if (!s->writer->AppendBlock(static_cast<std::uint64_t>(first), cluster_id, B_small, a, nullptr,
-                                       s->err)) {
-        return 1;
+    bool ok;
+    if (s->keep_raw && s->u8)
+        ok = s->writer->AppendBlockRawU8(static_cast<std::uint64_t>(first), cluster_id, B_small, a,
+                                         static_cast<const std::uint8_t*>(out->input), s->d, s->err);
+    else if (s->keep_raw)
+        ok = s->writer->AppendBlockRawF32(static_cast<std::uint64_t>(first), cluster_id, B_small, a,
+                                          static_cast<const float*>(out->input), s->d, s->err);
+    else
+        ok = s->writer->AppendBlock(static_cast<std::uint64_t>(first), cluster_id, B_small, a, nullptr, s->err);
+    if (!ok) return 1;
+    if (s->hook && s->hook->OnCommit) {
+        if (!s->writer->Flush(s->err)) return 1;
+        if (!s->hook->OnCommit(static_cast<std::uint64_t>(first + count), s->writer, s->hook->ctx, s->err)) return 1;
     }
-    if (s->hook && s->hook->OnCommit &&
-        !s->hook->OnCommit(static_cast<std::uint64_t>(first + count), s->writer, s->hook->ctx, s->err))
-        return 1;
     return 0;
 }
 
-}  // namespace detail
-
-// EncodeBaseStreamingF32 (include/stlq/quantizer/encode_base_streaming.h:46-58,
-// src/quantizer/encode_base_streaming.cpp:4544-4579): encodes the reader's vectors start_id..n()-1
-// in blocks of config.large.base_block, double-buffered on the device, and appends each block's
-// cluster ids, small codes and LS coefficients to the writer in order (then calls the commit
-// hook). Reader is io::FvecsReader-like (d(), n(), ReadBlockInto(start, count, dst, bytes, err));
-// Writer is io::BaseBasicWriter-like: AppendBlockRawF32(start_id, cluster_id, B_small, a, x, ld, err)
-// with the raw (unrotated) tile when config.large.write_vector_bucket is set (:4396-4404), else
-// AppendBlock(start_id, cluster_id, B_small, a, nullptr, err).
-// pre_large selects the large-root beam with the nearest root forced (the device beams the
-// reference's streaming calls, :1005-1083) and its refit; otherwise the full precomp
-// is used and layer 0's code becomes the cluster id. The rotation R (d x d) is applied on the
-// device (empty R: none). out_final_mse receives the mean cost; out_beam_mse the same when no ICM
-// runs (the streamed refit is final).
-template <class Reader, class Writer>
-bool EncodeBaseStreamingF32(const Config& cfg, const Reader& base_reader, const ColMajorMatrix<float>& R,
-                            const CodebookPack& C_root, const Precomp& pre_full, const PrecompLargeRoot* pre_large,
-                            StreamKernelProvider* kernels, Writer* writer, float* out_beam_mse, float* out_final_mse,
-                            std::string* err, std::uint64_t start_id = 0,
-                            const StreamingBasicCommitHookT<Writer>* commit_hook = nullptr) {
-    (void)C_root;
-    (void)kernels;
+template <class T, class Reader, class Writer>
+bool EncodeStreaming(const Config& cfg, const Reader& base_reader, const ColMajorMatrix<float>& R,
+                     const Precomp& pre_full, const PrecompLargeRoot* pre_large, Writer* writer, float* out_beam_mse,
+                     float* out_final_mse, std::string* err, std::uint64_t start_id,
+                     const StreamingBasicCommitHookT<Writer>* commit_hook) {
     if (!writer) {
         if (err) *err = "EncodeBaseStreaming: writer is null.";
         return false;
@@ -649,24 +852,23 @@ bool EncodeBaseStreamingF32(const Config& cfg, const Reader& base_reader, const 
         if (err) *err = "EncodeBaseStreaming: start_id must be a multiple of large.base_block when using checkpointing.";
         return false;
     }
+    if (start_id == nbase) return true;
     const BaseEncodeConfig& e = cfg.base.encode;
     stlq_mi355_stream_params sp{};
     sp.encode = stlq_mi355_encode_params{std::max(1, e.H_beam), e.icm_iters, e.ils_iters, e.perturb_k,
                                           e.use_abs ? 1 : 0, static_cast<std::uint32_t>(e.seed), 1};
-    sp.input_u8 = 0;
+    sp.input_u8 = sizeof(T) == 1 ? 1 : 0;
     sp.large_root = pre_large ? 1 : 0;
     sp.root_mode = 1;
     sp.R = (R.rows == d && R.cols == d) ? R.data.data() : nullptr;
     sp.start_id = start_id;
-    detail::StreamUser<Reader, Writer> u{&base_reader, writer, commit_hook, d,
-                                         pre_large ? pre_large->m : pre_full.m, pre_large != nullptr, err,
-                                         cfg.large.write_vector_bucket};
-    stlq_mi355_ctx* ctx = pre_large ? detail::BindLargeRoot(*pre_large) : detail::Bind(pre_full);
+    StreamUser<Reader, Writer> u{&base_reader, writer, commit_hook, d, pre_large ? pre_large->m : pre_full.m,
+                                 pre_large != nullptr, err, cfg.large.write_vector_bucket, sizeof(T) == 1};
+    stlq_mi355_ctx* ctx = pre_large ? BindLargeRoot(*pre_large) : Bind(pre_full);
     stlq_mi355_stream_stats st{};
     const int rc = stlq_mi355_encode_stream(ctx, static_cast<std::int64_t>(nbase - start_id),
-                                            static_cast<std::int64_t>(block), &sp,
-                                            &detail::StreamFill<Reader, Writer>, &detail::StreamSink<Reader, Writer>,
-                                            &u, &st);
+                                            static_cast<std::int64_t>(block), &sp, &StreamFill<Reader, Writer, T>,
+                                            &StreamSink<Reader, Writer>, &u, &st);
     if (rc != STLQ_MI355_OK) {
         if (err && err->empty()) *err = stlq_mi355_last_error();
         return false;
@@ -675,6 +877,49 @@ bool EncodeBaseStreamingF32(const Config& cfg, const Reader& base_reader, const 
     if (out_final_mse) *out_final_mse = mse;
     if (out_beam_mse) *out_beam_mse = mse;
     return true;
+}
+
+}  // namespace detail
+
+// EncodeBaseStreaming (include/stlq/quantizer/encode_base_streaming.h:32-44,
+// src/quantizer/encode_base_streaming.cpp:1913-2060 and :3060-3212): encodes the reader's uint8
+// vectors start_id..n()-1 in blocks of config.large.base_block, double-buffered on the device
+// (uint8 widened there), and appends each block's cluster ids, small codes and LS coefficients to
+// the writer in order, then calls the commit hook (after writer->Flush).
+// Reader is io::BvecsReader-like (d(), n(), ReadBlockInto(start, count, uint8_t* dst, bytes, err));
+// Writer is io::BaseBasicWriter (or one with its AppendBlock/AppendBlockRawU8/Flush): with
+// config.large.write_vector_bucket the raw uint8 tile goes into the bucket records (:3114-3124),
+// else AppendBlock(..., nullptr, ...). pre_large selects the large-root beam with the nearest root
+// forced and its refit (:1005-1210); otherwise the full precomp is used and layer 0's code is the
+// cluster id. The rotation R (d x d) is applied on the device (empty R: none). out_final_mse
+// receives the mean cost; out_beam_mse the same (the streamed refit is final).
+template <class Reader, class Writer>
+bool EncodeBaseStreaming(const Config& cfg, const Reader& base_reader, const ColMajorMatrix<float>& R,
+                         const CodebookPack& C_root, const Precomp& pre_full, const PrecompLargeRoot* pre_large,
+                         StreamKernelProvider* kernels, Writer* writer, float* out_beam_mse, float* out_final_mse,
+                         std::string* err, std::uint64_t start_id = 0,
+                         const StreamingBasicCommitHookT<Writer>* commit_hook = nullptr) {
+    (void)C_root;
+    (void)kernels;
+    return detail::EncodeStreaming<std::uint8_t>(cfg, base_reader, R, pre_full, pre_large, writer, out_beam_mse,
+                                                 out_final_mse, err, start_id, commit_hook);
+}
+
+// EncodeBaseStreamingF32 (include/stlq/quantizer/encode_base_streaming.h:46-58,
+// src/quantizer/encode_base_streaming.cpp:3285-3420, :4544-4579): as EncodeBaseStreaming for float
+// vectors. Reader is io::FvecsReader-like (ReadBlockInto(start, count, float* dst, bytes, err));
+// with write_vector_bucket the raw (unrotated) float tile goes into the bucket records through
+// AppendBlockRawF32 (:4396-4404).
+template <class Reader, class Writer>
+bool EncodeBaseStreamingF32(const Config& cfg, const Reader& base_reader, const ColMajorMatrix<float>& R,
+                            const CodebookPack& C_root, const Precomp& pre_full, const PrecompLargeRoot* pre_large,
+                            StreamKernelProvider* kernels, Writer* writer, float* out_beam_mse, float* out_final_mse,
+                            std::string* err, std::uint64_t start_id = 0,
+                            const StreamingBasicCommitHookT<Writer>* commit_hook = nullptr) {
+    (void)C_root;
+    (void)kernels;
+    return detail::EncodeStreaming<float>(cfg, base_reader, R, pre_full, pre_large, writer, out_beam_mse,
+                                          out_final_mse, err, start_id, commit_hook);
 }
 
 }  // namespace stlq

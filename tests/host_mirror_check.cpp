@@ -92,6 +92,31 @@ struct MemWriter {
         }
         return Put(start, cid, Bs, am, x, ld, err);
     }
+    bool AppendBlockRawU8(std::uint64_t, const std::vector<std::uint32_t>&, const s::ColMajorMatrix<s::Code>&,
+                          const s::ColMajorMatrix<float>&, const std::uint8_t*, int, std::string* err) {
+        if (err) *err = "MemWriter: float stream gave a uint8 tile";
+        return false;
+    }
+    bool Flush(std::string*) { return true; }
+};
+
+// BvecsReader-like (uint8) view of a caller array (d x n column-major).
+struct MemReaderU8 {
+    int d_;
+    std::uint64_t n_;
+    const std::uint8_t* x;
+    int d() const { return d_; }
+    std::uint64_t n() const { return n_; }
+    bool ReadBlockInto(std::uint64_t start, std::uint32_t count, std::uint8_t* dst, std::size_t bytes,
+                       std::string* err) const {
+        const std::size_t want = static_cast<std::size_t>(count) * static_cast<std::size_t>(d_);
+        if (start + count > n_ || bytes < want) {
+            if (err) *err = "MemReaderU8: block out of range";
+            return false;
+        }
+        std::memcpy(dst, x + start * static_cast<std::uint64_t>(d_), want);
+        return true;
+    }
 };
 
 struct HookLog {
@@ -270,6 +295,101 @@ int mirror_stream(int d, int m, const int* h_vec, const float* C_all, const floa
         if (writer.next != static_cast<std::uint64_t>(n)) {
             PutError("stream ended before the last id", err, errlen);
             return 4;
+        }
+        return 0;
+    } catch (const std::exception& ex) {
+        PutError(ex.what(), err, errlen);
+        return 4;
+    }
+}
+
+
+// EncodeBaseStreaming (u8 != 0, uint8 X) or EncodeBaseStreamingF32 (float X) writing a real
+// BaseBasicStore at dir through io::BaseBasicWriter, with the pipeline's checkpoint hook
+// (app::OnCommitBaseBasicCkpt at app::BaseBasicCheckpointPath(dir)) when use_ckpt. resume != 0
+// continues the store the way the pipeline does (stlq_large_base_stages.cpp:321-390): read the
+// checkpoint, cut the store back to it, OpenResume at its next id and stream from there. stop_at > 0
+// stops the stream at that id (a run cut short). Store layout: shard_size, bucket_size, flush_mb
+// and write_raw (vector buckets). Return 0 on success, 1 when a call returned false, 4 on an exception.
+int mirror_stream_store(const char* dir, int d, int m, const int* h_vec, const float* C_all, const void* X, int u8,
+                        int n, int large, int H_beam, int icm_iters, int ils_iters, int base_block, int shard_size,
+                        int bucket_size, int flush_mb, int write_raw, int use_ckpt, int resume, int stop_at,
+                        char* err, int errlen) {
+    try {
+        s::Config cfg;
+        cfg.base.encode.H_beam = H_beam;
+        cfg.base.encode.icm_iters = icm_iters;
+        cfg.base.encode.ils_iters = ils_iters;
+        cfg.large.base_block = base_block;
+        cfg.large.write_vector_bucket = write_raw != 0;
+        const s::CodebookPack pack = MakePack(d, m, h_vec, C_all);
+        s::Precomp pre_full;
+        s::PrecompLargeRoot pre_large;
+        std::string e;
+        if (large) {
+            if (!s::BuildPrecompLargeRoot(pack, nullptr, s::PrecompLargeRootBuildOptions{}, &pre_large, &e)) {
+                PutError("BuildPrecompLargeRoot: " + e, err, errlen);
+                return 4;
+            }
+        } else if (!s::BuildPrecomp(pack, &pre_full)) {
+            PutError("BuildPrecomp failed", err, errlen);
+            return 4;
+        }
+        s::io::BaseBasicStoreConfig sc;
+        sc.dir = dir;
+        sc.d = d;
+        sc.m = m;
+        sc.h_vec.assign(h_vec, h_vec + m);
+        sc.shard_size = shard_size;
+        sc.bucket_size = bucket_size;
+        sc.bucket_flush_mb = flush_mb;
+        sc.write_vector_bucket = write_raw != 0;
+        sc.raw_bytes_per_vec = write_raw ? (u8 ? d : d * static_cast<int>(sizeof(float))) : 0;
+        const std::string ckpt = s::app::BaseBasicCheckpointPath(dir);
+        s::io::BaseBasicWriter writer;
+        std::uint64_t start_id = 0;
+        bool ok = true;
+        if (resume) {
+            s::app::BaseBasicCheckpoint ck;
+            ok = s::app::ReadBaseBasicCheckpoint(ckpt, &ck, &e) && s::app::TruncateBaseBasicToCheckpoint(dir, sc, ck, &e) &&
+                 writer.OpenResume(sc, ck.next_id, ck.bucket_sizes, &e);
+            start_id = ck.next_id;
+        } else {
+            ok = writer.Open(sc, &e);
+            if (ok && use_ckpt) {
+                s::app::BaseBasicCheckpoint init;
+                init.nbucket = static_cast<std::uint32_t>(s::app::ComputeNbucketsForBasic(sc));
+                init.bucket_sizes.assign(init.nbucket, 0);
+                ok = s::app::WriteBaseBasicCheckpointAtomic(ckpt, init, &e);
+            }
+        }
+        if (!ok) {
+            PutError(e, err, errlen);
+            return 1;
+        }
+        s::app::BaseBasicCkptCtx hook_ctx;
+        hook_ctx.path = ckpt;
+        hook_ctx.nbucket = static_cast<std::uint32_t>(s::app::ComputeNbucketsForBasic(sc));
+        s::StreamingBasicCommitHook hook;
+        hook.ctx = &hook_ctx;
+        hook.OnCommit = &s::app::OnCommitBaseBasicCkpt;
+        const std::uint64_t end = stop_at > 0 ? static_cast<std::uint64_t>(stop_at) : static_cast<std::uint64_t>(n);
+        float mse[2];
+        if (u8) {
+            const MemReaderU8 reader{d, end, static_cast<const std::uint8_t*>(X)};
+            ok = s::EncodeBaseStreaming(cfg, reader, s::ColMajorMatrix<float>(), pack, pre_full,
+                                        large ? &pre_large : nullptr, nullptr, &writer, &mse[0], &mse[1], &e, start_id,
+                                        use_ckpt ? &hook : nullptr);
+        } else {
+            const MemReader reader{d, end, static_cast<const float*>(X)};
+            ok = s::EncodeBaseStreamingF32(cfg, reader, s::ColMajorMatrix<float>(), pack, pre_full,
+                                           large ? &pre_large : nullptr, nullptr, &writer, &mse[0], &mse[1], &e,
+                                           start_id, use_ckpt ? &hook : nullptr);
+        }
+        ok = ok && writer.Close(&e);
+        if (!ok) {
+            PutError(e, err, errlen);
+            return 1;
         }
         return 0;
     } catch (const std::exception& ex) {

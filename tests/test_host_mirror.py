@@ -216,3 +216,75 @@ def test_mirror_stream_matches_oracle_and_resumes(orc, large):
     for key in ("cid", "Bs", "a"):
         assert np.array_equal(part[key][start:], full[key][start:]), key
     assert not part["raw"].any()  # write_vector_bucket off: AppendBlock without the raw tile
+
+
+def _stream_store(root, d, m, h, C_all, X, u8, n, large, Hb, icm, ils, block, shard, bucket, resume=0, stop_at=0):
+    lib = _lib()
+    lib.mirror_stream_store.restype = ctypes.c_int
+    lib.mirror_stream_store.argtypes = [ctypes.c_char_p, ctypes.c_int, ctypes.c_int, _i32p, _f32p, ctypes.c_void_p] + \
+        [ctypes.c_int] * 14 + [ctypes.c_char_p, ctypes.c_int]
+    err = ctypes.create_string_buffer(512)
+    rc = lib.mirror_stream_store(str(root).encode(), d, m, _p(h, _i32p), _p(C_all, _f32p),
+                                 X.ctypes.data_as(ctypes.c_void_p), int(u8), n, large, Hb, icm, ils, block, shard,
+                                 bucket, 1, 1, 1, resume, stop_at, err, 512)
+    return rc, err.value.decode()
+
+
+def _tree(root):
+    out = {}
+    for dp, _, fns in os.walk(root):
+        for f in fns:
+            out[os.path.relpath(os.path.join(dp, f), root)] = open(os.path.join(dp, f), "rb").read()
+    return out
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("large", [1, 0], ids=["large_root_u8", "full_precomp_f32"])
+def test_mirror_stream_store_matches_c_abi_and_resumes(ctx, tmp_path, large):
+    """EncodeBaseStreaming[F32] through the mirror into io::BaseBasicWriter with the pipeline's
+    checkpoint hook writes the same store, byte for byte, as stlq_mi355_encode_stream_store; a run
+    stopped after two blocks, resumed through ReadBaseBasicCheckpoint + TruncateBaseBasicToCheckpoint
+    + OpenResume, ends with the same files as the uninterrupted one (checkpoint included)."""
+    from stlq_amd import store as S
+    from stlq_amd.encoder import EncodeConfig
+
+    n, d, m, h, C_all, X = _stream_problem(large)
+    Hb, icm, ils, block, shard, bucket = 8, 1, 2, 400, 800, 300
+    if large:
+        X = np.clip(np.rint(X), 0, 255).astype(np.uint8)
+    print(f"mirror stream store large={large} n={n}", flush=True)
+    rc, err = _stream_store(tmp_path / "mirror", d, m, h, C_all, X, large, n, large, Hb, icm, ils, block, shard, bucket)
+    assert rc == 0, err
+    if large:
+        ctx.set_large_root(C_all[:h[0]], C_all[h[0]:], list(h))
+    else:
+        ctx.set_codebooks(C_all, list(h))
+    cfg = S.BaseBasicStoreConfig(dir=str(tmp_path / "abi"), d=d, m=m, h_vec=list(h), shard_size=shard,
+                                 bucket_size=bucket, bucket_flush_mb=1,
+                                 raw_bytes_per_vec=d if large else 4 * d)
+    w = S.BaseBasicWriter()
+    assert w.Open(cfg), w.err
+
+    def fill(first, cnt, out):
+        out[:] = X[first:first + cnt]
+
+    S.encode_stream_store(ctx, w, n, block, EncodeConfig(H_beam=Hb, icm_iters=icm, ils_iters=ils), fill,
+                          input_u8=bool(large), large_root=bool(large), root_mode=1,
+                          checkpoint_path=S.BaseBasicCheckpointPath(str(tmp_path / "abi")))
+    assert w.Close(), w.err
+    a, b = _tree(tmp_path / "mirror"), _tree(tmp_path / "abi")
+    assert sorted(a) == sorted(b)
+    for k in a:
+        assert a[k] == b[k], k
+    root = tmp_path / "resumed"
+    rc, err = _stream_store(root, d, m, h, C_all, X, large, n, large, Hb, icm, ils, block, shard, bucket,
+                            stop_at=2 * block)
+    assert rc == 0, err
+    with open(root / "cluster_id.u32", "ab") as fh:
+        fh.write(b"\x01" * 40)
+    rc, err = _stream_store(root, d, m, h, C_all, X, large, n, large, Hb, icm, ils, block, shard, bucket, resume=1)
+    assert rc == 0, err
+    c = _tree(root)
+    assert sorted(a) == sorted(c)
+    for k in a:
+        assert a[k] == c[k], k
