@@ -18,6 +18,7 @@ of that sample with the oracle's.
 from __future__ import annotations
 
 import argparse
+import concurrent.futures as cf
 import json
 import os
 import sys
@@ -108,12 +109,20 @@ def _calib_copy(ctx, mb: int):
 
 
 def _layer_kernel_name(L: int, lr: bool) -> str:
-    """The profiled name of the beam layer kernel that runs layer L (full codebook, best-first
-    pass): the survivor-queue kernel for layers 3..8, the per-parent kernel otherwise."""
-    b = "true" if lr else "false"
-    if 3 <= L <= 8:
-        return f"LayerKernel<{L}, {b}, true, true>"
-    return f"LayerKernelDeep<{L}, {b}, true, true>"
+    """The profiled name of the beam layer kernel that runs layer L with a full codebook (the
+    dispatch of LaunchL in k_beam.hip): the per-parent kernel for layers 1..2, the survivor-queue
+    kernel for 3..8, then the staged kernel (the large root: the per-parent kernel up to layer 13).
+    The full-precomp beam runs its best-first pass, the large-root beam the reference order."""
+    b, best = ("true", "false") if lr else ("false", "true")
+    if L < 3:
+        kind = "LayerKernelDeep"
+    elif L <= 8:
+        kind = "LayerKernel"
+    elif lr and L < 14:
+        kind = "LayerKernelDeep"
+    else:
+        kind = "LayerKernelStaged"
+    return f"{kind}<{L}, {b}, true, {best}>"
 
 
 def _cpu_model() -> str:
@@ -371,7 +380,9 @@ def bench_stream_large_root(args, w):
     chunk = min(chunk, n)
     t0 = time.perf_counter()
     mix = workloads.Mixture(w.kind, w.d, w.n_comp, w.seed)
-    pool = mix.sample(0, chunk).astype(np.uint8)  # values are already integers in [0, 255]
+    # Every vector of the stream is drawn from the mixture by its global id while the previous
+    # chunk encodes (fill runs on the host between chunk launches); row blocks in parallel.
+    gen = cf.ThreadPoolExecutor(max_workers=min(16, os.cpu_count() or 1))
     C0, Cs = workloads.make_large_root(w, h0, w.m - 1)
     h = [h0] + [w.K] * (w.m - 1)
     log(f"workload C5 generated in {time.perf_counter() - t0:.1f}s: stream n={n} chunk={chunk} d={w.d} "
@@ -380,17 +391,11 @@ def bench_stream_large_root(args, w):
     dev_name, cus = ctx.device_info()
     ctx.set_large_root(C0, Cs, h)
     cfg = EncodeConfig(H_beam=w.H_beam, icm_iters=0, want_coeffs=True)
-    P = pool.shape[0]
     keep = min(2000, chunk)
     first_codes = {}
 
     def fill(first, count, out):
-        # chunk c replays the pool rotated by a chunk-dependent offset (distinct rows per chunk)
-        off = (first // chunk) * 7919 % P
-        k = min(count, P - off)
-        out[:k] = pool[off:off + k]
-        if k < count:
-            out[k:] = pool[:count - k]
+        mix.sample_into(first, out, gen)  # values are integers in [0, 255]: exact as uint8
 
     t_prog = [time.perf_counter(), 0]
 
@@ -483,7 +488,7 @@ def bench_stream_large_root(args, w):
         ns = min(args.cpu_sample, keep)
         threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
         use_ref = ref.available()
-        Xs = pool[:ns].astype(np.float32)
+        Xs = mix.sample(0, min(chunk, 65536))[:ns]  # the stream's first rows (same row blocks)
         norm0, Gs, G0S = orc.build_precomp_large_root(C0, Cs, nthreads=threads)
         tc = time.perf_counter()
         nx2 = ref.xnorm2(Xs) if use_ref else orc.xnorm2(Xs, nthreads=threads)

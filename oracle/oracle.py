@@ -21,7 +21,9 @@ import subprocess
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-_LIB_PATH = os.path.join(_HERE, "_build", "libstlq_oracle.so")
+# STLQ_ORACLE_LIB selects another build of the same source (the sanitizer test loads an
+# AddressSanitizer/UBSan build through it).
+_LIB_PATH = os.environ.get("STLQ_ORACLE_LIB") or os.path.join(_HERE, "_build", "libstlq_oracle.so")
 _lib = None
 
 _f32p = ctypes.POINTER(ctypes.c_float)

@@ -514,6 +514,20 @@ __device__ __forceinline__ void EvalStaged(const float* f, const float (&A)[L], 
     e = ee < 0.0f ? 0.0f : ee;
 }
 
+// The queue kernel's per-slot state in LDS: EvalStaged's factor layout (record dwords 1 ..
+// L(L+3)/2: R(0..c, c) then RN(1/R(c,c)) for c < L), then a_old[L], then E_old. The stride is odd,
+// so the slots that different lanes read at one offset sit in different LDS banks.
+template <int L>
+struct QStage {
+    static constexpr int kRWords = L * (L + 3) / 2;
+    static constexpr int kEold = kRWords + L;
+    static constexpr int kStride = (kEold + 1) | 1;
+    // dynamic LDS of one workgroup for beam width Hb
+    static constexpr size_t Bytes(int Hb) {
+        return sizeof(float) * static_cast<size_t>(kBeamWavesPerBlock) * static_cast<size_t>(Hb) * kStride;
+    }
+};
+
 // Vector index i and beam-state index w of this wave (see LayerArgs::list); false when the wave
 // has no vector.
 __device__ __forceinline__ bool WaveItem(const LayerArgs& p, int wave, int64_t& i, int64_t& w) {
@@ -617,7 +631,8 @@ __global__ __launch_bounds__(256) void Layer0Kernel(LayerArgs p) {
 //  * the other layers at the allocator's own choice.
 template <int L, bool LR, bool BEST>
 constexpr int LayerMinWaves() {
-    return L >= 11 ? (LR ? 5 : 4) : (L == 3 && !LR ? 7 : 1);  // layer 3: 72 VGPRs, one wave more than left alone
+    if (LR) return L >= 11 ? 5 : 1;
+    return L == 3 ? 8 : (L <= 5 ? 7 : (L == 6 ? 6 : 1));
 }
 
 // Layers up to kVStateMaxL read the slot state into VGPRs (see process() in LayerKernel): on the
@@ -684,6 +699,33 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LayerMinWav
     __shared__ int s_pack[kBeamWavesPerBlock][kMaxK];
     int* __restrict__ pack = s_pack[wave];
     const bool prune_on = p.prune != 0;
+
+    // The queue scan's exact evaluations read each lane's parent state from LDS (QStage), staged
+    // here for every slot: the factor is then read row by row as the solves need it (EvalStaged)
+    // instead of being held whole in registers, which keeps the kernel's VGPRs, and so its
+    // occupancy, near the bound stage's. diag_mask bit h: slot h's diagonal is in the range where
+    // the Markstein quotients are exact.
+    HIP_DYNAMIC_SHARED(float, s_stage)
+    float* __restrict__ stage = s_stage + static_cast<size_t>(wave) * Hb * QStage<L>::kStride;
+    uint64_t diag_mask = 0;
+    if (prune_on) {
+        constexpr int kW = QStage<L>::kEold + 1;
+        for (int q = lane; q < curH * kW; q += kWave) {
+            const int h = q / kW, o = q - h * kW;
+            const float* src = recs_in + h * rc.stride;
+            stage[h * QStage<L>::kStride + o] =
+                o < QStage<L>::kRWords ? src[1 + o] : (o < QStage<L>::kEold ? src[rc.coef + o - QStage<L>::kRWords] : src[0]);
+        }
+        bool dok = lane < curH;
+        if (dok) {
+            const float* src = recs_in + lane * rc.stride;
+#pragma unroll
+            for (int r = 0; r < L; ++r) dok = dok && DiagFastOk(src[Rec::R(r, r)]);
+        }
+        diag_mask = Ballot(dok);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
 
     // Evaluates slot h's candidates and replays them into the top-H (scan order: slot, then code).
     // Returns false when the replay asks for the slow pass.
@@ -835,18 +877,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LayerMinWav
             const int ent = act ? queue[(qhead + lane) & (kQueueCap - 1)] : 0;
             const int hl = ent >> 8;
             const uint32_t k = static_cast<uint32_t>(ent & 0xFF);
-            const float* rl = recs_in + hl * rc.stride;
-            float Rv[L][L], Ri[L], aold[L], A[L];
-            bool diag_ok = true;
-#pragma unroll
-            for (int r = 0; r < L; ++r) {
-#pragma unroll
-                for (int c = r; c < L; ++c) Rv[r][c] = rl[Rec::R(r, c)];
-                Ri[r] = rl[Rec::Rinv(r)];
-                aold[r] = rl[rc.coef + r];
-                diag_ok = diag_ok && DiagFastOk(Rv[r][r]);
-            }
-            const float E_old = rl[0];
+            const float* f = stage + hl * QStage<L>::kStride;
+            float A[L];
+            const bool diag_ok = ((diag_mask >> hl) & 1ull) != 0ull;
+            const float E_old = f[QStage<L>::kEold];
             const uint32_t rootl =
                 LR ? static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(hl << 2, static_cast<int>(rootw))) : 0u;
             // the parent's codes from its lane (lane h holds slot h's code words)
@@ -863,18 +897,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LayerMinWav
             }
             const float alpha = p.gdiag[offL + k];
             const float gamma = xCi[offL + k];
-            auto Rf = [&](int r, int c) { return Rv[r][c]; };
             float y[L], v[L], denom, a_last, e;
             bool ok, safe = true;
             if (LR) {
-                EvalCand<L, 2>(Rf, Ri, A, aold, E_old, alpha, gamma, y, v, e, denom, a_last, ok, safe);
+                EvalStaged<L, 2>(f, A, E_old, alpha, gamma, y, v, e, denom, a_last, ok, safe);
             } else {
                 bool ieee = Ballot(act && !diag_ok) != 0ull;
                 if (!ieee) {
-                    EvalCand<L, 1>(Rf, Ri, A, aold, E_old, alpha, gamma, y, v, e, denom, a_last, ok, safe);
+                    EvalStaged<L, 1>(f, A, E_old, alpha, gamma, y, v, e, denom, a_last, ok, safe);
                     ieee = Ballot(act && !safe) != 0ull;
                 }
-                if (ieee) EvalCand<L, 0>(Rf, Ri, A, aold, E_old, alpha, gamma, y, v, e, denom, a_last, ok, safe);
+                if (ieee) EvalStaged<L, 0>(f, A, E_old, alpha, gamma, y, v, e, denom, a_last, ok, safe);
             }
             qhead = (qhead + n) & (kQueueCap - 1);
             qlen -= n;
@@ -2067,16 +2100,17 @@ hipError_t LaunchWith(bool lr, const LayerArgs& a, hipStream_t s) {
     const unsigned blocks = static_cast<unsigned>((a.n + kBeamWavesPerBlock - 1) / kBeamWavesPerBlock);
     const dim3 block(kWave * kBeamWavesPerBlock);
     const bool full = a.K == kMaxK;
+    const unsigned lds = static_cast<unsigned>(KernelSel<L, false, true, false>::DynamicLds(a.Hb));
     if (lr) {  // the large-root beam always runs in the reference order
         if (a.flags) return hipErrorInvalidValue;
-        if (full) hipLaunchKernelGGL((KernelSel<L, true, true, false>::kernel), dim3(blocks), block, 0, s, a);
-        else hipLaunchKernelGGL((KernelSel<L, true, false, false>::kernel), dim3(blocks), block, 0, s, a);
+        if (full) hipLaunchKernelGGL((KernelSel<L, true, true, false>::kernel), dim3(blocks), block, lds, s, a);
+        else hipLaunchKernelGGL((KernelSel<L, true, false, false>::kernel), dim3(blocks), block, lds, s, a);
     } else if (a.flags) {
-        if (full) hipLaunchKernelGGL((KernelSel<L, false, true, true>::kernel), dim3(blocks), block, 0, s, a);
-        else hipLaunchKernelGGL((KernelSel<L, false, false, true>::kernel), dim3(blocks), block, 0, s, a);
+        if (full) hipLaunchKernelGGL((KernelSel<L, false, true, true>::kernel), dim3(blocks), block, lds, s, a);
+        else hipLaunchKernelGGL((KernelSel<L, false, false, true>::kernel), dim3(blocks), block, lds, s, a);
     } else {
-        if (full) hipLaunchKernelGGL((KernelSel<L, false, true, false>::kernel), dim3(blocks), block, 0, s, a);
-        else hipLaunchKernelGGL((KernelSel<L, false, false, false>::kernel), dim3(blocks), block, 0, s, a);
+        if (full) hipLaunchKernelGGL((KernelSel<L, false, true, false>::kernel), dim3(blocks), block, lds, s, a);
+        else hipLaunchKernelGGL((KernelSel<L, false, false, false>::kernel), dim3(blocks), block, lds, s, a);
     }
     return hipGetLastError();
 }
@@ -2084,15 +2118,18 @@ hipError_t LaunchWith(bool lr, const LayerArgs& a, hipStream_t s) {
 template <int L, bool LR, bool FULL, bool BEST>
 struct QueueSel {
     static constexpr auto kernel = LayerKernel<L, LR, FULL, BEST>;
+    static constexpr size_t DynamicLds(int Hb) { return QStage<L>::Bytes(Hb); }  // the staged slot states
 };
 template <int L, bool LR, bool FULL, bool BEST>
 struct DeepSel {
     static constexpr auto kernel = LayerKernelDeep<L, LR, FULL, BEST>;
+    static constexpr size_t DynamicLds(int) { return 0; }
 };
 
 template <int L, bool LR, bool FULL, bool BEST>
 struct StagedSel {
     static constexpr auto kernel = LayerKernelStaged<L, LR, FULL, BEST>;
+    static constexpr size_t DynamicLds(int) { return 0; }
 };
 
 template <int L>

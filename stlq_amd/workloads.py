@@ -75,23 +75,41 @@ class Mixture:
         else:
             raise ValueError(kind)
 
+    def _rows(self, g: int, rows: int, block: int) -> np.ndarray:
+        rng = np.random.default_rng([self.seed, 7919, g // block, g % block])
+        comp = rng.integers(0, self.n_comp, size=rows)
+        noise = rng.standard_normal((rows, self.d), dtype=np.float32)
+        if self.kind == "decay":
+            noise *= self.scale
+        x = self.centers[comp] + self.sigma * noise
+        if self.kind == "desc":
+            np.clip(np.rint(x), 0.0, 255.0, out=x)
+        elif self.kind == "sphere":
+            x /= np.linalg.norm(x, axis=1, keepdims=True)
+        return x
+
     def sample(self, first: int, count: int, block: int = 65536) -> np.ndarray:
         out = np.empty((count, self.d), np.float32)
         for b0 in range(0, count, block):
             b1 = min(count, b0 + block)
-            g = first + b0
-            rng = np.random.default_rng([self.seed, 7919, g // block, g % block])
-            comp = rng.integers(0, self.n_comp, size=b1 - b0)
-            noise = rng.standard_normal((b1 - b0, self.d), dtype=np.float32)
-            if self.kind == "decay":
-                noise *= self.scale
-            x = self.centers[comp] + self.sigma * noise
-            if self.kind == "desc":
-                np.clip(np.rint(x), 0.0, 255.0, out=x)
-            elif self.kind == "sphere":
-                x /= np.linalg.norm(x, axis=1, keepdims=True)
-            out[b0:b1] = x
+            out[b0:b1] = self._rows(first + b0, b1 - b0, block)
         return out
+
+    def sample_into(self, first: int, out: np.ndarray, executor=None, block: int = 65536) -> None:
+        """sample(first, len(out)) written into `out` (float32, or uint8 for the integer-valued
+        "desc" kind), its row blocks generated in parallel on `executor` when one is given."""
+        count = out.shape[0]
+
+        def one(b0):
+            b1 = min(count, b0 + block)
+            out[b0:b1] = self._rows(first + b0, b1 - b0, block)
+
+        starts = range(0, count, block)
+        if executor is None:
+            for b0 in starts:
+                one(b0)
+        else:
+            list(executor.map(one, starts))
 
 
 def _assign(X, C, spherical):
