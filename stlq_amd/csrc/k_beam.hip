@@ -386,6 +386,19 @@ __device__ __forceinline__ int VZero() {
     return z;
 }
 
+// Raw buffer access to a row-major Gram (G, Gs or G_small: ld x ld floats, ld <= 20 * 256): a
+// row's byte offset rides in a scalar register and the column in the lane's offset, so a row
+// address costs one 32-bit scalar multiply instead of 64-bit pointer arithmetic. Reads past
+// `bytes` return 0 (the buffer's range check).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t GramRsrc(const float* g, int ld) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(g), 0, ld * ld * static_cast<int>(sizeof(float)),
+                                             0x00020000);
+}
+__device__ __forceinline__ float GramLd(__amdgpu_buffer_rsrc_t r, uint32_t lane_bytes, uint32_t row_bytes) {
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, static_cast<int>(lane_bytes),
+                                                                static_cast<int>(row_bytes), 0));
+}
+
 __device__ __forceinline__ int CodeAt(const float* rec, int code_off, int t) {
     const uint32_t w = reinterpret_cast<const uint32_t*>(rec + code_off)[t >> 2];
     return static_cast<int>((w >> (8 * (t & 3))) & 0xFFu);
@@ -632,7 +645,7 @@ __global__ __launch_bounds__(256) void Layer0Kernel(LayerArgs p) {
 template <int L, bool LR, bool BEST>
 constexpr int LayerMinWaves() {
     if (LR) return L >= 11 ? 5 : 1;
-    return L == 3 ? 8 : (L <= 5 ? 7 : (L == 6 ? 6 : 1));
+    return L <= 3 ? 8 : (L <= 5 ? 7 : (L == 6 ? 6 : 1));
 }
 
 // Layers up to kVStateMaxL read the slot state into VGPRs (see process() in LayerKernel): on the
@@ -644,7 +657,7 @@ constexpr int kVStateMaxL = 3;
 // pruning bound from every parent go into one FIFO and are evaluated 64 at a time, each lane with
 // its own parent's factor in VGPRs. Deeper layers evaluate each parent's survivors apart, with the
 // factor in SGPRs, whose VGPR cost would otherwise grow as L^2.
-constexpr int kQueueMinL = 3;
+constexpr int kQueueMinL = 2;
 constexpr int kQueueMaxL = 8;
 constexpr int kQueueCap = 128;  // ring capacity: at most 63 carried over plus one chunk of 64
 // Layers above kQueueMaxL run the staged kernel (pruned, factor in LDS) where its solves outweigh
@@ -868,6 +881,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LayerMinWav
     int* __restrict__ queue = s_queue[wave];
     auto scan_queue = [&](auto&& replay, auto&& worst_now) -> bool {
         int qhead = 0, qlen = 0;
+        const __amdgpu_buffer_rsrc_t g_rsrc = GramRsrc(p.gram.G, ld);
+        const __amdgpu_buffer_rsrc_t gs_rsrc = GramRsrc(p.Gs, ld);
         // Exact evaluation of the first n queued candidates, one per lane, each with its own
         // parent's state.
         auto flush = [&](int n) -> bool {
@@ -888,12 +903,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LayerMinWav
 #pragma unroll
             for (int q = 0; q < kCodeWords; ++q)
                 cwl[q] = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(hl << 2, static_cast<int>(cw[q])));
+            const uint32_t kb4 = (k + static_cast<uint32_t>(offL)) * 4u;
 #pragma unroll
             for (int t = 0; t < L; ++t) {
-                const int code = static_cast<int>((cwl[t >> 2] >> (8 * (t & 3))) & 0xFFu);
-                const float* row = (LR && t == 0) ? p.gram.G0S + static_cast<int64_t>(rootl) * ld + offL
-                                                  : p.gram.G + static_cast<int64_t>(p.gram.off[t] + code) * ld + offL;
-                A[t] = row[k];
+                const uint32_t code = (cwl[t >> 2] >> (8 * (t & 3))) & 0xFFu;
+                if (LR && t == 0) {
+                    A[t] = p.gram.G0S[static_cast<int64_t>(rootl) * ld + offL + k];
+                } else {
+                    const uint32_t f = static_cast<uint32_t>(p.gram.off[t]) + code;
+                    A[t] = GramLd(g_rsrc, f * static_cast<uint32_t>(ld) * 4u + kb4, 0u);
+                }
             }
             const float alpha = p.gdiag[offL + k];
             const float gamma = xCi[offL + k];
@@ -918,24 +937,27 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LayerMinWav
             const float E_old = rec[0];
             const float kb = rec[rc.kb], cq = rec[rc.cq];
         const float k1 = L >= prune::kDiagMinL ? rec[rc.k1] : 0.0f, k2 = L >= prune::kDiagMinL ? rec[rc.k2] : 0.0f;
-            // Gs rows of the slot's prefix codewords (the large root's prefix 0: G0S(root, .),
-            // scaled by sw0[root]), ahat_t = a_t * isw_t and the diagonal split's c_t.
-            const float* rows[L];
+            // Gs rows of the slot's prefix codewords (byte offsets into Gs; the large root's
+            // prefix 0: G0S(root, .), scaled by sw0[root]), ahat_t = a_t * isw_t and the diagonal
+            // split's c_t.
+            uint32_t rowb[L];
+            const float* row0 = nullptr;
             float ahat[L], cdg[L];
             float sw0 = 1.0f;
 #pragma unroll
             for (int t = 0; t < L; ++t) {
                 float isw_t;
+                rowb[t] = 0;
                 if (LR && t == 0) {
                     const uint32_t root = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(rootw), h));
-                    rows[t] = p.gram.G0S + static_cast<int64_t>(root) * ld + offL;
+                    row0 = p.gram.G0S + static_cast<int64_t>(root) * ld + offL;
                     isw_t = p.isw0[root];
                     sw0 = p.sw0[root];
                 } else {
                     const uint32_t word =
                         static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(cw[t >> 2]), h));
-                    const int f = p.gram.off[t] + static_cast<int>((word >> (8 * (t & 3))) & 0xFFu);
-                    rows[t] = p.Gs + static_cast<int64_t>(f) * ld + offL;
+                    const uint32_t f = static_cast<uint32_t>(p.gram.off[t]) + ((word >> (8 * (t & 3))) & 0xFFu);
+                    rowb[t] = f * static_cast<uint32_t>(ld) * 4u;
                     isw_t = p.isw[f];
                 }
                 ahat[t] = rec[rc.coef + t] * isw_t;
@@ -945,10 +967,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LayerMinWav
             auto keep_of = [&](int j, float gp) -> bool {
                 const uint32_t k = static_cast<uint32_t>(lane + kWave * j);
                 const bool act = FULL || static_cast<int>(k) < K;
+                const uint32_t kb4 = (k + static_cast<uint32_t>(offL)) * 4u;
                 float et = 0.0f, b2 = 0.0f, xs = 0.0f;
 #pragma unroll
                 for (int t = 0; t < L; ++t) {
-                    float bt = act ? rows[t][k] : 0.0f;
+                    float bt = act ? ((LR && t == 0) ? row0[k] : GramLd(gs_rsrc, kb4, rowb[t])) : 0.0f;
                     if (LR && t == 0) bt = bt * sw0;
                     et = t == 0 ? bt * ahat[t] : __builtin_fmaf(bt, ahat[t], et);
                     b2 = t == 0 ? bt * bt : __builtin_fmaf(bt, bt, b2);
