@@ -35,6 +35,11 @@ __device__ __forceinline__ float ReadLane(float v, int l) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
 }
 
+// A value every lane holds (an LDS broadcast read), moved to a scalar register.
+__device__ __forceinline__ float Uniform(float v) {
+    return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v)));
+}
+
 template <int CTRL>
 __device__ __forceinline__ float Dpp(float v) {
     return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, 0xF, 0xF, false));
@@ -528,13 +533,19 @@ __device__ __forceinline__ void EvalStaged(const float* f, const float (&A)[L], 
 }
 
 // The queue kernel's per-slot state in LDS: EvalStaged's factor layout (record dwords 1 ..
-// L(L+3)/2: R(0..c, c) then RN(1/R(c,c)) for c < L), then a_old[L], then E_old. The stride is odd,
-// so the slots that different lanes read at one offset sit in different LDS banks.
+// L(L+3)/2: R(0..c, c) then RN(1/R(c,c)) for c < L), then a_old[L], then E_old, then the pruning
+// bound's per-slot operands: ahat[L] (a_t * isw_t), kb, cq and the large root's sw0[root]. The
+// stride is odd, so the slots that different lanes read at one offset sit in different LDS banks.
 template <int L>
 struct QStage {
     static constexpr int kRWords = L * (L + 3) / 2;
     static constexpr int kEold = kRWords + L;
-    static constexpr int kStride = (kEold + 1) | 1;
+    static constexpr int kAhat = kEold + 1;
+    static constexpr int kKb = kAhat + L;
+    static constexpr int kCq = kKb + 1;
+    static constexpr int kSw0 = kCq + 1;
+    static constexpr int kBoundWords = L + 3;  // ahat[L], kb, cq, sw0
+    static constexpr int kStride = (kSw0 + 1) | 1;
     // dynamic LDS of one workgroup for beam width Hb
     static constexpr size_t Bytes(int Hb) {
         return sizeof(float) * static_cast<size_t>(kBeamWavesPerBlock) * static_cast<size_t>(Hb) * kStride;
@@ -728,6 +739,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LayerMinWav
             const float* src = recs_in + h * rc.stride;
             stage[h * QStage<L>::kStride + o] =
                 o < QStage<L>::kRWords ? src[1 + o] : (o < QStage<L>::kEold ? src[rc.coef + o - QStage<L>::kRWords] : src[0]);
+        }
+        // the bound's operands: one pass over all slots here instead of a dependent isw[f] gather
+        // per slot in the scan
+        for (int q = lane; q < curH * QStage<L>::kBoundWords; q += kWave) {
+            const int h = q / QStage<L>::kBoundWords, o = q - h * QStage<L>::kBoundWords;
+            const float* src = recs_in + h * rc.stride;
+            float val;
+            if (o < L) {
+                const float isw_t = (LR && o == 0) ? p.isw0[reinterpret_cast<const uint32_t*>(src)[rc.root]]
+                                                   : p.isw[p.gram.off[o] + CodeAt(src, rc.code, o)];
+                val = src[rc.coef + o] * isw_t;
+            } else if (o == L) {
+                val = src[rc.kb];
+            } else if (o == L + 1) {
+                val = src[rc.cq];
+            } else {
+                val = LR ? p.sw0[reinterpret_cast<const uint32_t*>(src)[rc.root]] : 1.0f;
+            }
+            stage[h * QStage<L>::kStride + QStage<L>::kAhat + o] = val;
         }
         bool dok = lane < curH;
         if (dok) {
@@ -932,59 +962,53 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LayerMinWav
             qlen -= n;
             return replay(ok && act, e, hl * K + static_cast<int>(k));
         };
+        static_assert(kQueueMaxL < prune::kDiagMinL, "the queue scan uses the Frobenius bound only");
         for (int h = 0; h < curH; ++h) {
-            const float* rec = recs_in + h * rc.stride;
-            const float E_old = rec[0];
-            const float kb = rec[rc.kb], cq = rec[rc.cq];
-        const float k1 = L >= prune::kDiagMinL ? rec[rc.k1] : 0.0f, k2 = L >= prune::kDiagMinL ? rec[rc.k2] : 0.0f;
-            // Gs rows of the slot's prefix codewords (byte offsets into Gs; the large root's
-            // prefix 0: G0S(root, .), scaled by sw0[root]), ahat_t = a_t * isw_t and the diagonal
-            // split's c_t.
+            // The slot's bound operands, staged in LDS (wave-uniform reads).
+            const float* sp = stage + h * QStage<L>::kStride;
+            const float E_old = Uniform(sp[QStage<L>::kEold]);
+            const float kb = Uniform(sp[QStage<L>::kKb]), cq = Uniform(sp[QStage<L>::kCq]);
+            float ahat[L];
+#pragma unroll
+            for (int t = 0; t < L; ++t) ahat[t] = sp[QStage<L>::kAhat + t];
+            const float sw0 = LR ? sp[QStage<L>::kSw0] : 1.0f;
+            // Gs row byte offsets of the slot's prefix codewords (the large root's prefix 0:
+            // G0S(root, .), scaled by sw0[root] in the bound).
             uint32_t rowb[L];
             const float* row0 = nullptr;
-            float ahat[L], cdg[L];
-            float sw0 = 1.0f;
 #pragma unroll
             for (int t = 0; t < L; ++t) {
-                float isw_t;
                 rowb[t] = 0;
                 if (LR && t == 0) {
                     const uint32_t root = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(rootw), h));
                     row0 = p.gram.G0S + static_cast<int64_t>(root) * ld + offL;
-                    isw_t = p.isw0[root];
-                    sw0 = p.sw0[root];
                 } else {
                     const uint32_t word =
                         static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(cw[t >> 2]), h));
                     const uint32_t f = static_cast<uint32_t>(p.gram.off[t]) + ((word >> (8 * (t & 3))) & 0xFFu);
                     rowb[t] = f * static_cast<uint32_t>(ld) * 4u;
-                    isw_t = p.isw[f];
                 }
-                ahat[t] = rec[rc.coef + t] * isw_t;
-                cdg[t] = prune::DiagCoef(rec[Rec::Rinv(t)], isw_t);
             }
-            // Whether chunk j's candidate survives the bound (true when it may enter the top-H).
-            auto keep_of = [&](int j, float gp) -> bool {
+            // b_t = Gs(f_t, k) of chunk j's codeword k = lane + 64 j. Reads past the Gram return 0
+            // (buffer range check); a codeword beyond K is masked by the caller.
+            auto gs_of = [&](int j, int t) -> float {
                 const uint32_t k = static_cast<uint32_t>(lane + kWave * j);
-                const bool act = FULL || static_cast<int>(k) < K;
-                const uint32_t kb4 = (k + static_cast<uint32_t>(offL)) * 4u;
-                float et = 0.0f, b2 = 0.0f, xs = 0.0f;
+                if (LR && t == 0) return (FULL || static_cast<int>(k) < K) ? row0[k] * sw0 : 0.0f;
+                return GramLd(gs_rsrc, (k + static_cast<uint32_t>(offL)) * 4u, rowb[t]);
+            };
+            // Whether chunk j's candidate survives the bound (true when it may enter the top-H):
+            // eta~ = sum_t b_t ahat_t and b2 = sum_t b_t^2 by fma.
+            auto keep_b = [&](int j, const float (&b)[L], float gp) -> bool {
+                const bool act = FULL || lane + kWave * j < K;
+                float et = 0.0f, b2 = 0.0f;
 #pragma unroll
                 for (int t = 0; t < L; ++t) {
-                    float bt = act ? ((LR && t == 0) ? row0[k] : GramLd(gs_rsrc, kb4, rowb[t])) : 0.0f;
-                    if (LR && t == 0) bt = bt * sw0;
-                    et = t == 0 ? bt * ahat[t] : __builtin_fmaf(bt, ahat[t], et);
-                    b2 = t == 0 ? bt * bt : __builtin_fmaf(bt, bt, b2);
-                    if (L >= prune::kDiagMinL) {
-                        const float ut = cdg[t] * bt;
-                        xs = t == 0 ? ut * ut : __builtin_fmaf(ut, ut, xs);
-                    }
+                    et = t == 0 ? b[t] * ahat[t] : __builtin_fmaf(b[t], ahat[t], et);
+                    b2 = t == 0 ? b[t] * b[t] : __builtin_fmaf(b[t], b[t], b2);
                 }
-                return act && !(L >= prune::kDiagMinL ? prune::Prunable2(alc[j], b2, xs, gam[j] - et, kb, k1, k2, cq, gp)
-                                               : prune::Prunable(alc[j], b2, gam[j] - et, kb, cq, gp));
+                return act && !prune::Prunable(alc[j], b2, gam[j] - et, kb, cq, gp);
             };
-            auto enqueue = [&](int j, bool keep) -> bool {
-                const uint64_t km = Ballot(keep);
+            auto enqueue = [&](int j, bool keep, uint64_t km) -> bool {
                 if (keep) {
                     const int pos = (qhead + qlen + __popcll(km & ((1ull << lane) - 1ull))) & (kQueueCap - 1);
                     queue[pos] = (h << 8) | (lane + kWave * j);
@@ -992,33 +1016,54 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LayerMinWav
                 qlen += __popcll(km);
                 return qlen < kWave || flush(kWave);
             };
-            float gp = 0.0f;
             const float W0 = worst_now();
             if (!(W0 < kInfF)) {
                 // A slot is still empty: chunk by chunk, each tested against the worst after the
                 // previous one was evaluated.
                 for (int j = 0; j < nch; ++j) {
                     const bool act = FULL || lane + kWave * j < K;
+                    float gp = 0.0f;
                     const bool bounded = kb < kInfF && prune::ParentGap(E_old, worst_now(), gp);
                     bool keep = act;
 #pragma unroll
-                    for (int jj = 0; jj < kMaxChunks; ++jj)
-                        if (jj == j && bounded) keep = keep_of(jj, gp);
-                    if (!enqueue(j, keep)) return false;
+                    for (int jj = 0; jj < kMaxChunks; ++jj) {
+                        if (jj == j && bounded) {
+                            float b[L];
+#pragma unroll
+                            for (int t = 0; t < L; ++t) b[t] = gs_of(jj, t);
+                            keep = keep_b(jj, b, gp);
+                        }
+                    }
+                    if (!enqueue(j, keep, Ballot(keep))) return false;
                 }
             } else {
-                // The whole slot against the worst at its start (it only falls from there).
-                const bool bounded = kb < kInfF && prune::ParentGap(E_old, W0, gp);
-                bool keep[kMaxChunks];
+                // The whole slot against the worst at its start (it only falls from there). Every
+                // chunk's values are read in one go and tested without branches, so the slot costs
+                // one memory round trip; the tests are discarded when the slot is not bounded.
+                float b[kMaxChunks][L];
 #pragma unroll
                 for (int j = 0; j < kMaxChunks; ++j) {
                     if (!FULL && j >= nch) continue;
-                    keep[j] = bounded ? keep_of(j, gp) : (FULL || lane + kWave * j < K);
+#pragma unroll
+                    for (int t = 0; t < L; ++t) b[j][t] = gs_of(j, t);
+                }
+                float gp = 0.0f;
+                const bool bounded = kb < kInfF && prune::ParentGap(E_old, W0, gp);
+                // All four ballots before the first enqueue: the tests cannot then be moved past
+                // a flush, where their operands would hold registers.
+                bool keep[kMaxChunks];
+                uint64_t km[kMaxChunks];
+#pragma unroll
+                for (int j = 0; j < kMaxChunks; ++j) {
+                    if (!FULL && j >= nch) continue;
+                    const bool kt = keep_b(j, b[j], gp);
+                    keep[j] = bounded ? kt : (FULL || lane + kWave * j < K);
+                    km[j] = Ballot(keep[j]);
                 }
 #pragma unroll
                 for (int j = 0; j < kMaxChunks; ++j) {
                     if (!FULL && j >= nch) continue;
-                    if (!enqueue(j, keep[j])) return false;
+                    if (!enqueue(j, keep[j], km[j])) return false;
                 }
             }
         }
