@@ -1748,10 +1748,19 @@ template <int L>
 constexpr int WbStride() {
     return StagedWords<L>() | 1;  // odd: the lanes of a round read distinct banks
 }
+// The windowed queue scan stages kStagedWin slots at a time: factor, a_old and error per slot (odd
+// stride: the lanes of a group read distinct banks), then ahat and c per slot, after the FIFO.
+constexpr int kStagedWin = 8;
+template <int L>
+constexpr int StagedQStride() {
+    return (StagedWords<L>() + 1) | 1;
+}
 template <int L>
 constexpr int StagedWaveWords() {
-    return kMaxK + StagedWords<L>() + 2 * L > kWbSlots * WbStride<L>() ? kMaxK + StagedWords<L>() + 2 * L
-                                                                      : kWbSlots * WbStride<L>();
+    constexpr int scan = kMaxK + StagedWords<L>() + 2 * L;
+    constexpr int win = kQueueCap + kStagedWin * (StagedQStride<L>() + 2 * L);
+    constexpr int wb = kWbSlots * WbStride<L>();
+    return scan > win ? (scan > wb ? scan : wb) : (win > wb ? win : wb);
 }
 
 // Waves per SIMD asked of the register allocator: the kernel needs about 5L + 60 VGPRs, so 4 waves
@@ -1807,6 +1816,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(StagedMinWa
     float* __restrict__ fac = wbuf + kMaxK;
     float* __restrict__ cf = fac + StagedWords<L>();  // per slot: ahat[L], then c[L]
 
+    // 32-bit byte offsets from one base (H <= 5120, so H * ld * 4 < 2^32): the loads take the
+    // scalar-base form with one VGPR offset instead of a 64-bit address per row.
+    auto ld32 = [](const float* base, uint32_t elem) {
+        return *reinterpret_cast<const float*>(reinterpret_cast<const char*>(base) + (elem << 2));
+    };
     // Evaluates slot h's candidates and replays them into the top-H (scan order: slot, then code).
     // Returns false when the replay asks for the slow pass. While a slot of the top-H is still
     // empty the chunks are listed one at a time without a bound, so the worst can become finite
@@ -1858,11 +1872,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(StagedMinWa
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         }
-        // 32-bit byte offsets from one base (H <= 5120, so H * ld * 4 < 2^32): the loads take the
-        // scalar-base form with one VGPR offset instead of a 64-bit address per row.
-        auto ld32 = [](const float* base, uint32_t elem) {
-            return *reinterpret_cast<const float*>(reinterpret_cast<const char*>(base) + (elem << 2));
-        };
         auto gv = [&](int t, uint32_t k) { return (LR && t == 0) ? ld32(row0, k) : ld32(p.gram.G, rowo[t] + k); };
         auto gs = [&](int t, uint32_t k) { return (LR && t == 0) ? ld32(row0, k) * sw0 : ld32(p.Gs, rowo[t] + k); };
         const float kb = rec[rc.kb], cq = rec[rc.cq];
@@ -1963,12 +1972,210 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(StagedMinWa
         return true;
     };
 
+    // The windowed queue scan (fast pass with pruning): slots are taken kStagedWin at a time. A
+    // window's factors, coefficients and errors are staged in LDS, its slots are bound-tested in
+    // scan order against the worst of that moment, and the survivors (slot, codeword) of all its
+    // slots go into one FIFO, evaluated exactly 64 at a time (each lane reading its own slot's
+    // factor) and replayed in scan order; the window's last survivors are evaluated before the
+    // next window is staged. The worst only falls between a test and the replay, so a pruned
+    // candidate stays one the reference rejects.
+    auto scan_windows = [&](auto&& replay, auto&& worst_now) -> bool {
+        int* __restrict__ queue = reinterpret_cast<int*>(wbuf);
+        float* __restrict__ wst = wbuf + kQueueCap;                    // factor, a_old, E_old per slot
+        float* __restrict__ wcf = wst + kStagedWin * StagedQStride<L>();  // ahat[L], c[L] per slot
+        int qhead = 0, qlen = 0, base = 0;
+        uint64_t diag_mask = 0;
+        auto flush = [&](int n) -> bool {
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            const bool act = lane < n;
+            const int ent = act ? queue[(qhead + lane) & (kQueueCap - 1)] : 0;
+            const int sl = ent >> 8;
+            const int hl = base + sl;
+            const uint32_t k = static_cast<uint32_t>(ent & 0xFF);
+            const float* f = wst + sl * StagedQStride<L>();
+            const float E_old = f[StagedWords<L>()];
+            const bool diag_ok = ((diag_mask >> sl) & 1ull) != 0ull;
+            const uint32_t rootl =
+                LR ? static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(hl << 2, static_cast<int>(rootw))) : 0u;
+            uint32_t cwl[kCodeWords];
+#pragma unroll
+            for (int q = 0; q < kCodeWords; ++q)
+                cwl[q] = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(hl << 2, static_cast<int>(cw[q])));
+            float A[L];
+#pragma unroll
+            for (int t = 0; t < L; ++t) {
+                if (LR && t == 0) {
+                    A[t] = p.gram.G0S[static_cast<int64_t>(rootl) * ld + offL + k];
+                } else {
+                    const uint32_t fi = static_cast<uint32_t>(p.gram.off[t]) + ((cwl[t >> 2] >> (8 * (t & 3))) & 0xFFu);
+                    A[t] = ld32(p.gram.G, fi * static_cast<uint32_t>(ld) + static_cast<uint32_t>(offL) + k);
+                }
+            }
+            const float alpha = p.gdiag[offL + k];
+            const float gamma = xCi[offL + k];
+            float y[L], v[L], denom, a_last, e;
+            bool ok, safe = true;
+            if (LR) {
+                EvalStaged<L, 2>(f, A, E_old, alpha, gamma, y, v, e, denom, a_last, ok, safe);
+            } else {
+                bool ieee = Ballot(act && !diag_ok) != 0ull;
+                if (!ieee) {
+                    EvalStaged<L, 1>(f, A, E_old, alpha, gamma, y, v, e, denom, a_last, ok, safe);
+                    ieee = Ballot(act && !safe) != 0ull;
+                }
+                if (ieee) EvalStaged<L, 0>(f, A, E_old, alpha, gamma, y, v, e, denom, a_last, ok, safe);
+            }
+            qhead = (qhead + n) & (kQueueCap - 1);
+            qlen -= n;
+            return replay(ok && act, e, hl * K + static_cast<int>(k));
+        };
+        for (base = 0; base < curH; base += kStagedWin) {
+            const int nw = min(kStagedWin, curH - base);
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            {
+                // the window's factor columns with 1/diag, coefficients and error
+                constexpr int kW1 = StagedWords<L>() + 1;
+                for (int q = lane; q < nw * kW1; q += kWave) {
+                    const int hw = q / kW1, o = q - hw * kW1;
+                    const float* src = recs_in + (base + hw) * rc.stride;
+                    wst[hw * StagedQStride<L>() + o] =
+                        o < kRWords ? src[1 + o] : (o < StagedWords<L>() ? src[rc.coef + o - kRWords] : src[0]);
+                }
+                // ahat_t = a_t * isw_t and the diagonal split's c_t of every window slot
+                for (int q = lane; q < nw * L; q += kWave) {
+                    const int hw = q / L, t = q - hw * L;
+                    const float* src = recs_in + (base + hw) * rc.stride;
+                    const float isw_t = (LR && t == 0) ? p.isw0[reinterpret_cast<const uint32_t*>(src)[rc.root]]
+                                                       : p.isw[p.gram.off[t] + CodeAt(src, rc.code, t)];
+                    wcf[hw * 2 * L + t] = src[rc.coef + t] * isw_t;
+                    wcf[hw * 2 * L + L + t] = prune::DiagCoef(src[Rec::Rinv(t)], isw_t);
+                }
+                bool dok = lane < nw;
+                if (dok) {
+                    const float* src = recs_in + (base + lane) * rc.stride;
+#pragma unroll
+                    for (int r = 0; r < L; ++r) dok = dok && DiagFastOk(src[Rec::R(r, r)]);
+                }
+                diag_mask = Ballot(dok);
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            for (int hw = 0; hw < nw; ++hw) {
+                const int h = base + hw;
+                const float* rec = recs_in + h * rc.stride;
+                const float E_old = rec[0];
+                const float kb = rec[rc.kb], cq = rec[rc.cq], k1 = rec[rc.k1], k2 = rec[rc.k2];
+                const float* cfh = wcf + hw * 2 * L;
+                uint32_t rowo[L];
+                const float* row0 = nullptr;
+                float sw0 = 1.0f;
+#pragma unroll
+                for (int t = 0; t < L; ++t) {
+                    if (LR && t == 0) {
+                        const uint32_t root = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(rootw), h));
+                        row0 = p.gram.G0S + static_cast<int64_t>(root) * ld + offL;
+                        rowo[0] = 0;
+                        sw0 = p.sw0[root];
+                    } else {
+                        const uint32_t word =
+                            static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(cw[t >> 2]), h));
+                        const uint32_t fi = static_cast<uint32_t>(p.gram.off[t]) + ((word >> (8 * (t & 3))) & 0xFFu);
+                        rowo[t] = fi * static_cast<uint32_t>(ld) + static_cast<uint32_t>(offL);
+                    }
+                }
+                auto gsw = [&](int t, uint32_t k) {
+                    return (LR && t == 0) ? ld32(row0, k) * sw0 : ld32(p.Gs, rowo[t] + k);
+                };
+                auto test = [&](const float (&b)[L], float alj, float gmj, float gp) -> bool {
+                    float et = 0.0f, b2 = 0.0f, xs = 0.0f;
+#pragma unroll
+                    for (int t = 0; t < L; ++t) {
+                        const float bt = b[t];
+                        const float ut = cfh[L + t] * bt;
+                        et = t == 0 ? bt * cfh[t] : __builtin_fmaf(bt, cfh[t], et);
+                        b2 = t == 0 ? bt * bt : __builtin_fmaf(bt, bt, b2);
+                        xs = t == 0 ? ut * ut : __builtin_fmaf(ut, ut, xs);
+                    }
+                    return !prune::Prunable2(alj, b2, xs, gmj - et, kb, k1, k2, cq, gp);
+                };
+                auto enqueue = [&](int j, bool keep, uint64_t km) -> bool {
+                    if (keep) {
+                        const int pos = (qhead + qlen + __popcll(km & ((1ull << lane) - 1ull))) & (kQueueCap - 1);
+                        queue[pos] = (hw << 8) | (lane + kWave * j);
+                    }
+                    qlen += __popcll(km);
+                    return qlen < kWave || flush(kWave);
+                };
+
+                const float W0 = worst_now();
+                if (!FULL || !(W0 < kInfF)) {
+                    // A slot of the top-H is still empty (or a partial layer): chunk by chunk,
+                    // each tested against the worst after the previous one was queued.
+#pragma unroll 1
+                    for (int j = 0; j < nch; ++j) {
+                        const bool act = FULL || lane + kWave * j < K;
+                        float gp = 0.0f;
+                        const bool bounded = kb < kInfF && prune::ParentGap(E_old, worst_now(), gp);
+                        bool keep = act;
+                        if (bounded) {
+                            const uint32_t k = static_cast<uint32_t>(lane + kWave * j);
+                            float b[L];
+#pragma unroll
+                            for (int t = 0; t < L; ++t) b[t] = act ? gsw(t, k) : 0.0f;
+                            // chunk j's alc and gamma read again (an index into alc/gam, j being
+                            // a loop variable here, would put them in scratch)
+                            const float alj = (act ? p.gdiag[offL + k] : 0.0f) * prune::kAlphaScale;
+                            const float gmj = act ? xCi[offL + k] : 0.0f;
+                            keep = act && test(b, alj, gmj, gp);
+                        }
+                        if (!enqueue(j, keep, Ballot(keep))) return false;
+                    }
+                } else {
+                    // The whole slot against the worst at its start (it only falls from there),
+                    // two chunks per step (a scheduling barrier keeps the second pair's reads
+                    // from being hoisted into the first, where they would hold registers).
+                    float gp = 0.0f;
+                    const bool bounded = kb < kInfF && prune::ParentGap(E_old, W0, gp);
+#pragma unroll
+                    for (int j0 = 0; j0 < kMaxChunks; j0 += 2) {
+                        __builtin_amdgcn_sched_barrier(0);
+                        bool keep[2];
+                        uint64_t km[2];
+                        if (bounded) {
+                            float b[2][L];
+#pragma unroll
+                            for (int jj = 0; jj < 2; ++jj) {
+#pragma unroll
+                                for (int t = 0; t < L; ++t) b[jj][t] = gsw(t, static_cast<uint32_t>(lane + kWave * (j0 + jj)));
+                            }
+#pragma unroll
+                            for (int jj = 0; jj < 2; ++jj) keep[jj] = test(b[jj], alc[j0 + jj], gam[j0 + jj], gp);
+                        } else {
+                            keep[0] = keep[1] = true;
+                        }
+                        km[0] = Ballot(keep[0]);
+                        km[1] = Ballot(keep[1]);
+                        if (!enqueue(j0, keep[0], km[0])) return false;
+                        if (!enqueue(j0 + 1, keep[1], km[1])) return false;
+                    }
+                }
+            }
+            if (qlen > 0 && !flush(qlen)) return false;
+        }
+        return true;
+    };
+
     float s_err;
     int s_cand;
     bool flagged = false;
     SelectTopH<true, BEST, BEST>(  // errors clamped at zero (EvalCand)
         Hb, lane,
         [&](auto&& replay, auto slow_tag, auto&& worst_now) {
+            if constexpr (!decltype(slow_tag)::value) {
+                if (prune_on) return scan_windows(replay, worst_now);
+            }
             for (int h = 0; h < curH; ++h) {
                 if (!process(h, replay, slow_tag, worst_now)) return false;
             }
