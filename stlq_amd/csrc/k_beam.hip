@@ -671,10 +671,8 @@ constexpr int kVStateMaxL = 3;
 constexpr int kQueueMinL = 2;
 constexpr int kQueueMaxL = 8;
 constexpr int kQueueCap = 128;  // ring capacity: at most 63 carried over plus one chunk of 64
-// Layers above kQueueMaxL run the staged kernel (pruned, factor in LDS) where its solves outweigh
-// its per-slot staging and bound; the large-root beam (32 slots in the streaming encode) keeps the
-// unpruned per-slot kernel below layer kLrStagedMinL, where that measured faster.
-constexpr int kLrStagedMinL = 14;
+// Layers above kQueueMaxL run the staged kernel (pruned, factors staged in LDS a window of slots
+// at a time), the full-precomp and the large-root beam alike.
 
 // BEST: the best-first pass (LayerArgs::flags). Its input records are rank-indexed, so slots are
 // scanned in ascending error order, and so are its output records. A vector flagged by an earlier
@@ -1252,24 +1250,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LayerMinWav
     }
 }
 
-// Layers 1-2, and the large-root beam's layers kQueueMaxL+1 .. kLrStagedMinL-1 (where a candidate's
-// solve costs little more than its bound and the staging of the pruned kernels): every candidate of
-// every slot is evaluated exactly, four chunks of 64 at a time with the slot's factor in SGPRs, and
-// the slots are written back by the lanes that hold them, with their pruning constants for the
-// later layers. LR selects the large-root cross-term source and reciprocal solves.
-// FULL: the layer has exactly 256 codewords (no partial chunk).
-// Minimum waves per SIMD requested from the register allocator, per layer (measured):
-//  * layers >= 11 at 4 waves (<= 128 VGPRs), 5 for the large root: left alone the allocator
-//    gives them 2-3 waves, or 1 at layer 16 (> 256 VGPRs); the M=16, beam-8 encode ran 9% faster
-//    and the large-root 16-layer beam-32 encode 18% faster (5 waves there: another 1%);
-//  * on the M=8, K=256, beam-16 encode layers 4 and 6 run best at 8 waves and layer 7 at 7 (6 in
-//    the best-first pass, where 80 VGPRs remove its spills), and layer 3 of the best-first pass
-//    at 8 (left alone it takes 65 VGPRs, one over);
-//  * the other layers at the allocator's own choice.
+// Layer 1 (below kQueueMinL, where a candidate's solve costs little more than its bound and the
+// staging of the pruned kernels): every candidate of every slot is evaluated exactly, four chunks
+// of 64 at a time with the slot's factor in SGPRs, and the slots are written back by the lanes that
+// hold them, with their pruning constants for the later layers. LR selects the large-root
+// cross-term source and reciprocal solves. FULL: the layer has exactly 256 codewords (no partial
+// chunk). The register allocator picks the occupancy.
 template <int L, bool LR, bool BEST>
 constexpr int DeepMinWaves() {
-    return L >= 11 ? (LR ? 5 : 4)
-                   : (LR ? 1 : ((L == 4 || L == 6 || (BEST && L == 3)) ? 8 : (L == 7 ? (BEST ? 6 : 7) : 1)));
+    return 1;
 }
 
 
@@ -2413,8 +2402,6 @@ hipError_t LaunchL(bool lr, const LayerArgs& a, hipStream_t s) {
         return LaunchWith<L, DeepSel>(lr, a, s);
     } else if constexpr (L <= kQueueMaxL) {
         return LaunchWith<L, QueueSel>(lr, a, s);
-    } else if constexpr (L < kLrStagedMinL) {
-        return lr ? LaunchWith<L, DeepSel>(true, a, s) : LaunchWith<L, StagedSel>(false, a, s);
     } else {
         return LaunchWith<L, StagedSel>(lr, a, s);
     }
