@@ -1731,6 +1731,22 @@ int LargeRootTile(stlq_mi355_ctx* c, const float* dX, int64_t nt, int Hb, int ro
         ra.root_slots = root_mode == 1 ? 1 : Hb;
     }
     HIP_TRY(rec(2));
+    // Best-first pass over the expansion (as RunBeam's): with one root slot per vector the seed is
+    // trivially in rank order, and every small layer must be full (the pass's kernels are built
+    // for K = 256). Flagged vectors are re-seeded and re-run in the reference order below.
+    bool best = m >= 2 && ra.root_slots == 1 && BestFirstBeam();
+    for (int L = 1; L < m && best; ++L) best = c->lr_h[L] == kMaxK;
+    if (best) {
+        HIP_TRY(c->bf_flags.Ensure(static_cast<size_t>(nt)));
+        HIP_TRY(c->bf_list.Ensure(static_cast<size_t>(nt) * 4));
+        HIP_TRY(c->bf_count.Ensure(8));
+        if (!c->bf_host && !c->noalloc)
+            HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&c->bf_host), 8, hipHostMallocDefault));
+        HIP_TRY(LaunchFill8(c->bf_flags.as<uint8_t>(), 0, nt, s));
+        HIP_TRY(LaunchFill8(c->bf_count.as<uint8_t>(), 0, (c->bf_reset || c->noalloc) ? 8 : 4, s));
+        c->bf_reset = c->noalloc;
+        c->bf_used = !c->noalloc;
+    }
     HIP_TRY(LaunchRootSeed(ra, s));
     if (te) {
         te->lay[0] = te->e[2];
@@ -1759,21 +1775,40 @@ int LargeRootTile(stlq_mi355_ctx* c, const float* dX, int64_t nt, int Hb, int ro
     a.codes_out = d_codes;
     a.cluster_out = d_cluster;
     a.best_err = d_best;
-    int cur = 0;
-    for (int L = 1; L < m; ++L) {
-        a.in = StateOf(c, cur);
-        a.out = StateOf(c, cur ^ 1);
-        a.K = c->lr_h[L];
-        a.offL = c->soff[L];
-        a.is_last = (L == m - 1);
-        HIP_TRY(LaunchBeamLayer(L, true, a, s));
-        cur ^= 1;
-        if (te) {
-            ++te->beam_launches;
-            te->lay[L + 1] = c->NextEvent();
-            te->layers = L + 1;
-            HIP_TRY(hipEventRecord(te->lay[L + 1], s));
+    a.flags = best ? c->bf_flags.as<uint8_t>() : nullptr;
+    auto expand = [&](bool timed) -> int {
+        int cur = 0;
+        for (int L = 1; L < m; ++L) {
+            a.in = StateOf(c, cur);
+            a.out = StateOf(c, cur ^ 1);
+            a.K = c->lr_h[L];
+            a.offL = c->soff[L];
+            a.is_last = (L == m - 1);
+            HIP_TRY(LaunchBeamLayer(L, true, a, s));
+            cur ^= 1;
+            if (te) ++te->beam_launches;
+            if (te && timed) {
+                te->lay[L + 1] = c->NextEvent();
+                te->layers = L + 1;
+                HIP_TRY(hipEventRecord(te->lay[L + 1], s));
+            }
         }
+        return STLQ_MI355_OK;
+    };
+    RC_TRY(expand(true));
+    if (best) {
+        // the flagged vectors: seeded again and expanded in the reference order, one wave per
+        // listed vector (grids sized for all nt; waves past the list's length exit at once)
+        int* counts = c->bf_count.as<int>();
+        HIP_TRY(LaunchCollectFlagged(c->bf_flags.as<uint8_t>(), nt, c->bf_list.as<int>(), counts, s));
+        ra.list = c->bf_list.as<int>();
+        ra.list_n = counts;
+        HIP_TRY(LaunchRootSeed(ra, s));
+        a.flags = nullptr;
+        a.list = ra.list;
+        a.list_n = counts;
+        RC_TRY(expand(false));
+        if (!c->noalloc) HIP_TRY(hipMemcpyAsync(c->bf_host, counts, 8, hipMemcpyDeviceToHost, s));
     }
     HIP_TRY(rec(3));
     if (!refine || !d_a || !d_cost) {

@@ -89,6 +89,10 @@ struct RootArgs {
     float* best_err = nullptr;
     uint32_t* cluster_out = nullptr;
     int is_last = 0;
+    // Seed over a list (the best-first pass's re-run, as LayerArgs::list): wave w seeds vector
+    // list[w] for w < *list_n into beam-state index w. null: wave w seeds vector w.
+    const int* list = nullptr;
+    const int* list_n = nullptr;
 };
 
 // ---- launchers (each defined in the .hip file that holds the kernel) ----

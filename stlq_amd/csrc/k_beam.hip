@@ -1585,8 +1585,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DeepMinWave
 __global__ __launch_bounds__(256) void RootSeedKernel(RootArgs p) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * kBeamWavesPerBlock + wave;
-    if (i >= p.n) return;
+    // i: the vector; w: its beam-state index (i, or its position in the re-run list)
+    const int64_t w = static_cast<int64_t>(blockIdx.x) * kBeamWavesPerBlock + wave;
+    int64_t i = w;
+    if (p.list) {
+        if (w >= *p.list_n) return;
+        i = p.list[w];
+    } else if (w >= p.n) {
+        return;
+    }
     const int m = p.m, Hb = p.Hb, rs = p.root_slots;
     const Rec rc(m);
     const float nx2 = p.nx2[i];
@@ -1637,7 +1644,7 @@ __global__ __launch_bounds__(256) void RootSeedKernel(RootArgs p) {
         bd = prune::FirstBounds(r00, p.sw0[s_cand], a0, p.isw0[s_cand]);
     }
     if (lane < Hb) {
-        float* rec = p.out.rec + (i * Hb + lane) * rc.stride;
+        float* rec = p.out.rec + (w * Hb + lane) * rc.stride;
         rec[0] = seeded ? s_err : kInfF;
         rec[rc.coef] = a0;
         rec[Rec::R(0, 0)] = r00;
@@ -1646,7 +1653,7 @@ __global__ __launch_bounds__(256) void RootSeedKernel(RootArgs p) {
         reinterpret_cast<uint32_t*>(rec)[rc.root] = root;
         rc.PutBounds(rec, bd);
     }
-    if (lane == 0) p.out.curH[i] = curH;
+    if (lane == 0) p.out.curH[w] = curH;
     if (p.is_last) {  // m == 1: the root is the whole code
         const int best = BestSlot(seeded ? s_err : kInfF, curH, lane);
         if (lane == best) {
@@ -2365,9 +2372,10 @@ hipError_t LaunchWith(bool lr, const LayerArgs& a, hipStream_t s) {
     const dim3 block(kWave * kBeamWavesPerBlock);
     const bool full = a.K == kMaxK;
     const unsigned lds = static_cast<unsigned>(KernelSel<L, false, true, false>::DynamicLds(a.Hb));
-    if (lr) {  // the large-root beam always runs in the reference order
-        if (a.flags) return hipErrorInvalidValue;
-        if (full) hipLaunchKernelGGL((KernelSel<L, true, true, false>::kernel), dim3(blocks), block, lds, s, a);
+    if (lr) {  // the large-root beam's best-first pass is built for full layers (K = 256) only
+        if (a.flags && !full) return hipErrorInvalidValue;
+        if (a.flags) hipLaunchKernelGGL((KernelSel<L, true, true, true>::kernel), dim3(blocks), block, lds, s, a);
+        else if (full) hipLaunchKernelGGL((KernelSel<L, true, true, false>::kernel), dim3(blocks), block, lds, s, a);
         else hipLaunchKernelGGL((KernelSel<L, true, false, false>::kernel), dim3(blocks), block, lds, s, a);
     } else if (a.flags) {
         if (full) hipLaunchKernelGGL((KernelSel<L, false, true, true>::kernel), dim3(blocks), block, lds, s, a);

@@ -507,6 +507,57 @@ def test_large_root_bit_exact(ctx, orc, name, seed, n, d, h0, small, Hb, mode):
         assert np.array_equal(cid_g, forced)
 
 
+@pytest.mark.parametrize("case", ["plain", "dup_small", "nan_small"])
+def test_large_root_best_first_equals_reference_order(ctx, orc, monkeypatch, case):
+    """The large-root expansion's best-first pass (one root slot per vector, nearest or forced;
+    full small layers) plus the re-seeded reference-order re-run of the vectors it flags returns
+    the reference order's cluster ids, small codes and errors bit for bit, and the oracle's.
+    dup_small: duplicate small codewords within and across layers (boundary ties, re-runs);
+    nan_small: a small codeword with a NaN entry (NaN candidate errors, re-runs)."""
+    from stlq_amd import workloads
+
+    seed, d, h0, K, ms, Hb, n = 76, 64, 512, 256, 5, 32, 1500
+    mix = workloads.Mixture("desc", d, 256, seed)
+    rng = np.random.default_rng(seed)
+    C0 = mix.sample(5_000_000, h0)
+    Xtr = mix.sample(1_000_000, 3000)
+    Cs = workloads.residual_codebooks(Xtr - C0[rng.integers(0, h0, 3000)], ms, K, 3, seed + 1)
+    X = mix.sample(0, n)
+    if case == "dup_small":
+        Cs[5] = Cs[9]
+        Cs[K + 17] = Cs[K + 3]
+        Cs[2 * K + 100] = Cs[3 * K + 7]
+    elif case == "nan_small":
+        Cs[2 * K + 7, 1] = np.nan
+    h = [h0] + [K] * ms
+    ctx.set_large_root(C0, Cs, h)
+    norm0, Gs, G0S = orc.build_precomp_large_root(C0, Cs)
+    nx2 = orc.xnorm2(X)
+    xs = orc.gemm_xc(Cs, X, mode=1)
+    for mode in ("nearest", "forced"):
+        forced = rng.integers(0, h0, n).astype(np.uint32) if mode == "forced" else None
+        rm = 1 if mode == "nearest" else 0
+        monkeypatch.delenv("STLQ_MI355_BEAM_ORDER", raising=False)
+        cid_b, Bs_b, err_b = ctx.beam_search_large_root(X, Hb, forced_root=forced, root_mode=rm)
+        reruns = ctx.last_timings().beam_reruns
+        monkeypatch.setenv("STLQ_MI355_BEAM_ORDER", "reference")
+        cid_r, Bs_r, err_r = ctx.beam_search_large_root(X, Hb, forced_root=forced, root_mode=rm)
+        assert ctx.last_timings().beam_reruns == 0
+        monkeypatch.delenv("STLQ_MI355_BEAM_ORDER")
+        print(f"{case}/{mode}: {reruns} of {n} vectors re-run", flush=True)
+        assert np.array_equal(cid_b, cid_r), (case, mode)
+        assert np.array_equal(Bs_b, Bs_r), (case, mode, np.nonzero(np.any(Bs_b != Bs_r, axis=1))[0][:10])
+        same = (_bits(err_b) == _bits(err_r)) | (np.isnan(err_b) & np.isnan(err_r))
+        assert np.all(same), (case, mode)
+        cid_o, Bs_o, err_o = orc.beam_search_large_root(X, nx2, C0, norm0, xs, Gs, G0S, h, Hb, forced_root=forced,
+                                                        root_mode=rm)
+        assert np.array_equal(cid_o, cid_b) and np.array_equal(Bs_o, Bs_b), (case, mode)
+        if case == "plain":
+            assert reruns <= 0.02 * n, (mode, reruns)
+        else:
+            assert reruns > 0, (case, mode)
+
+
 def _crafted_roots(variant, seed=90, n=500, d=32, h0=300, K=16, m=4):
     """Root codebooks built to hit the root scan's corner cases (beam_search.cpp:686-705):
     ties: exact duplicate roots (adjacent and far apart; the lower code must win), zero roots
