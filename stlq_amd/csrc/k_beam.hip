@@ -133,12 +133,64 @@ template <bool kNonNeg>
 struct TopKeys {
     uint64_t key;
     uint32_t whi, wlo;  // key of lane 0 (the worst slot)
+    bool empty = true;  // no candidate has entered yet
     __device__ explicit TopKeys(int lane)
         : key((static_cast<uint64_t>(KeyImage<kNonNeg>(__builtin_huge_valf())) << 32) |
               (static_cast<uint64_t>(63 - lane) << 26) | kNoCand),
           whi(KeyImage<kNonNeg>(__builtin_huge_valf())),
           wlo((63u << 26) | kNoCand) {}
 };
+
+// Lane (lane ^ J)'s value, J a power of two below 64: DPP quad permutations for 1 and 2, LDS
+// swizzle (xor mode, within 32 lanes) for 4 to 16, bpermute for 32.
+template <int J>
+__device__ __forceinline__ uint32_t XorLane(uint32_t v, int lane) {
+    if constexpr (J == 1) {
+        return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0xB1, 0xF, 0xF, false));
+    } else if constexpr (J == 2) {
+        return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x4E, 0xF, 0xF, false));
+    } else if constexpr (J < 32) {
+        return static_cast<uint32_t>(__builtin_amdgcn_ds_swizzle(static_cast<int>(v), (J << 10) | 0x1F));
+    } else {
+        return static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute((lane ^ 32) << 2, static_cast<int>(v)));
+    }
+}
+
+// One compare-exchange step of a bitonic sort over the wave: sequences of K lanes, partners J
+// lanes apart; lanes whose K-block is even sort ascending.
+template <int K, int J>
+__device__ __forceinline__ void BitonicStep(uint64_t& x, int lane) {
+    const uint64_t y = (static_cast<uint64_t>(XorLane<J>(static_cast<uint32_t>(x >> 32), lane)) << 32) |
+                       XorLane<J>(static_cast<uint32_t>(x), lane);
+    const bool take_min = ((lane & K) == 0) == ((lane & J) == 0);
+    x = (take_min == (y < x)) ? y : x;
+}
+
+// The 64 lanes' keys sorted ascending (lane 0 the smallest).
+__device__ __forceinline__ uint64_t SortWave(uint64_t x, int lane) {
+    BitonicStep<2, 1>(x, lane);
+    BitonicStep<4, 2>(x, lane);
+    BitonicStep<4, 1>(x, lane);
+    BitonicStep<8, 4>(x, lane);
+    BitonicStep<8, 2>(x, lane);
+    BitonicStep<8, 1>(x, lane);
+    BitonicStep<16, 8>(x, lane);
+    BitonicStep<16, 4>(x, lane);
+    BitonicStep<16, 2>(x, lane);
+    BitonicStep<16, 1>(x, lane);
+    BitonicStep<32, 16>(x, lane);
+    BitonicStep<32, 8>(x, lane);
+    BitonicStep<32, 4>(x, lane);
+    BitonicStep<32, 2>(x, lane);
+    BitonicStep<32, 1>(x, lane);
+    BitonicStep<64, 32>(x, lane);
+    BitonicStep<64, 16>(x, lane);
+    BitonicStep<64, 8>(x, lane);
+    BitonicStep<64, 4>(x, lane);
+    BitonicStep<64, 2>(x, lane);
+    BitonicStep<64, 1>(x, lane);
+    return x;
+}
 
 struct TopSlots {
     float s_err = __builtin_huge_valf();
@@ -187,7 +239,7 @@ struct OutTrack {
     uint32_t ev = 0xFFFFFFFFu;
 };
 
-template <bool kNonNeg, bool kTrack>
+template <bool kNonNeg, bool kTrack, bool kSortFirst>
 __device__ __forceinline__ bool ReplayFast(bool ok, float e, int cand, int Hb, int lane, TopKeys<kNonNeg>& t,
                                            OutTrack& ot) {
     const uint64_t okm = Ballot(ok);
@@ -195,6 +247,36 @@ __device__ __forceinline__ bool ReplayFast(bool ok, float e, int cand, int Hb, i
     if ((Ballot(bad) & okm) != 0ull) return false;
     const uint32_t oe = KeyImage<kNonNeg>(e);
     uint64_t mask = okm & Ballot(oe < t.whi);
+    if (kTrack && kSortFirst && t.empty) {
+        // Best-first pass, first group into an empty top-H: the group's keys sorted at once
+        // instead of inserted one by one. Every entering candidate would enter in turn, so the
+        // top-H after the group is its min(n, H) smallest keys: the same set the insertions give
+        // (among equal errors the earlier candidate, which has the smaller key, stays), and the
+        // smallest key left out counts as evicted for the tie check. Slots still empty keep their
+        // placeholder keys, which sort above every candidate's.
+        const int n = __popcll(mask);
+        if (n == 0) return true;
+        const bool in = ((mask >> lane) & 1ull) != 0ull;
+        const uint64_t x = SortWave(in ? ((static_cast<uint64_t>(oe) << 32) | static_cast<uint32_t>(cand)) : ~0ull,
+                                    lane);
+        const int src = (Hb - 1 - lane) & 63;  // lane h (< Hb) takes the (Hb-1-h)-th smallest
+        const uint64_t y =
+            (static_cast<uint64_t>(static_cast<uint32_t>(
+                 __builtin_amdgcn_ds_bpermute(src << 2, static_cast<int>(static_cast<uint32_t>(x >> 32)))))
+             << 32) |
+            static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(src << 2, static_cast<int>(static_cast<uint32_t>(x))));
+        if (lane < Hb && lane >= Hb - n) t.key = y;
+        if (n > Hb) {
+            const uint32_t out = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(x >> 32), Hb));
+            ot.ev = ot.ev < out ? ot.ev : out;
+        }
+        t.whi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(t.key >> 32), 0));
+        t.wlo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(t.key), 0));
+        t.empty = false;
+        const uint32_t img = __builtin_amdgcn_inverse_ballot_w64(okm & ~mask) ? oe : 0xFFFFFFFFu;
+        ot.rej = img < ot.rej ? img : ot.rej;
+        return true;
+    }
     uint64_t entered = 0;
     // lanes 1..Hb-1 of the sorted keys: the ones that stay when lane 0 (the worst) is evicted
     const uint64_t keep = (Hb >= 64 ? ~0ull : ((1ull << Hb) - 1ull)) & ~1ull;
@@ -287,12 +369,12 @@ __device__ __forceinline__ void ReplaySlow(bool ok, float e, int cand, int Hb, i
 // evicted) with the same error as the final worst of a full top-H. Without such a tie the top-H
 // set does not depend on the scan order: every candidate with an error below the final worst
 // enters when it is scanned and is never evicted, whatever came before it.
-template <bool kNonNeg, bool kBest, bool kRank, class Chunks>
+template <bool kNonNeg, bool kBest, bool kRank, bool kSortFirst = kBest, class Chunks>
 __device__ __forceinline__ void SelectTopH(int Hb, int lane, Chunks&& chunks, float& s_err, int& s_cand, bool& flag) {
     TopKeys<kNonNeg> tk(lane);
     OutTrack ot;
     const bool fast = chunks(
-        [&](bool ok, float e, int cand) { return ReplayFast<kNonNeg, kBest>(ok, e, cand, Hb, lane, tk, ot); },
+        [&](bool ok, float e, int cand) { return ReplayFast<kNonNeg, kBest, kSortFirst>(ok, e, cand, Hb, lane, tk, ot); },
         std::false_type(), [&]() { return KeyError<kNonNeg>(tk.whi); });
     if constexpr (kBest) {
         if (!fast) {
@@ -645,17 +727,14 @@ __global__ __launch_bounds__(256) void Layer0Kernel(LayerArgs p) {
 
 // Layers L >= 1. LR selects the large-root cross-term source and reciprocal solves.
 // FULL: the layer has exactly 256 codewords (no partial chunk).
-// Minimum waves per SIMD requested from the register allocator, per layer (measured):
-//  * layers >= 11 at 4 waves (<= 128 VGPRs), 5 for the large root: left alone the allocator
-//    gives them 2-3 waves, or 1 at layer 16 (> 256 VGPRs); the M=16, beam-8 encode ran 9% faster
-//    and the large-root 16-layer beam-32 encode 18% faster (5 waves there: another 1%);
-//  * on the M=8, K=256, beam-16 encode layers 4 and 6 run best at 8 waves and layer 7 at 7 (6 in
-//    the best-first pass, where 80 VGPRs remove its spills), and layer 3 of the best-first pass
-//    at 8 (left alone it takes 65 VGPRs, one over);
-//  * the other layers at the allocator's own choice.
+// Minimum waves per SIMD asked of the register allocator by the queue kernel (layers 2-8),
+// measured on the M=8, K=256, beam-16 encode: layers 2-3 at 8, 4-5 at 7, 6 at 6; layers 7 and 8
+// at the allocator's choice (5 and 4 waves; forcing 6 spills and ran 3% slower). The large root:
+// layer 2 at 8 (the best-first pass's sorted first group takes its SGPRs to 106, which gives 7),
+// the others at the allocator's choice (forcing 6-8 waves ran 2-9% slower on the beam-32 encode).
 template <int L, bool LR, bool BEST>
 constexpr int LayerMinWaves() {
-    if (LR) return L >= 11 ? 5 : 1;
+    if (LR) return L <= 2 ? 8 : 1;
     return L <= 3 ? 8 : (L <= 5 ? 7 : (L == 6 ? 6 : 1));
 }
 
@@ -1255,10 +1334,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LayerMinWav
 // of 64 at a time with the slot's factor in SGPRs, and the slots are written back by the lanes that
 // hold them, with their pruning constants for the later layers. LR selects the large-root
 // cross-term source and reciprocal solves. FULL: the layer has exactly 256 codewords (no partial
-// chunk). The register allocator picks the occupancy.
+// chunk). 8 waves per SIMD: left alone, the best-first pass's sorted first group (SortWave) takes
+// the SGPRs to 106, and 7 waves made the M=8, beam-16 layer 8% slower.
 template <int L, bool LR, bool BEST>
 constexpr int DeepMinWaves() {
-    return 1;
+    return 8;
 }
 
 
@@ -1744,6 +1824,10 @@ template <int L>
 constexpr int WbStride() {
     return StagedWords<L>() | 1;  // odd: the lanes of a round read distinct banks
 }
+// Deepest large-root staged layer whose best-first pass sorts its first group into the empty top-H
+// (ReplayFast): on the large-root beam-32 encode layers 15 and 16 ran 3% and 2% slower with it,
+// its layers up to 14 and every layer of the M=16, beam-8 encode 1-3% faster.
+constexpr int kLrSortFirstMaxL = 14;
 // The windowed queue scan stages kStagedWin slots at a time: factor, a_old and error per slot (odd
 // stride: the lanes of a group read distinct banks), then ahat and c per slot, after the FIFO.
 constexpr int kStagedWin = 8;
@@ -2166,7 +2250,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(StagedMinWa
     float s_err;
     int s_cand;
     bool flagged = false;
-    SelectTopH<true, BEST, BEST>(  // errors clamped at zero (EvalCand)
+    SelectTopH<true, BEST, BEST, BEST && (!LR || L <= kLrSortFirstMaxL)>(  // errors clamped at zero (EvalCand)
         Hb, lane,
         [&](auto&& replay, auto slow_tag, auto&& worst_now) {
             if constexpr (!decltype(slow_tag)::value) {
