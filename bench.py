@@ -109,20 +109,17 @@ def _calib_copy(ctx, mb: int):
 
 
 def _layer_kernel_name(L: int, lr: bool) -> str:
-    """The profiled name of the beam layer kernel that runs layer L with a full codebook (the
-    dispatch of LaunchL in k_beam.hip): the per-parent kernel for layers 1..2, the survivor-queue
-    kernel for 3..8, then the staged kernel (the large root: the per-parent kernel up to layer 13).
-    The full-precomp beam runs its best-first pass, the large-root beam the reference order."""
-    b, best = ("true", "false") if lr else ("false", "true")
-    if L < 3:
+    """The profiled name of the beam layer kernel that runs layer L with a full codebook in the
+    best-first pass (the dispatch of LaunchL in k_beam.hip): the per-parent kernel for layer 1, the
+    survivor-queue kernel for layers 2..8, then the staged kernel, for the full-precomp and the
+    large-root beam alike."""
+    if L < 2:
         kind = "LayerKernelDeep"
     elif L <= 8:
         kind = "LayerKernel"
-    elif lr and L < 14:
-        kind = "LayerKernelDeep"
     else:
         kind = "LayerKernelStaged"
-    return f"{kind}<{L}, {b}, true, {best}>"
+    return f"{kind}<{L}, {'true' if lr else 'false'}, true, true>"
 
 
 def _cpu_model() -> str:
