@@ -110,12 +110,9 @@ def _calib_copy(ctx, mb: int):
 
 def _layer_kernel_name(L: int, lr: bool) -> str:
     """The profiled name of the beam layer kernel that runs layer L with a full codebook in the
-    best-first pass (the dispatch of LaunchL in k_beam.hip): the per-parent kernel for layer 1, the
-    survivor-queue kernel for layers 2..8, then the staged kernel, for the full-precomp and the
-    large-root beam alike."""
-    if L < 2:
-        kind = "LayerKernelDeep"
-    elif L <= 8:
+    best-first pass (the dispatch of LaunchL in k_beam.hip): the survivor-queue kernel for layers
+    1..8, then the staged kernel, for the full-precomp and the large-root beam alike."""
+    if L <= 8:
         kind = "LayerKernel"
     else:
         kind = "LayerKernelStaged"
@@ -425,6 +422,8 @@ def bench_stream_large_root(args, w):
     sel_bytes = 4.0 * w.K * w.H_beam * chunk
     beam_ach = sel_bytes / (avg_last_ms * 1e-3) / 1e9
     h2d_gbs = st.h2d_bytes / (st.h2d_ms * 1e-3) / 1e9 if st.h2d_ms > 0 else None
+    dist_flops = 2.0 * w.d * (h0 + (M - 1) * w.K) * (n / nch)
+    dist_ach = dist_flops / (t.gemm_ms / nch * 1e-3) / 1e12 if t.gemm_ms > 0 else None
     prof_kernel = _layer_kernel_name(last, lr=True)
     traffic, traffic_src = _profiled_traffic(prof_kernel, "c5_stream")
     valu, _, valu_src = _profiled_valu(prof_kernel, "c5_stream")
@@ -459,6 +458,19 @@ def bench_stream_large_root(args, w):
             "avg_launch_ms": avg_last_ms,
         },
         "roofline_valu": _roofline_valu(prof_kernel, valu, avg_last_ms, valu_src),
+        # The distance stage: the nearest-root GEMM over the 65,536 roots (2*d*h0 flops per vector,
+        # first-minimum epilogue) and the xC GEMM over the 16 x 256 small codewords (2*d*Hs), both
+        # fp32 MFMA, timed together by HIP events with the NaN fix-up and the root-dot gather.
+        "roofline_distance": {
+            "kernel": "NearestRootKernel + GemmXcKernel (fp32 MFMA, lookup form)",
+            "bound": "mfma",
+            "achieved": dist_ach,
+            "peak": PEAK_FP32_MFMA_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": dist_ach / PEAK_FP32_MFMA_TFLOPS if dist_ach else None,
+            "flops_per_chunk": dist_flops,
+            "ms_per_chunk": t.gemm_ms / nch,
+        },
         "streaming": {
             "h2d_GBps": h2d_gbs,
             "h2d_bytes": st.h2d_bytes,

@@ -1653,7 +1653,10 @@ int64_t LargeRootTileVectors(stlq_mi355_ctx* c, int64_t n, int Hb, bool one_scor
     const int64_t per = 4LL * c->lr_d + 4 + 8LL * std::max(c->Hs, 1) + (one_score ? 16 : 4LL * c->h0) +
                         2 * (4LL * Hb * BeamRecordStride(m) + 4) + m + 16 +
                         (5LL * m + 20);  // refit: b0, ICM flags and proposals, ILS candidate codes/coefficients/cost
-    int64_t t = std::max<int64_t>(EnvWorkspaceBytes() / per, 1024);
+    // A multiple of 128 vectors: the nearest-root kernel sweeps all h0 roots for 128 vectors per
+    // block, and a partial last block runs as a launch of its own on one CU (7.8 ms per tile at
+    // C5 against 48 ms for the full blocks), so only the last tile of a call may have one.
+    int64_t t = std::max<int64_t>(EnvWorkspaceBytes() / per, 1024) / 128 * 128;
     return std::min<int64_t>(t, std::max<int64_t>(n, 1));
 }
 

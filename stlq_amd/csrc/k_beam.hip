@@ -727,10 +727,11 @@ __global__ __launch_bounds__(256) void Layer0Kernel(LayerArgs p) {
 
 // Layers L >= 1. LR selects the large-root cross-term source and reciprocal solves.
 // FULL: the layer has exactly 256 codewords (no partial chunk).
-// Minimum waves per SIMD asked of the register allocator by the queue kernel (layers 2-8),
-// measured on the M=8, K=256, beam-16 encode: layers 2-3 at 8, 4-5 at 7, 6 at 6; layers 7 and 8
-// at the allocator's choice (5 and 4 waves; forcing 6 spills and ran 3% slower). The large root:
-// layer 2 at 8 (the best-first pass's sorted first group takes its SGPRs to 106, which gives 7),
+// Minimum waves per SIMD asked of the register allocator by the queue kernel (layers 1-8),
+// measured on the M=8, K=256, beam-16 encode: layers 1-3 at 8, 4-5 at 7, 6 at 6 (5 waves, without
+// its small spill, ran 1% slower); layers 7 and 8 at the allocator's choice (5 and 4 waves; forcing
+// 6 spills and ran 3% slower). The large root: layers 1-2 at 8 (the best-first pass's sorted first
+// group takes the SGPRs to 106, which gives 7),
 // the others at the allocator's choice (forcing 6-8 waves ran 2-9% slower on the beam-32 encode).
 template <int L, bool LR, bool BEST>
 constexpr int LayerMinWaves() {
@@ -743,11 +744,11 @@ constexpr int LayerMinWaves() {
 // extra VGPRs cost occupancy.
 constexpr int kVStateMaxL = 3;
 
-// Layers kQueueMinL..kQueueMaxL scan through a queue (LayerKernel, scan_queue): the survivors of the
-// pruning bound from every parent go into one FIFO and are evaluated 64 at a time, each lane with
-// its own parent's factor in VGPRs. Deeper layers evaluate each parent's survivors apart, with the
-// factor in SGPRs, whose VGPR cost would otherwise grow as L^2.
-constexpr int kQueueMinL = 2;
+// Layers 1..kQueueMaxL scan through a queue (LayerKernel, scan_queue): the survivors of the pruning
+// bound from every parent go into one FIFO and are evaluated 64 at a time, each lane reading its own
+// parent's state from LDS. At layer 1 too: there a solve costs little more than the bound, but the
+// queue's full groups and the staged state cut the layer from 5.7 to 4.2 ms on the M=8, beam-16
+// encode against evaluating every candidate slot by slot.
 constexpr int kQueueMaxL = 8;
 constexpr int kQueueCap = 128;  // ring capacity: at most 63 carried over plus one chunk of 64
 // Layers above kQueueMaxL run the staged kernel (pruned, factors staged in LDS a window of slots
@@ -1326,332 +1327,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LayerMinWav
             p.codes_out[i * m + L] = static_cast<uint8_t>(knew);
         }
         if (p.best_err) p.best_err[i] = out_err;
-    }
-}
-
-// Layer 1 (below kQueueMinL, where a candidate's solve costs little more than its bound and the
-// staging of the pruned kernels): every candidate of every slot is evaluated exactly, four chunks
-// of 64 at a time with the slot's factor in SGPRs, and the slots are written back by the lanes that
-// hold them, with their pruning constants for the later layers. LR selects the large-root
-// cross-term source and reciprocal solves. FULL: the layer has exactly 256 codewords (no partial
-// chunk). 8 waves per SIMD: left alone, the best-first pass's sorted first group (SortWave) takes
-// the SGPRs to 106, and 7 waves made the M=8, beam-16 layer 8% slower.
-template <int L, bool LR, bool BEST>
-constexpr int DeepMinWaves() {
-    return 8;
-}
-
-
-// BEST: the best-first pass (LayerArgs::flags). Its input records are rank-indexed, so slots are
-// scanned in ascending error order, and so are its output records. A vector flagged by an earlier
-// layer arrives with an empty beam.
-template <int L, bool LR, bool FULL, bool BEST>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DeepMinWaves<L, LR, BEST>(), 8))) void LayerKernelDeep(
-    LayerArgs p) {
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    int64_t i, w;
-    if (!WaveItem(p, wave, i, w)) return;
-    const int m = p.m, Hb = p.Hb, K = FULL ? kMaxK : p.K, offL = p.offL;
-    const Rec rc(m);
-    const int ld = p.gram.ld;
-    const float* xCi = p.xC + i * p.ldx;
-    const int nch = FULL ? kMaxChunks : (K + kWave - 1) / kWave;
-    const float* __restrict__ recs_in = p.in.rec + w * Hb * rc.stride;
-    float* __restrict__ recs_out = p.out.rec + w * Hb * rc.stride;
-    const float* __restrict__ G = p.gram.G + offL + lane;
-    const int vz = VZero();
-
-    float gam[kMaxChunks], alp[kMaxChunks];
-#pragma unroll
-    for (int j = 0; j < kMaxChunks; ++j) {
-        const int k = lane + kWave * j;
-        const bool act = FULL || (j < nch && k < K);
-        gam[j] = act ? xCi[offL + k] : 0.0f;
-        alp[j] = act ? p.gdiag[offL + k] : 0.0f;
-    }
-
-    const int curH = p.in.curH[w];
-
-    // Beam slot h's codes (and root) sit in lane h, read with one vector load per word for all
-    // slots at once, so a slot's G rows can be addressed without waiting for its record.
-    constexpr int kCodeWords = (L + 3) / 4;
-    uint32_t cw[kCodeWords];
-    uint32_t rootw = 0;
-    {
-        const uint32_t* rl = reinterpret_cast<const uint32_t*>(recs_in + (lane < curH ? lane : 0) * rc.stride);
-#pragma unroll
-        for (int w = 0; w < kCodeWords; ++w) cw[w] = rl[rc.code + w];
-        if (LR) rootw = rl[rc.root];
-    }
-    // G rows of slot h: A[j][t] = G(prefix_t, offL + lane + 64 j) (the large root's prefix 0 reads
-    // G0S(root, .)).
-    auto load_rows = [&](int h, float (&A)[kMaxChunks][L]) {
-        const float* rowp[L];
-#pragma unroll
-        for (int t = 0; t < L; ++t) {
-            if (LR && t == 0) {
-                const uint32_t root = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(rootw), h));
-                rowp[t] = p.gram.G0S + static_cast<int64_t>(root) * ld + offL + lane;
-            } else {
-                const uint32_t word = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(cw[t >> 2]), h));
-                const uint32_t code = (word >> (8 * (t & 3))) & 0xFFu;
-                rowp[t] = G + static_cast<uint32_t>(p.gram.off[t] + static_cast<int>(code)) * static_cast<uint32_t>(ld);
-            }
-        }
-#pragma unroll
-        for (int j = 0; j < kMaxChunks; ++j) {
-#pragma unroll
-            for (int t = 0; t < L; ++t) {
-                const bool act = FULL || (j < nch && lane + kWave * j < K);
-                A[j][t] = act ? rowp[t][kWave * j] : 0.0f;
-            }
-        }
-    };
-    // Evaluates slot h's candidates and replays them into the top-H (scan order: slot, then code).
-    // Returns false when the replay asks for the slow pass.
-    auto process = [&](int h, const float (&A)[kMaxChunks][L], auto&& replay, auto slow_tag) -> bool {
-        constexpr bool kSlow = decltype(slow_tag)::value;
-        const float* rec = recs_in + h * rc.stride;
-        const float E_old = rec[0];
-        // The slot's R, 1/diag and coefficients are wave-uniform. Up to kVStateMaxL they are read
-        // into VGPRs, so the solves' products have two VGPR sources; beyond it they stay in
-        // SGPRs, where they cost no occupancy.
-        const float* recv = kVStateMaxL >= L ? rec + vz : rec;
-        float aold[L];
-        float Rv[L][L];
-        float Ri[L];
-#pragma unroll
-        for (int t = 0; t < L; ++t) aold[t] = recv[rc.coef + t];
-        bool diag_ok = true;
-#pragma unroll
-        for (int r = 0; r < L; ++r) {
-#pragma unroll
-            for (int c = r; c < L; ++c) Rv[r][c] = recv[Rec::R(r, c)];
-            Ri[r] = recv[Rec::Rinv(r)];
-            diag_ok = diag_ok && DiagFastOk(Rv[r][r]);
-        }
-        const bool diag_fast = !LR && Ballot(!diag_ok) == 0ull;
-        auto Rf = [&](int r, int c) { return Rv[r][c]; };
-
-        float ech[kMaxChunks];
-        bool okc[kMaxChunks];
-        // All chunks of the slot with one arithmetic mode (the choice is per slot), so the chunk
-        // loop below is straight-line code.
-        auto eval_all = [&](auto mode_tag, bool& safe) {
-            constexpr int MODE = decltype(mode_tag)::value;
-#pragma unroll
-            for (int j = 0; j < kMaxChunks; ++j) {
-                ech[j] = kInfF;
-                okc[j] = false;
-                if (!FULL && j >= nch) continue;
-                float y[L], v[L], denom, a_last, e;
-                bool ok;
-                EvalCand<L, MODE>(Rf, Ri, A[j], aold, E_old, alp[j], gam[j], y, v, e, denom, a_last, ok, safe);
-                ech[j] = e;
-                okc[j] = ok && (FULL || (j < nch && lane + kWave * j < K));
-            }
-        };
-        bool safe = true;
-        if (LR) {
-            eval_all(std::integral_constant<int, 2>(), safe);
-        } else if (kSlow) {  // the rare slow pass: IEEE division only (same quotients)
-            eval_all(std::integral_constant<int, 0>(), safe);
-        } else if (diag_fast) {
-            eval_all(std::integral_constant<int, 1>(), safe);
-            // A numerator left the range where the reciprocal-corrected quotient is exact:
-            // re-evaluate this slot's chunks with IEEE division (rare).
-            if (Ballot(!safe) != 0ull) eval_all(std::integral_constant<int, 0>(), safe);
-        } else {
-            eval_all(std::integral_constant<int, 0>(), safe);
-        }
-#pragma unroll
-        for (int j = 0; j < kMaxChunks; ++j) {
-            if (FULL || j < nch) {
-                if (!replay(okc[j], ech[j], h * K + kWave * j + lane)) return false;
-            }
-        }
-        return true;
-    };
-
-    float s_err;
-    int s_cand;
-    bool flagged = false;
-    SelectTopH<true, BEST, BEST>(  // errors clamped at zero (EvalCand)
-        Hb, lane,
-        [&](auto&& replay, auto slow_tag, auto) {
-            for (int h = 0; h < curH; ++h) {
-                float A[kMaxChunks][L];
-                load_rows(h, A);
-                if (!process(h, A, replay, slow_tag)) return false;
-            }
-            return true;
-        },
-        s_err, s_cand, flagged);
-    if (BEST && flagged) {
-        // No records: the next layers see an empty beam (curH = 0), do no work for this vector
-        // and keep it well-formed until its re-run.
-        if (lane == 0) {
-            p.flags[i] = 1;
-            p.out.curH[w] = 0;
-        }
-        return;
-    }
-
-    // Deferred write-back (beam_search.cpp:337-383) or the all-skipped fallback (:385-400).
-    const int newH = __popcll(__ballot(lane < Hb && s_err < kInfF));
-    int outH;
-    float out_err = kInfF;
-    // pruning constants of the new slots, while a later layer runs the queue scan
-    constexpr bool kNextQueued = true;  // every later layer prunes
-    prune::SlotBounds out_bd = prune::NoBounds();
-    uint8_t ncode[L + 1];
-    uint32_t nroot = 0;
-#pragma unroll
-    for (int t = 0; t <= L; ++t) ncode[t] = 0;
-    if (newH == 0) {
-        const int nh = min(curH, Hb);
-        outH = max(1, nh);
-        if (lane < nh) {
-            const float* ri = recs_in + lane * rc.stride;
-            float* ro = recs_out + lane * rc.stride;
-            out_err = ri[0];
-#pragma unroll
-            for (int t = 0; t < L; ++t) {
-                ncode[t] = static_cast<uint8_t>(CodeAt(ri, rc.code, t));
-                ro[rc.coef + t] = ri[rc.coef + t];
-            }
-            ro[rc.coef + L] = 0.0f;
-#pragma unroll
-            for (int r = 0; r < L; ++r) {
-#pragma unroll
-                for (int c = r; c < L; ++c) ro[Rec::R(r, c)] = ri[Rec::R(r, c)];
-                ro[Rec::R(r, L)] = 0.0f;
-                ro[Rec::Rinv(r)] = ri[Rec::Rinv(r)];
-            }
-            ro[Rec::R(L, L)] = 0.0f;
-            ro[Rec::Rinv(L)] = 1.0f / 0.0f;
-            nroot = reinterpret_cast<const uint32_t*>(ri)[rc.root];
-        } else if (nh == 0 && lane == 0) {
-            // No beam at all (layer 0 had no finite candidate): the reference's next-buffer slot 0
-            // keeps its never-written (zero) state with error +inf.
-            float* ro = recs_out;
-#pragma unroll
-            for (int t = 0; t <= L; ++t) ro[rc.coef + t] = 0.0f;
-#pragma unroll
-            for (int r = 0; r <= L; ++r) {
-#pragma unroll
-                for (int c = r; c <= L; ++c) ro[Rec::R(r, c)] = 0.0f;
-                ro[Rec::Rinv(r)] = 1.0f / 0.0f;
-            }
-        }
-    } else {
-        outH = max(1, newH);
-        const bool live = lane < Hb && !(s_err >= kInfF);
-        if (live) {
-            const int src = s_cand / K;
-            const int k = s_cand - src * K;
-            const float* ri = recs_in + src * rc.stride;
-            float* ro = recs_out + lane * rc.stride;
-            float Rv[L][L], Ri[L], aold[L], A[L];
-            nroot = reinterpret_cast<const uint32_t*>(ri)[rc.root];
-#pragma unroll
-            for (int r = 0; r < L; ++r) {
-#pragma unroll
-                for (int c = r; c < L; ++c) Rv[r][c] = ri[Rec::R(r, c)];
-                Ri[r] = ri[Rec::Rinv(r)];
-            }
-#pragma unroll
-            for (int t = 0; t < L; ++t) {
-                aold[t] = ri[rc.coef + t];
-                const int ct = CodeAt(ri, rc.code, t);
-                ncode[t] = static_cast<uint8_t>(ct);
-                const float* row = (LR && t == 0)
-                                       ? p.gram.G0S + static_cast<int64_t>(nroot) * ld + offL
-                                       : p.gram.G + static_cast<int64_t>(p.gram.off[t] + ct) * ld + offL;
-                A[t] = row[k];
-            }
-            ncode[L] = static_cast<uint8_t>(k);
-            auto Rf = [&](int r, int c) { return Rv[r][c]; };
-            float y[L], v[L], e, denom, a_last;
-            bool ok, unused = true;
-            // IEEE division here: it is the quotient the fast path reproduces when it is taken.
-            if (LR) {
-                EvalCand<L, 2>(Rf, Ri, A, aold, ri[0], p.gdiag[offL + k], xCi[offL + k], y, v, e, denom, a_last, ok,
-                               unused);
-            } else {
-                EvalCand<L, 0>(Rf, Ri, A, aold, ri[0], p.gdiag[offL + k], xCi[offL + k], y, v, e, denom, a_last, ok,
-                               unused);
-            }
-            out_err = s_err;
-            double asq = 0.0;  // ||ahat||^2 of the new coefficients (pruning constants)
-#pragma unroll
-            for (int t = 0; t <= L; ++t) {
-                const float at = t < L ? aold[t] - v[t] * a_last : a_last;
-                ro[rc.coef + t] = at;
-                if (kNextQueued) {
-                    const int ft = t < L ? ((LR && t == 0) ? static_cast<int>(nroot) : p.gram.off[t] + ncode[t])
-                                         : offL + k;
-                    const float iswt = (LR && t == 0) ? p.isw0[ft] : p.isw[ft];
-                    const double ah = static_cast<double>(at) * static_cast<double>(iswt);
-                    asq += ah * ah;
-                }
-            }
-#pragma unroll
-            for (int r = 0; r < L; ++r) {
-#pragma unroll
-                for (int c = r; c < L; ++c) ro[Rec::R(r, c)] = Rv[r][c];
-                ro[Rec::R(r, L)] = y[r];
-                ro[Rec::Rinv(r)] = Ri[r];
-            }
-            const float rLL = sqrtf(denom);
-            ro[Rec::R(L, L)] = rLL;
-            ro[Rec::Rinv(L)] = 1.0f / rLL;
-            if (kNextQueued) {
-                auto swf = [&](int t) {
-                    return (LR && t == 0) ? p.sw0[nroot] : p.sw[p.gram.off[t] + ncode[t]];
-                };
-                out_bd =
-                    prune::NextBounds<L>(y, v, rLL, swf, p.sw[offL + k], ri[rc.kap], ri[rc.phi], rc.Nf2(ri), asq);
-            }
-        }
-    }
-    if (lane < Hb) {
-        float* ro = recs_out + lane * rc.stride;
-        ro[0] = out_err;
-        rc.PutBounds(ro, out_bd);
-        uint32_t* cw = reinterpret_cast<uint32_t*>(ro + rc.code);
-#pragma unroll
-        for (int q = 0; q <= L / 4; ++q) {
-            uint32_t word = 0;
-#pragma unroll
-            for (int b = 0; b < 4; ++b) {
-                const int t = 4 * q + b;
-                if (t <= L) word |= static_cast<uint32_t>(ncode[t]) << (8 * b);
-            }
-            cw[q] = word;
-        }
-        reinterpret_cast<uint32_t*>(ro)[rc.root] = nroot;
-    }
-    if (lane == 0) p.out.curH[w] = outH;
-
-    if (BEST && p.is_last && FinalTie(out_err, outH)) {
-        if (lane == 0) p.flags[i] = 1;
-        return;
-    }
-    if (p.is_last) {
-        const int best = BestSlot(out_err, outH, lane);
-        if (lane == best) {
-            if (LR) {
-                p.cluster_out[i] = nroot;
-#pragma unroll
-                for (int t = 1; t <= L; ++t) p.codes_out[i * (m - 1) + (t - 1)] = ncode[t];
-            } else {
-#pragma unroll
-                for (int t = 0; t <= L; ++t) p.codes_out[i * m + t] = ncode[t];
-            }
-            if (p.best_err) p.best_err[i] = out_err;
-        }
     }
 }
 
@@ -2476,11 +2151,6 @@ struct QueueSel {
     static constexpr auto kernel = LayerKernel<L, LR, FULL, BEST>;
     static constexpr size_t DynamicLds(int Hb) { return QStage<L>::Bytes(Hb); }  // the staged slot states
 };
-template <int L, bool LR, bool FULL, bool BEST>
-struct DeepSel {
-    static constexpr auto kernel = LayerKernelDeep<L, LR, FULL, BEST>;
-    static constexpr size_t DynamicLds(int) { return 0; }
-};
 
 template <int L, bool LR, bool FULL, bool BEST>
 struct StagedSel {
@@ -2490,9 +2160,7 @@ struct StagedSel {
 
 template <int L>
 hipError_t LaunchL(bool lr, const LayerArgs& a, hipStream_t s) {
-    if constexpr (L < kQueueMinL) {
-        return LaunchWith<L, DeepSel>(lr, a, s);
-    } else if constexpr (L <= kQueueMaxL) {
+    if constexpr (L <= kQueueMaxL) {
         return LaunchWith<L, QueueSel>(lr, a, s);
     } else {
         return LaunchWith<L, StagedSel>(lr, a, s);
