@@ -728,15 +728,15 @@ __global__ __launch_bounds__(256) void Layer0Kernel(LayerArgs p) {
 // Layers L >= 1. LR selects the large-root cross-term source and reciprocal solves.
 // FULL: the layer has exactly 256 codewords (no partial chunk).
 // Minimum waves per SIMD asked of the register allocator by the queue kernel (layers 1-8),
-// measured on the M=8, K=256, beam-16 encode: layers 1-3 at 8, 4-5 at 7, 6 at 6 (5 waves, without
-// its small spill, ran 1% slower); layers 7 and 8 at the allocator's choice (5 and 4 waves; forcing
-// 6 spills and ran 3% slower). The large root: layers 1-2 at 8 (the best-first pass's sorted first
-// group takes the SGPRs to 106, which gives 7),
-// the others at the allocator's choice (forcing 6-8 waves ran 2-9% slower on the beam-32 encode).
+// measured on the M=8, K=256, beam-16 encode: layers 1-3 at 8, 4-5 at 7, 6 at 6, 7 at 5 (the
+// allocator alone gives it 101 VGPRs and 4 waves, and the last layer of that encode ran 3% slower),
+// layer 8 at the allocator's choice (4 waves). The large root: layers 1-2 at 8 (the best-first
+// pass's sorted first group takes the SGPRs to 106, which gives 7), the others at the allocator's
+// choice (forcing 6-8 waves ran 2-9% slower on the beam-32 encode).
 template <int L, bool LR, bool BEST>
 constexpr int LayerMinWaves() {
     if (LR) return L <= 2 ? 8 : 1;
-    return L <= 3 ? 8 : (L <= 5 ? 7 : (L == 6 ? 6 : 1));
+    return L <= 3 ? 8 : (L <= 5 ? 7 : (L == 6 ? 6 : (L == 7 ? 5 : 1)));
 }
 
 // Layers up to kVStateMaxL read the slot state into VGPRs (see process() in LayerKernel): on the
@@ -805,12 +805,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LayerMinWav
     // The queue scan's exact evaluations read each lane's parent state from LDS (QStage), staged
     // here for every slot: the factor is then read row by row as the solves need it (EvalStaged)
     // instead of being held whole in registers, which keeps the kernel's VGPRs, and so its
-    // occupancy, near the bound stage's. diag_mask bit h: slot h's diagonal is in the range where
-    // the Markstein quotients are exact.
+    // occupancy, near the bound stage's. The write-back reads each new slot's parent from here too.
+    // diag_mask bit h: slot h's diagonal is in the range where the Markstein quotients are exact.
     HIP_DYNAMIC_SHARED(float, s_stage)
     float* __restrict__ stage = s_stage + static_cast<size_t>(wave) * Hb * QStage<L>::kStride;
     uint64_t diag_mask = 0;
-    if (prune_on) {
+    {
         constexpr int kW = QStage<L>::kEold + 1;
         for (int q = lane; q < curH * kW; q += kWave) {
             const int h = q / kW, o = q - h * kW;
@@ -1198,6 +1198,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LayerMinWav
     if (!p.is_last) {
         float* ro = recs_out + lane * rc.stride;
         const float* ri = recs_in + (src < 0 ? 0 : src) * rc.stride;
+        // the parent's code words (and root) from the lane that holds them, the whole wave active
+        const int srcl = (src < 0 ? 0 : src) << 2;
+        uint32_t pcw[kCodeWords];
+#pragma unroll
+        for (int q = 0; q < kCodeWords; ++q)
+            pcw[q] = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(srcl, static_cast<int>(cw[q])));
+        const uint32_t prootw =
+            LR ? static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(srcl, static_cast<int>(rootw))) : 0u;
         auto put_codes = [&](bool from_parent, int kc, uint32_t root) {
             uint32_t* cwo = reinterpret_cast<uint32_t*>(ro + rc.code);
 #pragma unroll
@@ -1251,51 +1259,69 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LayerMinWav
         } else if (live) {
             // The chosen candidate once more with the reference's arithmetic (IEEE division, or the
             // large root's reciprocal multiply): its new coefficients, Cholesky column and bounds.
-            const uint32_t root = reinterpret_cast<const uint32_t*>(ri)[rc.root];
-            float Rv[L][L], Ri[L], aold[L], A[L];
+            // The parent's factor, coefficients and error come from the LDS stage and its codes
+            // from the lane that holds them (no per-lane gathers from the parent's record); the
+            // record's first columns, at offsets fixed by L, leave as 16-byte stores.
+            const float* sf = stage + src * QStage<L>::kStride;
+            const uint32_t root = LR ? prootw : 0u;
+            float A[L];
             int fl[L];  // flat index of each prefix codeword (the root for a large root's prefix 0)
 #pragma unroll
             for (int t = 0; t < L; ++t) {
-#pragma unroll
-                for (int c = t; c < L; ++c) Rv[t][c] = ri[Rec::R(t, c)];
-                Ri[t] = ri[Rec::Rinv(t)];
-                aold[t] = ri[rc.coef + t];
-                fl[t] = (LR && t == 0) ? static_cast<int>(root) : p.gram.off[t] + CodeAt(ri, rc.code, t);
+                const uint32_t code = (pcw[t >> 2] >> (8 * (t & 3))) & 0xFFu;
+                fl[t] = (LR && t == 0) ? static_cast<int>(root) : p.gram.off[t] + static_cast<int>(code);
                 const float* row = (LR && t == 0) ? p.gram.G0S + static_cast<int64_t>(root) * ld + offL
                                                   : p.gram.G + static_cast<int64_t>(fl[t]) * ld + offL;
                 A[t] = row[knew];
             }
-            auto Rf = [&](int r, int c) { return Rv[r][c]; };
+            // EvalCand's operations on the staged factor (IEEE division, or the large root's
+            // reciprocal multiply), so no copy of the factor is held in registers
+            const float E_old = sf[QStage<L>::kEold];
             float y[L], v[L], e, denom, a_last;
             bool ok, unused = true;
             if (LR) {
-                EvalCand<L, 2>(Rf, Ri, A, aold, ri[0], p.gdiag[offL + knew], xCi[offL + knew], y, v, e, denom, a_last,
-                               ok, unused);
+                EvalStaged<L, 2>(sf, A, E_old, p.gdiag[offL + knew], xCi[offL + knew], y, v, e, denom, a_last, ok,
+                                 unused);
             } else {
-                EvalCand<L, 0>(Rf, Ri, A, aold, ri[0], p.gdiag[offL + knew], xCi[offL + knew], y, v, e, denom, a_last,
-                               ok, unused);
+                EvalStaged<L, 0>(sf, A, E_old, p.gdiag[offL + knew], xCi[offL + knew], y, v, e, denom, a_last, ok,
+                                 unused);
             }
-            ro[0] = s_err;
             double asq = 0.0;  // ||ahat||^2 of the new coefficients
 #pragma unroll
             for (int t = 0; t <= L; ++t) {
-                const float at = t < L ? aold[t] - v[t] * a_last : a_last;
+                const float at = t < L ? sf[QStage<L>::kRWords + t] - v[t] * a_last : a_last;
                 ro[rc.coef + t] = at;
                 const float iswt = t < L ? ((LR && t == 0) ? p.isw0[fl[t]] : p.isw[fl[t]]) : p.isw[offL + knew];
                 const double ah = static_cast<double>(at) * static_cast<double>(iswt);
                 asq += ah * ah;
             }
-#pragma unroll
-            for (int r = 0; r < L; ++r) {
-#pragma unroll
-                for (int c = r; c < L; ++c) ro[Rec::R(r, c)] = Rv[r][c];
-                ro[Rec::R(r, L)] = y[r];
-                ro[Rec::Rinv(r)] = Ri[r];
-            }
             const float rLL = sqrtf(denom);
-            ro[Rec::R(L, L)] = rLL;
-            ro[Rec::Rinv(L)] = 1.0f / rLL;
-            put_codes(true, knew, root);
+            // Dwords 0 .. Rinv(L): the error and columns 0..L of the factor with their 1/diag,
+            // rounded up to whole 16-byte words. The padding falls in column L+1 (L < m-1 here),
+            // which the next layer writes into its own output and never reads from this record.
+            constexpr int kHead = (Rec::Rinv(L) + 1 + 3) / 4;
+            float hd[4 * kHead];
+#pragma unroll
+            for (int q = 0; q < 4 * kHead; ++q) hd[q] = 0.0f;
+            hd[0] = s_err;
+#pragma unroll
+            for (int q = 1; q <= QStage<L>::kRWords; ++q) hd[q] = sf[q - 1];  // columns 0..L-1
+#pragma unroll
+            for (int r = 0; r < L; ++r) hd[Rec::R(r, L)] = y[r];
+            hd[Rec::R(L, L)] = rLL;
+            hd[Rec::Rinv(L)] = 1.0f / rLL;
+            float4* ro4 = reinterpret_cast<float4*>(ro);
+#pragma unroll
+            for (int q = 0; q < kHead; ++q) ro4[q] = make_float4(hd[4 * q], hd[4 * q + 1], hd[4 * q + 2], hd[4 * q + 3]);
+            // the parent's code bytes below L, the new code at L, zeros above (as put_codes)
+            uint32_t* cwo = reinterpret_cast<uint32_t*>(ro + rc.code);
+#pragma unroll
+            for (int qq = 0; qq <= L / 4; ++qq) {
+                const uint32_t low = qq < L / 4 ? 0xFFFFFFFFu : ((1u << (8 * (L & 3))) - 1u);
+                const uint32_t par = qq < kCodeWords ? pcw[qq < kCodeWords ? qq : 0] & low : 0u;
+                cwo[qq] = par | (qq == L / 4 ? static_cast<uint32_t>(knew) << (8 * (L & 3)) : 0u);
+            }
+            reinterpret_cast<uint32_t*>(ro)[rc.root] = root;
             auto swf = [&](int t) { return (LR && t == 0) ? p.sw0[fl[t]] : p.sw[fl[t]]; };
             rc.PutBounds(ro, prune::NextBounds<L>(y, v, rLL, swf, p.sw[offL + knew], ri[rc.kap], ri[rc.phi], rc.Nf2(ri),
                                                   asq));
@@ -1519,10 +1545,13 @@ constexpr int StagedWaveWords() {
 }
 
 // Waves per SIMD asked of the register allocator: the kernel needs about 5L + 60 VGPRs, so 4 waves
-// (128) hold it without spills up to layer 12, 3 waves (168) up to layer 18.
+// (128) hold it without spills up to layer 10 and with small ones (up to 25 VGPRs at layer 14)
+// above, 3 waves (168) without spills up to layer 18. 4 waves up to layer 14 ran layers 13-14 5-6%
+// faster than 3 on the large-root beam-32 encode and the M=16, beam-8 encode; 5 waves at layers
+// 9-10 ran 8-9% slower.
 template <int L>
 constexpr int StagedMinWaves() {
-    return L <= 12 ? 4 : 3;
+    return L <= 14 ? 4 : 3;
 }
 
 template <int L, bool LR, bool FULL, bool BEST>
