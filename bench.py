@@ -11,9 +11,10 @@ Prints one JSON line. `roofline` covers the dominant kernel (the last beam layer
 by the benchmark's selection-stage figure (4 bytes per scored candidate, 4*K*B per vector per
 layer) against HBM; `roofline_distance` covers the xC GEMM (2*d*H flops per vector, lookup
 form) against fp32 MFMA. Kernel durations come from HIP events recorded on the stream the
-kernels run on. `cpu_baseline` times the CPU oracle (a C++ restatement of the reference
-encoder, OpenMP) on the first vectors of the same workload, and `parity` compares the GPU codes
-of that sample with the oracle's.
+kernels run on. `cpu_baseline` times the reference's own CPU encoder, compiled from its sources
+into oracle/_ref (kind "reference"), or the CPU oracle (a C++ restatement of it, kind "port")
+where that build is absent, on the first vectors of the same workload with all host threads;
+`parity` compares the GPU codes of that sample with the same CPU run's.
 """
 from __future__ import annotations
 
@@ -84,13 +85,25 @@ def _profiled_valu(kernel: str, stem: str):
         return None, None, None
 
 
-def _roofline_valu(kernel: str, valu, avg_ms, src):
+def _profiled_waves(kernel: str, stem: str):
+    """Waves per launch of `kernel` in the committed SQ counter summary (one wave per vector for
+    the beam layers), or None."""
+    rows, _ = _profile_table(f"{stem}_sq_counters.md")
+    try:
+        return float(rows[kernel]["WAVES"])
+    except (KeyError, ValueError):
+        return None
+
+
+def _roofline_valu(kernel: str, valu, avg_ms, src, per: str = "launch"):
     """The VALU-issue roofline of `kernel`: its SQ_INSTS_VALU per launch (committed profile of the
-    same workload) over this run's average launch time, against PEAK_VALU_WAVE_INSTS."""
+    same workload; `per` = "chunk" when both figures are summed over a streamed chunk's launches)
+    over this run's average time for the same unit, against PEAK_VALU_WAVE_INSTS."""
     rate = valu / (avg_ms * 1e-3) if valu and avg_ms > 0 else None
     return {"kernel": kernel, "bound": "valu", "achieved": rate, "peak": PEAK_VALU_WAVE_INSTS,
             "unit": "wave-instructions/s", "frac": rate / PEAK_VALU_WAVE_INSTS if rate else None,
-            "valu_wave_insts_per_launch": valu, "avg_launch_ms": avg_ms, "valu_source": src}
+            f"valu_wave_insts_per_{per}": valu, ("avg_launch_ms" if per == "launch" else f"ms_per_{per}"): avg_ms,
+            "valu_source": src}
 
 
 def _calib_copy(ctx, mb: int):
@@ -108,15 +121,15 @@ def _calib_copy(ctx, mb: int):
     log(f"calibration copy of {mb} MiB done")
 
 
-def _layer_kernel_name(L: int, lr: bool) -> str:
+def _layer_kernel_name(L: int, lr: bool, last: bool = False) -> str:
     """The profiled name of the beam layer kernel that runs layer L with a full codebook in the
     best-first pass (the dispatch of LaunchL in k_beam.hip): the survivor-queue kernel for layers
-    1..8, then the staged kernel, for the full-precomp and the large-root beam alike."""
+    1..8, then the staged kernel, for the full-precomp and the large-root beam alike; the
+    full-precomp beam's last queue layer runs the queue kernel built without the write-back."""
     if L <= 8:
-        kind = "LayerKernel"
-    else:
-        kind = "LayerKernelStaged"
-    return f"{kind}<{L}, {'true' if lr else 'false'}, true, true>"
+        tail = ", true" if last and not lr else ""
+        return f"LayerKernel<{L}, {'true' if lr else 'false'}, true, true{tail}>"
+    return f"LayerKernelStaged<{L}, {'true' if lr else 'false'}, true, true>"
 
 
 def _cpu_model() -> str:
@@ -226,7 +239,7 @@ def main():
     }
 
     # the timed layer kernel: full codebook, best-first pass (the default beam order)
-    prof_kernel = _layer_kernel_name(last, lr=False)
+    prof_kernel = _layer_kernel_name(last, lr=False, last=True)
     stem = f"{args.config.lower()}_encode"
     traffic, traffic_src = _profiled_traffic(prof_kernel, stem)
     valu, salu, valu_src = _profiled_valu(prof_kernel, stem)
@@ -427,6 +440,12 @@ def bench_stream_large_root(args, w):
     prof_kernel = _layer_kernel_name(last, lr=True)
     traffic, traffic_src = _profiled_traffic(prof_kernel, "c5_stream")
     valu, _, valu_src = _profiled_valu(prof_kernel, "c5_stream")
+    # A chunk's layer runs as one launch per workspace tile, and the counter runs used smaller
+    # chunks: scale the profiled per-launch figures by vectors (one wave per vector) to a chunk.
+    pw = _profiled_waves(prof_kernel, "c5_stream")
+    per_chunk = chunk / pw if pw else None
+    traffic = traffic * per_chunk if traffic and per_chunk else None
+    valu = valu * per_chunk if valu and per_chunk else None
     out = {
         "metric": "vectors encoded/sec (stream, d=128 uint8, forced nearest root h0=65536 + 16x256, B=32)",
         "value": n / wall,
@@ -454,10 +473,11 @@ def bench_stream_large_root(args, w):
             "frac": beam_ach / PEAK_HBM_GBS,
             "traffic": traffic,
             "traffic_source": traffic_src,
-            "algorithmic_bytes_per_launch": sel_bytes,
-            "avg_launch_ms": avg_last_ms,
+            # per chunk: the sum over the chunk's tile launches (bytes, counters and time alike)
+            "algorithmic_bytes_per_chunk": sel_bytes,
+            "ms_per_chunk": avg_last_ms,
         },
-        "roofline_valu": _roofline_valu(prof_kernel, valu, avg_last_ms, valu_src),
+        "roofline_valu": _roofline_valu(prof_kernel, valu, avg_last_ms, valu_src, per="chunk"),
         # The distance stage: the nearest-root GEMM over the 65,536 roots (2*d*h0 flops per vector,
         # first-minimum epilogue) and the xC GEMM over the 16 x 256 small codewords (2*d*Hs), both
         # fp32 MFMA, timed together by HIP events with the NaN fix-up and the root-dot gather.
