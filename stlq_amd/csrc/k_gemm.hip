@@ -173,6 +173,114 @@ __global__ __launch_bounds__(256) void GemmXcKernel(const float* __restrict__ X,
     }
 }
 
+// The nearest-root epilogue of one 128 x 128 score tile: for each of the lane's 16 rows, the
+// running first strict minimum of e1 over this tile's columns (ascending code order within a lane;
+// the cross-lane order is restored by the final reduction), NaN errors flagged in nanm.
+__device__ __forceinline__ void RootTileEpilogue(const floatx4 (&acc)[4][4], const float (&alpha_c)[4], int64_t hb,
+                                                 int wn, int r16, const float (&xn)[4][4], float (&be)[4][4],
+                                                 uint32_t (&bc)[4][4], uint32_t& nanm) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const int col = static_cast<int>(hb) + wn * 64 + c * 16 + r16;
+        const float alpha = alpha_c[c];
+        if (alpha == 0.0f) continue;  // beam_search.cpp: alpha == 0 roots are skipped
+        // a1 = RN(gam / alpha) without a division per element: gam/alpha = (gam*sc)/(alpha*sc)
+        // with sc a power of two and alpha*sc = ap in [1, 2), so q0 = sp*yp,
+        // q = fma(-fma(ap, q0, -sp), yp, q0) with yp = RN(1/ap) is the correctly rounded
+        // quotient whenever sp = gam*sc is exact and |sp| lies in [2^-100, 2^100] (the identity
+        // tests/division_check.c verifies, as for the beam's quotients). Any lane outside that
+        // range sends the column back to IEEE division.
+        int ex;
+        const float mant = frexpf(alpha, &ex);
+        const bool colfast = alpha >= 0x1p-60f && alpha <= 0x1p60f;
+        const float ap = 2.0f * mant;
+        const float sc = colfast ? ldexpf(1.0f, 1 - ex) : 0.0f;  // 0: always the IEEE path
+        const float yp = 1.0f / ap;
+        float a1v[4][4];
+        float lo = __builtin_huge_valf(), hi = 0.0f;
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float sp = acc[a][c][r] * sc;
+                const float q0 = sp * yp;
+                const float rr = __builtin_fmaf(ap, q0, -sp);
+                a1v[a][r] = __builtin_fmaf(-rr, yp, q0);
+                lo = __builtin_fminf(lo, __builtin_fabsf(sp));
+                hi = __builtin_fmaxf(hi, __builtin_fabsf(sp));
+            }
+        if (__builtin_amdgcn_ballot_w64(!(lo >= 0x1p-100f && hi <= 0x1p100f)) != 0ull) {
+#pragma unroll
+            for (int a = 0; a < 4; ++a)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) a1v[a][r] = acc[a][c][r] / alpha;
+        }
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float gam = acc[a][c][r];
+                const float a1 = a1v[a][r];
+                const float e1 = xn[a][r] - gam * a1;
+                if (__builtin_isnan(e1)) nanm |= 1u << (4 * a + r);
+                if (e1 < be[a][r]) {
+                    be[a][r] = e1;
+                    bc[a][r] = static_cast<uint32_t>(col);
+                }
+            }
+    }
+}
+
+// The block's answer from the per-lane running minima: first minimum over the 16 lanes that
+// share the lane's rows (codes differ, so ties go to the lower code), then over the two column
+// waves through LDS; rows of the block at or past `nrows` are not written.
+__device__ __forceinline__ void RootFinish(const float (&be)[4][4], const uint32_t (&bc)[4][4], uint32_t nanm,
+                                           int64_t i0, int64_t nrows, float (*red_e)[kBM], uint32_t (*red_c)[kBM],
+                                           uint32_t (*red_f)[kBM], uint32_t* __restrict__ root_out,
+                                           uint8_t* __restrict__ flag) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int g = lane >> 4, r16 = lane & 15;
+    // first minimum over the 16 lanes that share these rows (codes differ, so ties go to the
+    // lower code), then over the two column waves through LDS
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            float e = be[a][r];
+            uint32_t cd = bc[a][r];
+            uint32_t f = (nanm >> (4 * a + r)) & 1u;
+#pragma unroll
+            for (int sh = 1; sh < 16; sh <<= 1) {
+                const float e2 = __shfl_xor(e, sh, 16);
+                const uint32_t c2 = __shfl_xor(cd, sh, 16);
+                f |= __shfl_xor(f, sh, 16);
+                if (e2 < e || (e2 == e && c2 < cd)) {
+                    e = e2;
+                    cd = c2;
+                }
+            }
+            if (r16 == 0) {
+                const int lr = wm * 64 + a * 16 + 4 * g + r;
+                red_e[wn][lr] = e;
+                red_c[wn][lr] = cd;
+                red_f[wn][lr] = f;
+            }
+        }
+    __syncthreads();
+    const int t = threadIdx.x;
+    if (t < kBM && i0 + t < nrows) {
+        float e = red_e[0][t];
+        uint32_t cd = red_c[0][t];
+        const float e2 = red_e[1][t];
+        const uint32_t c2 = red_c[1][t];
+        if (e2 < e || (e2 == e && c2 < cd)) cd = c2;
+        root_out[i0 + t] = cd;
+        flag[i0 + t] = static_cast<uint8_t>(red_f[0][t] | red_f[1][t]);
+    }
+}
+
 // Nearest root of the large-root beam (beam_search.cpp:639-709 with one root slot, the forced
 // nearest root): per vector, the first root code in ascending order with the smallest
 // e1 = ||x||^2 - g*(g/alpha), g = <x, C0[:,code]>, alpha = ||C0[:,code]||^2 != 0, where a later
@@ -183,8 +291,10 @@ __global__ __launch_bounds__(256) void GemmXcKernel(const float* __restrict__ X,
 // A NaN e1 has no such reduction (the reference lets it in and then accepts the next candidate
 // whatever it is), so a vector that meets one is flagged for NearestRootFixupKernel.
 // root_out: code or kNoRoot; flag: 1 where a NaN was met.
+// Two waves per SIMD asked of the register allocator: the accumulators, the per-row minima and
+// the epilogue take about 250 registers, and left alone the allocator can land just above 256.
 template <bool kInteriorRows>
-__global__ __launch_bounds__(256) void NearestRootKernel(const float* __restrict__ X, int64_t n, int d,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) void NearestRootKernel(const float* __restrict__ X, int64_t n, int d,
                                                          const float* __restrict__ C0, int h0,
                                                          const float* __restrict__ norm0,
                                                          const float* __restrict__ nx2, uint32_t* __restrict__ root_out,
@@ -231,94 +341,95 @@ __global__ __launch_bounds__(256) void NearestRootKernel(const float* __restrict
         } else {
             GemmAcc<false>(X, n, d, C0, h0, i0, hb, As, Bs, acc);
         }
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const int col = static_cast<int>(hb) + wn * 64 + c * 16 + r16;
-            const float alpha = alpha_c[c];
-            if (alpha == 0.0f) continue;  // beam_search.cpp: alpha == 0 roots are skipped
-            // a1 = RN(gam / alpha) without a division per element: gam/alpha = (gam*sc)/(alpha*sc)
-            // with sc a power of two and alpha*sc = ap in [1, 2), so q0 = sp*yp,
-            // q = fma(-fma(ap, q0, -sp), yp, q0) with yp = RN(1/ap) is the correctly rounded
-            // quotient whenever sp = gam*sc is exact and |sp| lies in [2^-100, 2^100] (the identity
-            // tests/division_check.c verifies, as for the beam's quotients). Any lane outside that
-            // range sends the column back to IEEE division.
-            int ex;
-            const float mant = frexpf(alpha, &ex);
-            const bool colfast = alpha >= 0x1p-60f && alpha <= 0x1p60f;
-            const float ap = 2.0f * mant;
-            const float sc = colfast ? ldexpf(1.0f, 1 - ex) : 0.0f;  // 0: always the IEEE path
-            const float yp = 1.0f / ap;
-            float a1v[4][4];
-            float lo = __builtin_huge_valf(), hi = 0.0f;
-#pragma unroll
-            for (int a = 0; a < 4; ++a)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const float sp = acc[a][c][r] * sc;
-                    const float q0 = sp * yp;
-                    const float rr = __builtin_fmaf(ap, q0, -sp);
-                    a1v[a][r] = __builtin_fmaf(-rr, yp, q0);
-                    lo = __builtin_fminf(lo, __builtin_fabsf(sp));
-                    hi = __builtin_fmaxf(hi, __builtin_fabsf(sp));
-                }
-            if (__builtin_amdgcn_ballot_w64(!(lo >= 0x1p-100f && hi <= 0x1p100f)) != 0ull) {
-#pragma unroll
-                for (int a = 0; a < 4; ++a)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) a1v[a][r] = acc[a][c][r] / alpha;
-            }
-#pragma unroll
-            for (int a = 0; a < 4; ++a)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const float gam = acc[a][c][r];
-                    const float a1 = a1v[a][r];
-                    const float e1 = xn[a][r] - gam * a1;
-                    if (__builtin_isnan(e1)) nanm |= 1u << (4 * a + r);
-                    if (e1 < be[a][r]) {
-                        be[a][r] = e1;
-                        bc[a][r] = static_cast<uint32_t>(col);
-                    }
-                }
-        }
+        RootTileEpilogue(acc, alpha_c, hb, wn, r16, xn, be, bc, nanm);
     }
-    // first minimum over the 16 lanes that share these rows (codes differ, so ties go to the
-    // lower code), then over the two column waves through LDS
+    RootFinish(be, bc, nanm, i0, n, red_e, red_c, red_f, root_out, flag);
+}
+
+// NearestRootKernel for the all-interior case (every row and root tile full, d a multiple of 16,
+// 16-byte aligned operands: the C5 shape), with the k-loop run across the root tiles as one
+// pipeline: the last slice of a root tile prefetches the next tile's first slice, so a tile starts
+// from data already in LDS instead of waiting on its first global loads behind a barrier. The MFMA
+// order over k, and so every score's bits, the epilogue and the reduction are NearestRootKernel's.
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) void NearestRootFlatKernel(const float* __restrict__ X, int64_t n, int d,
+                                                             const float* __restrict__ C0, int h0,
+                                                             const float* __restrict__ norm0,
+                                                             const float* __restrict__ nx2,
+                                                             uint32_t* __restrict__ root_out,
+                                                             uint8_t* __restrict__ flag) {
+    __shared__ float As[2][kBM][kLdsStride];
+    __shared__ float Bs[2][kBN][kLdsStride];
+    __shared__ float red_e[2][kBM];
+    __shared__ uint32_t red_c[2][kBM];
+    __shared__ uint32_t red_f[2][kBM];
+    const int64_t i0 = static_cast<int64_t>(blockIdx.x) * kBM;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int g = lane >> 4, r16 = lane & 15;
+
+    float be[4][4], xn[4][4];
+    uint32_t bc[4][4];
+    uint32_t nanm = 0;  // bit 4a+r: a NaN e1 met on that row
 #pragma unroll
     for (int a = 0; a < 4; ++a)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            float e = be[a][r];
-            uint32_t cd = bc[a][r];
-            uint32_t f = (nanm >> (4 * a + r)) & 1u;
-#pragma unroll
-            for (int sh = 1; sh < 16; sh <<= 1) {
-                const float e2 = __shfl_xor(e, sh, 16);
-                const uint32_t c2 = __shfl_xor(cd, sh, 16);
-                f |= __shfl_xor(f, sh, 16);
-                if (e2 < e || (e2 == e && c2 < cd)) {
-                    e = e2;
-                    cd = c2;
-                }
-            }
-            if (r16 == 0) {
-                const int lr = wm * 64 + a * 16 + 4 * g + r;
-                red_e[wn][lr] = e;
-                red_c[wn][lr] = cd;
-                red_f[wn][lr] = f;
-            }
+            be[a][r] = __builtin_huge_valf();
+            bc[a][r] = kNoRoot;
+            xn[a][r] = nx2[i0 + wm * 64 + a * 16 + 4 * g + r];
         }
+    const int tiles = h0 / kBN;
+    const int nk = d / kBK;
+    Staged sa, sb;
+    LoadSlice<true>(X, n, d, i0, 0, true, sa);
+    LoadSlice<true>(C0, h0, d, 0, 0, true, sb);
+    StoreSlice(As[0], sa);
+    StoreSlice(Bs[0], sb);
     __syncthreads();
-    const int t = threadIdx.x;
-    if (t < kBM && (kInteriorRows || i0 + t < n)) {
-        float e = red_e[0][t];
-        uint32_t cd = red_c[0][t];
-        const float e2 = red_e[1][t];
-        const uint32_t c2 = red_c[1][t];
-        if (e2 < e || (e2 == e && c2 < cd)) cd = c2;
-        root_out[i0 + t] = cd;
-        flag[i0 + t] = static_cast<uint8_t>(red_f[0][t] | red_f[1][t]);
+    int cur = 0;
+    for (int th = 0; th < tiles; ++th) {
+        const int64_t hb = static_cast<int64_t>(th) * kBN;
+        float alpha_c[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) alpha_c[c] = norm0[static_cast<int>(hb) + wn * 64 + c * 16 + r16];
+        floatx4 acc[4][4];
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) acc[a][c] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int kt = 0; kt < nk; ++kt) {
+            // the next slice: this tile's, or the next tile's first (none after the last)
+            const bool last_k = kt + 1 == nk;
+            const bool more = !last_k || th + 1 < tiles;
+            if (more) {
+                LoadSlice<true>(X, n, d, i0, last_k ? 0 : (kt + 1) * kBK, true, sa);
+                LoadSlice<true>(C0, h0, d, last_k ? hb + kBN : hb, last_k ? 0 : (kt + 1) * kBK, true, sb);
+            }
+            floatx4 af[4], bf[4];
+#pragma unroll
+            for (int a = 0; a < 4; ++a)
+                af[a] = *reinterpret_cast<const floatx4*>(&As[cur][wm * 64 + a * 16 + r16][4 * g]);
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                bf[c] = *reinterpret_cast<const floatx4*>(&Bs[cur][wn * 64 + c * 16 + r16][4 * g]);
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+#pragma unroll
+                for (int a = 0; a < 4; ++a)
+#pragma unroll
+                    for (int c = 0; c < 4; ++c)
+                        acc[a][c] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[a][s], bf[c][s], acc[a][c], 0, 0, 0);
+            if (more) {
+                StoreSlice(As[cur ^ 1], sa);
+                StoreSlice(Bs[cur ^ 1], sb);
+            }
+            __syncthreads();
+            cur ^= 1;
+        }
+        RootTileEpilogue(acc, alpha_c, hb, wn, r16, xn, be, bc, nanm);
     }
+    RootFinish(be, bc, nanm, i0, n, red_e, red_c, red_f, root_out, flag);
 }
 
 }  // namespace
@@ -327,7 +438,12 @@ hipError_t LaunchNearestRoot(const float* X, int64_t n, int d, const float* C0, 
                              const float* nx2, uint32_t* root_out, uint8_t* flag, hipStream_t s) {
     if (n <= 0 || h0 <= 0) return hipSuccess;
     const int64_t full = n / kBM;
-    if (full > 0)
+    const bool flat = (h0 % kBN) == 0 && (d % kBK) == 0 &&
+                      ((reinterpret_cast<uintptr_t>(X) | reinterpret_cast<uintptr_t>(C0)) & 15u) == 0;
+    if (full > 0 && flat)
+        hipLaunchKernelGGL(NearestRootFlatKernel, dim3(static_cast<unsigned>(full)), dim3(256), 0, s, X, n, d, C0, h0,
+                           norm0, nx2, root_out, flag);
+    else if (full > 0)
         hipLaunchKernelGGL(NearestRootKernel<true>, dim3(static_cast<unsigned>(full)), dim3(256), 0, s, X, n, d, C0,
                            h0, norm0, nx2, root_out, flag);
     if (full * kBM < n) {
