@@ -125,11 +125,10 @@ def _layer_kernel_name(L: int, lr: bool, last: bool = False) -> str:
     """The profiled name of the beam layer kernel that runs layer L with a full codebook in the
     best-first pass (the dispatch of LaunchL in k_beam.hip): the survivor-queue kernel for layers
     1..8, then the staged kernel, for the full-precomp and the large-root beam alike; the
-    full-precomp beam's last queue layer runs the queue kernel built without the write-back."""
-    if L <= 8:
-        tail = ", true" if last and not lr else ""
-        return f"LayerKernel<{L}, {'true' if lr else 'false'}, true, true{tail}>"
-    return f"LayerKernelStaged<{L}, {'true' if lr else 'false'}, true, true>"
+    last layer runs the kernel built for the final pick only (template flag LAST)."""
+    tail = ", true" if last else ""
+    kind = "LayerKernel" if L <= 8 else "LayerKernelStaged"
+    return f"{kind}<{L}, {'true' if lr else 'false'}, true, true{tail}>"
 
 
 def _cpu_model() -> str:
@@ -437,7 +436,7 @@ def bench_stream_large_root(args, w):
     h2d_gbs = st.h2d_bytes / (st.h2d_ms * 1e-3) / 1e9 if st.h2d_ms > 0 else None
     dist_flops = 2.0 * w.d * (h0 + (M - 1) * w.K) * (n / nch)
     dist_ach = dist_flops / (t.gemm_ms / nch * 1e-3) / 1e12 if t.gemm_ms > 0 else None
-    prof_kernel = _layer_kernel_name(last, lr=True)
+    prof_kernel = _layer_kernel_name(last, lr=True, last=True)
     traffic, traffic_src = _profiled_traffic(prof_kernel, "c5_stream")
     valu, _, valu_src = _profiled_valu(prof_kernel, "c5_stream")
     # A chunk's layer runs as one launch per workspace tile, and the counter runs used smaller

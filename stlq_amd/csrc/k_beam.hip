@@ -725,6 +725,66 @@ __global__ __launch_bounds__(256) void Layer0Kernel(LayerArgs p) {
     }
 }
 
+// Last layer of the best-first pass (LayerKernel and LayerKernelStaged built with LAST): only the
+// final pick leaves the layer, the first minimum over the top-H slots (beam_search.cpp:409-419).
+// When the smallest eligible error is unique and finite, that candidate enters whenever it is
+// scanned (every slot then holds a larger error) and is never evicted (it is never the worst), so
+// it is the pick in any scan order. So the scan only tracks the running minimum, and the pruning
+// bound tests against it: a pruned candidate's error exceeds the minimum of its moment, so it can
+// neither be the pick nor tie with it. Everything else is flagged and re-run in the reference
+// order: a tie for the minimum, an eligible NaN or -0, or no finite candidate (the all-skipped
+// fallback).
+struct LastPick {
+    uint32_t best_img = 0x7F800000u;  // the minimum's float bits (+inf: nothing yet)
+    int best_cand = -1;
+    bool tie = false;
+    // One group of candidates in scan order (lane = scan position); false: flag the vector.
+    __device__ bool Take(bool ok, float e, int cand) {
+        const uint32_t img = __float_as_uint(e);
+        // errors are clamped at +0 here, so NaN and -0 are the images above +inf's
+        if (Ballot(ok && img > 0x7F800000u) != 0ull) return false;
+        const uint32_t mine = ok ? img : 0xFFFFFFFFu;
+        const uint32_t mn = WaveMinU32(mine);
+        if (mn >= 0x7F800000u) return true;  // no finite error in this group
+        const uint64_t at = Ballot(mine == mn);
+        if (mn < best_img) {
+            best_img = mn;
+            best_cand = __builtin_amdgcn_readlane(cand, static_cast<int>(__builtin_ctzll(at)));
+            tie = __popcll(at) > 1;
+        } else if (mn == best_img) {
+            tie = true;
+        }
+        return true;
+    }
+    __device__ float Now() const { return __uint_as_float(best_img); }
+};
+
+// The pick's codes (and the large root's cluster id) and error, or the vector's re-run flag.
+template <int L, bool LR>
+__device__ __forceinline__ void WriteLastPick(bool fine, const LastPick& lp, const LayerArgs& p, const Rec& rc,
+                                              const float* recs_in, int K, int64_t i, int lane) {
+    if (lane != 0) return;
+    if (!fine || lp.tie || lp.best_cand < 0) {
+        p.flags[i] = 1;
+        return;
+    }
+    const int m = p.m;
+    const int src = lp.best_cand / K;
+    const int knew = lp.best_cand - src * K;
+    const float* ri = recs_in + src * rc.stride;
+    if (LR) {
+        p.cluster_out[i] = reinterpret_cast<const uint32_t*>(ri)[rc.root];
+#pragma unroll
+        for (int t = 1; t < L; ++t) p.codes_out[i * (m - 1) + (t - 1)] = CodeAt(ri, rc.code, t);
+        p.codes_out[i * (m - 1) + (L - 1)] = static_cast<uint8_t>(knew);
+    } else {
+#pragma unroll
+        for (int t = 0; t < L; ++t) p.codes_out[i * m + t] = CodeAt(ri, rc.code, t);
+        p.codes_out[i * m + L] = static_cast<uint8_t>(knew);
+    }
+    if (p.best_err) p.best_err[i] = __uint_as_float(lp.best_img);
+}
+
 // Layers L >= 1. LR selects the large-root cross-term source and reciprocal solves.
 // FULL: the layer has exactly 256 codewords (no partial chunk).
 // Minimum waves per SIMD asked of the register allocator by the queue kernel (layers 1-8),
@@ -757,8 +817,9 @@ constexpr int kQueueCap = 128;  // ring capacity: at most 63 carried over plus o
 
 // BEST: the best-first pass (LayerArgs::flags). Its input records are rank-indexed, so slots are
 // scanned in ascending error order, and so are its output records. A vector flagged by an earlier
-// layer arrives with an empty beam. LAST: built for the last layer only (p.is_last), without the
-// write-back's code and registers (the M=8, beam-16 encode's last layer ran 3% faster).
+// layer arrives with an empty beam. LAST: built for the last layer of the best-first pass only
+// (p.is_last): the running minimum of LastPick instead of the top-H, and no write-back (on the M=8,
+// beam-16 encode the last layer took 9.35 against 11.38 ms).
 template <int L, bool LR, bool FULL, bool BEST, bool LAST = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LayerMinWaves<L, LR, BEST, LAST>(), 8))) void LayerKernel(
     LayerArgs p) {
@@ -1150,6 +1211,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LayerMinWav
         if (qlen > 0 && !flush(qlen)) return false;
         return true;
     };
+
+    if constexpr (LAST && BEST) {
+        if (prune_on) {  // the final pick only (LastPick)
+            LastPick lp;
+            auto track = [&](bool ok, float e, int cand) { return lp.Take(ok, e, cand); };
+            auto min_now = [&]() { return lp.Now(); };
+            const bool fine = scan_queue(track, min_now);
+            WriteLastPick<L, LR>(fine, lp, p, rc, recs_in, K, i, lane);
+            return;
+        }
+    }
 
     float s_err;
     int s_cand;
@@ -1556,7 +1628,8 @@ constexpr int StagedMinWaves() {
     return L <= 14 ? 4 : 3;
 }
 
-template <int L, bool LR, bool FULL, bool BEST>
+// LAST: built for the last layer of the best-first pass only (LastPick), as LayerKernel's.
+template <int L, bool LR, bool FULL, bool BEST, bool LAST = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(StagedMinWaves<L>(), 8))) void LayerKernelStaged(
     LayerArgs p) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1953,6 +2026,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(StagedMinWa
         return true;
     };
 
+    if constexpr (LAST && BEST) {
+        if (prune_on) {  // the final pick only (LastPick)
+            LastPick lp;
+            auto track = [&](bool ok, float e, int cand) { return lp.Take(ok, e, cand); };
+            auto min_now = [&]() { return lp.Now(); };
+            const bool fine = scan_windows(track, min_now);
+            WriteLastPick<L, LR>(fine, lp, p, rc, recs_in, K, i, lane);
+            return;
+        }
+    }
+
     float s_err;
     int s_cand;
     bool flagged = false;
@@ -2164,11 +2248,13 @@ hipError_t LaunchWith(bool lr, const LayerArgs& a, hipStream_t s) {
     const unsigned lds = static_cast<unsigned>(KernelSel<L, false, true, false>::DynamicLds(a.Hb));
     if (lr) {  // the large-root beam's best-first pass is built for full layers (K = 256) only
         if (a.flags && !full) return hipErrorInvalidValue;
-        if (a.flags) hipLaunchKernelGGL((KernelSel<L, true, true, true>::kernel), dim3(blocks), block, lds, s, a);
+        if (a.flags && a.is_last)
+            hipLaunchKernelGGL((KernelSel<L, true, true, true>::kernel_last), dim3(blocks), block, lds, s, a);
+        else if (a.flags) hipLaunchKernelGGL((KernelSel<L, true, true, true>::kernel), dim3(blocks), block, lds, s, a);
         else if (full) hipLaunchKernelGGL((KernelSel<L, true, true, false>::kernel), dim3(blocks), block, lds, s, a);
         else hipLaunchKernelGGL((KernelSel<L, true, false, false>::kernel), dim3(blocks), block, lds, s, a);
     } else if (a.flags) {
-        // the last layer of the best-first pass over full layers (the M=8 headline encode's)
+        // the last layer of the best-first pass over full layers: the final pick only
         if (full && a.is_last)
             hipLaunchKernelGGL((KernelSel<L, false, true, true>::kernel_last), dim3(blocks), block, lds, s, a);
         else if (full) hipLaunchKernelGGL((KernelSel<L, false, true, true>::kernel), dim3(blocks), block, lds, s, a);
@@ -2190,7 +2276,7 @@ struct QueueSel {
 template <int L, bool LR, bool FULL, bool BEST>
 struct StagedSel {
     static constexpr auto kernel = LayerKernelStaged<L, LR, FULL, BEST>;
-    static constexpr auto kernel_last = kernel;
+    static constexpr auto kernel_last = LayerKernelStaged<L, LR, FULL, BEST, true>;
     static constexpr size_t DynamicLds(int) { return 0; }
 };
 
