@@ -13,6 +13,7 @@
 // and runs the beam again skipping the pruned candidates: codes and best errors must be identical.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 #include <cstring>
@@ -42,6 +43,11 @@ struct Slot {
 
 struct Stats {
     int64_t candidates = 0, tested = 0, pruned = 0, violations = 0, self_kept_fail = 0, mismatches = 0;
+    // the last layer's minimum rule (LastPick in k_beam.hip): vectors it decides, vectors it would
+    // flag for a re-run, decided vectors whose pick differs from the reference's, and the last
+    // layer's candidates and how many of them the bound against the running minimum prunes
+    int64_t lp_decided = 0, lp_flagged = 0, lp_mismatches = 0, lp_candidates = 0, lp_pruned = 0;
+    int64_t last_pruned_worst = 0;  // the last layer's candidates the top-H bound prunes
 };
 
 // One candidate with the reference's arithmetic (beam_search.cpp:286-318).
@@ -135,6 +141,9 @@ int prune_check(const float* G, const float* xC, const float* nx2, int H, int m,
         const float* xc = xC + i * H;
         std::vector<int> codes_run[2];
         float err_run[2] = {kInf, kInf};
+        std::vector<Slot> last_parents;  // the last layer's parent slots (pass 0)
+        std::vector<float> last_e;       // their candidates' errors, parent-major
+        std::vector<uint8_t> last_elig;
         for (int pass = 0; pass < 2; ++pass) {  // pass 1 skips the pruned candidates
             std::vector<Slot> cur;
             {  // layer 0 (beam_search.cpp:240-263), reference slot order
@@ -167,6 +176,11 @@ int prune_check(const float* G, const float* xC, const float* nx2, int H, int m,
                 }
             }
             for (int L = 1; L < m && !cur.empty(); ++L) {
+                if (pass == 0 && L == m - 1) {
+                    last_parents = cur;
+                    last_e.assign(cur.size() * static_cast<size_t>(h_vec[L]), kInf);
+                    last_elig.assign(cur.size() * static_cast<size_t>(h_vec[L]), 0);
+                }
                 struct Pick {
                     int h = -1, k = 0;
                     float denom = 0, a_last = 0;
@@ -186,6 +200,11 @@ int prune_check(const float* G, const float* xC, const float* nx2, int H, int m,
                         const bool elig = EvalRef(s, L, m, A.data(), gd[fk], xc[fk], y.data(), v.data(), ec, dn, al);
                         const bool pruned = DeviceTest(s, L, m, Gs.data(), sw.data(), isw.data(), off.data(), H, fk,
                                                        gd[fk], xc[fk], W0);
+                        if (pass == 0 && L == m - 1) {
+                            last_e[static_cast<size_t>(h) * h_vec[L] + k] = ec;
+                            last_elig[static_cast<size_t>(h) * h_vec[L] + k] = elig ? 1 : 0;
+                            if (pruned) ++st.last_pruned_worst;
+                        }
                         if (pass == 0) {
                             ++st.candidates;
                             if (s.bd.kb < kInf && W0 < kInf) ++st.tested;
@@ -284,6 +303,51 @@ int prune_check(const float* G, const float* xC, const float* nx2, int H, int m,
         if (codes_run[0] != codes_run[1] ||
             std::memcmp(&err_run[0], &err_run[1], sizeof(float)) != 0)
             ++st.mismatches;
+        if (m >= 2 && !last_parents.empty()) {
+            // The minimum rule: parents in ascending error order (the best-first pass's), each
+            // candidate bound-tested against the running minimum at its parent's start; flagged
+            // on a tie for the minimum, an eligible NaN or -0, or no finite candidate.
+            const int L = m - 1, K = h_vec[L];
+            std::vector<int> ord(last_parents.size());
+            for (size_t q = 0; q < ord.size(); ++q) ord[q] = static_cast<int>(q);
+            std::stable_sort(ord.begin(), ord.end(),
+                             [&](int a, int b) { return last_parents[a].err < last_parents[b].err; });
+            float best = kInf;
+            int bh = -1, bk = 0;
+            bool tie = false, bad = false;
+            for (int h : ord) {
+                const Slot& s = last_parents[h];
+                const float W0 = best;
+                for (int k = 0; k < K; ++k) {
+                    const int fk = off[L] + k;
+                    ++st.lp_candidates;
+                    if (DeviceTest(s, L, m, Gs.data(), sw.data(), isw.data(), off.data(), H, fk, gd[fk], xc[fk], W0)) {
+                        ++st.lp_pruned;
+                        continue;
+                    }
+                    if (!last_elig[static_cast<size_t>(h) * K + k]) continue;
+                    const float ec = last_e[static_cast<size_t>(h) * K + k];
+                    if (std::isnan(ec) || (ec == 0.0f && std::signbit(ec))) bad = true;
+                    if (!(ec < kInf)) continue;
+                    if (ec < best) {
+                        best = ec;
+                        bh = h;
+                        bk = k;
+                        tie = false;
+                    } else if (ec == best) {
+                        tie = true;
+                    }
+                }
+            }
+            if (bad || tie || bh < 0) {
+                ++st.lp_flagged;
+            } else {
+                ++st.lp_decided;
+                std::vector<int> codes = last_parents[bh].code;
+                codes.push_back(bk);
+                if (codes != codes_run[0] || std::memcmp(&best, &err_run[0], sizeof(float)) != 0) ++st.lp_mismatches;
+            }
+        }
     }
     stats[0] = st.candidates;
     stats[1] = st.tested;
@@ -291,6 +355,12 @@ int prune_check(const float* G, const float* xC, const float* nx2, int H, int m,
     stats[3] = st.violations;
     stats[4] = st.self_kept_fail;
     stats[5] = st.mismatches;
+    stats[6] = st.lp_decided;
+    stats[7] = st.lp_flagged;
+    stats[8] = st.lp_mismatches;
+    stats[9] = st.lp_candidates;
+    stats[10] = st.lp_pruned;
+    stats[11] = st.last_pruned_worst;
     return 0;
 }
 

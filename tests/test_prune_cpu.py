@@ -6,7 +6,10 @@ and requires
   * no pruned candidate the reference would have inserted,
   * every candidate kept when the threshold is its own error (a strict lower bound),
   * the beam that skips the pruned candidates equal to the full beam, codes and errors bit for bit,
-  * on the benchmark samples, most candidates pruned (the bound is tight enough to matter)."""
+  * on the benchmark samples, most candidates pruned (the bound is tight enough to matter),
+  * the last layer's minimum rule (LastPick in k_beam.hip: parents in ascending error order, each
+    candidate bound-tested against the running minimum, only the minimum kept) picking the
+    reference's codes and error bit for bit on every vector it does not flag for a re-run."""
 import ctypes
 import os
 import subprocess
@@ -39,13 +42,18 @@ def _run(checker, orc, X, C, h, Hb):
     xC = np.ascontiguousarray(orc.gemm_xc(C, X))
     nx2 = np.ascontiguousarray(orc.xnorm2(X))
     hv = (ctypes.c_int * len(h))(*h)
-    st = (ctypes.c_int64 * 6)()
+    st = (ctypes.c_int64 * 12)()
     f32p = ctypes.POINTER(ctypes.c_float)
     G = np.ascontiguousarray(G)
     assert checker.prune_check(G.ctypes.data_as(f32p), xC.ctypes.data_as(f32p), nx2.ctypes.data_as(f32p),
                                int(sum(h)), len(h), hv, X.shape[0], Hb, st) == 0
-    keys = ["candidates", "tested", "pruned", "violations", "self_kept_fail", "mismatches"]
-    return dict(zip(keys, list(st)))
+    keys = ["candidates", "tested", "pruned", "violations", "self_kept_fail", "mismatches", "lp_decided",
+            "lp_flagged", "lp_mismatches", "lp_candidates", "lp_pruned", "last_pruned_worst"]
+    rep = dict(zip(keys, list(st)))
+    # the minimum rule decides or flags every vector, and never disagrees with the reference
+    assert rep["lp_decided"] + rep["lp_flagged"] == X.shape[0], rep
+    assert rep["lp_mismatches"] == 0, rep
+    return rep
 
 
 @pytest.mark.parametrize("cfg,n,Hb", [("C2", 400, 16), ("C4", 60, 8), ("C3", 300, 16)])
@@ -59,6 +67,11 @@ def test_pruning_never_drops_an_entrant(checker, orc, cfg, n, Hb):
     print(cfg, rep)
     assert rep["violations"] == 0 and rep["self_kept_fail"] == 0 and rep["mismatches"] == 0, rep
     assert rep["pruned"] >= 0.75 * rep["candidates"], rep  # tight enough to matter (reference scan order)
+    # the minimum rule decides most vectors (C4's deep near-zero codewords leave ties for the
+    # minimum, which the best-first pass flags in any case) and prunes more of the last layer than
+    # the top-H bound does
+    assert rep["lp_flagged"] <= 0.2 * n, rep
+    assert rep["lp_pruned"] > rep["last_pruned_worst"], rep
 
 
 @pytest.mark.parametrize("kind", ["near_dependent", "scaled", "tiny"])
