@@ -123,7 +123,7 @@ def _calib_copy(ctx, mb: int):
 
 def _layer_kernel_name(L: int, lr: bool, last: bool = False) -> str:
     """The profiled name of the beam layer kernel that runs layer L with a full codebook in the
-    best-first pass (the dispatch of LaunchL in k_beam.hip): the survivor-queue kernel for layers
+    best-first pass (the dispatch of LaunchL in beam_kernels.hpp): the survivor-queue kernel for layers
     1..8, then the staged kernel, for the full-precomp and the large-root beam alike; the
     last layer runs the kernel built for the final pick only (template flag LAST)."""
     tail = ", true" if last else ""

@@ -23,7 +23,8 @@ LIB = os.path.join(LIBDIR, "libstlq_mi355.so")
 # test driver of the C++ host mirror (stlq_amd/host/stlq_mi355.hpp), linked against LIB
 HOSTCHECK_SRC = os.path.join(ROOT, "tests", "host_mirror_check.cpp")
 HOSTCHECK = os.path.join(LIBDIR, "libstlq_mi355_hostcheck.so")
-SOURCES = ["k_precomp.hip", "k_gemm.hip", "k_beam.hip", "k_ls.hip", "capi.hip"]
+SOURCES = ["k_precomp.hip", "k_gemm.hip", "k_beam.hip", "k_beam_queue.hip", "k_beam_staged_a.hip",
+           "k_beam_staged_b.hip", "k_ls.hip", "capi.hip"]
 HOST_SOURCES = ["base_store.cpp"]  # plain host C++ (the on-disk store), built by the host compiler
 ARCH = "gfx950"
 

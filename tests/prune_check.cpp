@@ -43,7 +43,7 @@ struct Slot {
 
 struct Stats {
     int64_t candidates = 0, tested = 0, pruned = 0, violations = 0, self_kept_fail = 0, mismatches = 0;
-    // the last layer's minimum rule (LastPick in k_beam.hip): vectors it decides, vectors it would
+    // the last layer's minimum rule (LastPick in beam_kernels.hpp): vectors it decides, vectors it would
     // flag for a re-run, decided vectors whose pick differs from the reference's, and the last
     // layer's candidates and how many of them the bound against the running minimum prunes
     int64_t lp_decided = 0, lp_flagged = 0, lp_mismatches = 0, lp_candidates = 0, lp_pruned = 0;

@@ -7,7 +7,7 @@ and requires
   * every candidate kept when the threshold is its own error (a strict lower bound),
   * the beam that skips the pruned candidates equal to the full beam, codes and errors bit for bit,
   * on the benchmark samples, most candidates pruned (the bound is tight enough to matter),
-  * the last layer's minimum rule (LastPick in k_beam.hip: parents in ascending error order, each
+  * the last layer's minimum rule (LastPick in beam_kernels.hpp: parents in ascending error order, each
     candidate bound-tested against the running minimum, only the minimum kept) picking the
     reference's codes and error bit for bit on every vector it does not flag for a re-run."""
 import ctypes
