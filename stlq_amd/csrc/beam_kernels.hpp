@@ -803,15 +803,16 @@ __device__ __forceinline__ void WriteLastPick(bool fine, const LastPick& lp, con
 // Layers L >= 1. LR selects the large-root cross-term source and reciprocal solves.
 // FULL: the layer has exactly 256 codewords (no partial chunk).
 // Minimum waves per SIMD asked of the register allocator by the queue kernel (layers 1-8),
-// measured on the M=8, K=256, beam-16 encode: layers 1-3 at 8, 4-5 at 7, 6 at 6, 7 at 5 (the
-// allocator alone gives it 101 VGPRs and 4 waves, and the last layer of that encode ran 3% slower),
-// layer 8 at the allocator's choice (4 waves). The large root: layers 1-2 at 8 (the best-first
+// measured on the M=8, K=256, beam-16 encode: layers 1-3 at 8, 4-5 at 7, 6 at 6 (7 waves ran 1%
+// slower), 7 at 5 (the allocator alone gives it 101 VGPRs and 4 waves, 3% slower); the last layer's
+// minimum-only build (LAST) of layer 7 at 6 (80 VGPRs with a small spill: 8.87 against 9.33 ms at
+// 5 waves); layer 8 at the allocator's choice (4 waves). The large root: layers 1-2 at 8 (the best-first
 // pass's sorted first group takes the SGPRs to 106, which gives 7), the others at the allocator's
 // choice (forcing 6-8 waves ran 2-9% slower on the beam-32 encode).
 template <int L, bool LR, bool BEST, bool LAST>
 constexpr int LayerMinWaves() {
     if (LR) return L <= 2 ? 8 : 1;
-    if (LAST && L == 7) return 1;
+    if (LAST && L == 7) return 6;
     return L <= 3 ? 8 : (L <= 5 ? 7 : (L == 6 ? 6 : (L == 7 ? 5 : 1)));
 }
 
