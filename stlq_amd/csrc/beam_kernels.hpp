@@ -1483,20 +1483,19 @@ constexpr int StagedWaveWords() {
 }
 
 // Waves per SIMD asked of the register allocator: the kernel needs about 5L + 60 VGPRs, so 4 waves
-// (128) hold it without spills up to layer 10 and with small ones (up to 25 VGPRs at layer 14)
-// above, 3 waves (168) without spills up to layer 18. 4 waves up to layer 14 ran layers 13-14 5-6%
-// faster than 3 on the large-root beam-32 encode and the M=16, beam-8 encode; 5 waves at layers
-// 9-10 ran 8-9% slower. The last layer's minimum-only build (LAST) holds fewer values: at 4 waves
-// up to layer 16 (with small spills) it ran 12-15% faster than at 3 (the large root's layer 16,
-// the M=16 encode's layer 15).
+// (128) hold it without spills up to layer 10 and with spills of up to 46 VGPRs above, 3 waves
+// (168) without spills up to layer 18. 4 waves up to layer 16 ran layers 13-16 5-15% faster than 3
+// on the large-root beam-32 encode and the M=16, beam-8 encode (the large root's layer 15: 84.3
+// against 92.5 ms per 1M vectors); 5 waves at layers 9-10 ran 8-9% slower. The last layer's
+// minimum-only build (LAST) takes the same setting.
 template <int L>
-constexpr int StagedMinWaves(bool last = false) {
-    return (L <= 14 || (last && L <= 16)) ? 4 : 3;
+constexpr int StagedMinWaves() {
+    return L <= 16 ? 4 : 3;
 }
 
 // LAST: built for the last layer of the best-first pass only (LastPick), as LayerKernel's.
 template <int L, bool LR, bool FULL, bool BEST, bool LAST = false>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(StagedMinWaves<L>(LAST), 8))) void LayerKernelStaged(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(StagedMinWaves<L>(), 8))) void LayerKernelStaged(
     LayerArgs p) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
